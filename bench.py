@@ -1,0 +1,189 @@
+"""MASt3R two-view inference throughput on one MI355X (pairs/s, fp32).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|2|4]
+
+A step is one full forward (ViT-L encoder on both views, ViT-B cross-attention
+decoder, two DPT heads, two local-feature heads) over one batch of synthetic
+image pairs already resident in HBM. Default workload: config 3 of the
+baseline (16 pairs at 3x384x512, U(-1,1) images, seed-0 N(0,0.02) weights).
+Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "crystal-gausplat_amd"))
+
+MFMA_FP32_PEAK_TFLOPS = 157.3
+HBM_PEAK_GBS = 8000.0
+# Algorithmic work of one 384x512 pair and of one config-0 encoder block
+# (GFLOP), from the FLOP model of the path.
+PAIR_GFLOP_384x512 = 2037.2
+BLOCK_GFLOP = 21.74
+
+CONFIGS = {
+    2: dict(pairs=1, img_h=384, img_w=512),
+    3: dict(pairs=16, img_h=384, img_w=512),
+    4: dict(pairs=32, img_h=512, img_w=512),
+}
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def cpu_baseline():
+    """Reference CPU path stand-in: the oracle with the reference's literal
+    loops (linear i-j-k, attention scores/softmax/PV), one thread, on a bounded
+    sample -- one config-0 ViT-L block (768 tokens) -- extrapolated to a
+    384x512 pair by algorithmic FLOPs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import gsplat_hip as G
+    import pyoracle as O
+
+    cfg = G.default_config(enc_depth=1, dec_depth=1)
+    w = {}
+    for i, (n, s, k) in enumerate(G.weight_inventory(cfg)):
+        if n.startswith("enc_blocks.0."):
+            w[n] = G.weight_values(cfg, i, int(np.prod(s))).reshape(s)
+    x = G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)
+    O.set_threads(1)
+    O.set_naive(True)
+    t0 = time.perf_counter()
+    O.encoder_block(cfg.as_dict(), w, "enc_blocks.0", x, 24, 32)
+    dt = time.perf_counter() - t0
+    O.set_naive(False)
+    O.set_threads(0)
+    s_per_pair = dt * PAIR_GFLOP_384x512 / BLOCK_GFLOP
+    return {
+        "value": 1.0 / s_per_pair,
+        "unit": "pairs/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": (f"one config-0 ViT-L block (768 tokens, 21.74 GFLOP) through the oracle's "
+                   f"literal reference loops, 1 thread, {dt:.2f} s; extrapolated x"
+                   f"{PAIR_GFLOP_384x512 / BLOCK_GFLOP:.1f} by FLOPs to one 384x512 pair "
+                   f"({s_per_pair:.0f} s/pair); host CPU: {cpu_model()}, "
+                   f"{os.cpu_count()} logical CPUs"),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
+    ap.add_argument("--pairs", type=int, default=0, help="override the config's pair count")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only. MASt3R pairs are independent, so "
+              "N GPUs would each run pairs/N with replicated weights and no collectives; "
+              "run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import gsplat_hip as G
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    wl = CONFIGS[args.config]
+    B = args.pairs or wl["pairs"]
+    cfg = G.default_config(img_h=wl["img_h"], img_w=wl["img_w"])
+    H, W = cfg.img_h, cfg.img_w
+
+    m = G.Mastr(cfg, B)
+    m.init_seeded(0)
+    n = B * 3 * H * W
+    img1 = torch.from_numpy(G.seed_uniform(0, "view1", n).reshape(B, 3, H, W)).cuda()
+    img2 = torch.from_numpy(G.seed_uniform(0, "view2", n).reshape(B, 3, H, W)).cuda()
+    outs = [torch.empty(B, H, W, c, device="cuda") for c in (3, 1, cfg.desc_dim) * 2]
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def step():
+        m.pair(img1, img2, B, *outs, stream=stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    G.profile_begin()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        step()
+    end.record()
+    torch.cuda.synchronize()
+    prof = G.profile_end()
+    ms = start.elapsed_time(end)
+    ms_per_step = ms / args.steps
+    value = B * args.steps / (ms / 1000.0)
+
+    # roofline of the dominant kernel (largest summed event time)
+    dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
+    avg_ms = dom["ms"] / dom["launches"]
+    if dom["flops"] > 0 and dom_name.startswith(("gemm", "attn")):
+        achieved = dom["flops"] / dom["launches"] / (avg_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_FP32_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_FP32_PEAK_TFLOPS, 4),
+                "traffic": None}
+    else:
+        achieved = dom["bytes"] / dom["launches"] / (avg_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    roof["kernel"] = dom_name
+    roof["launches_per_step"] = dom["launches"] // args.steps
+    roof["avg_launch_ms"] = round(avg_ms, 4)
+    mfma_ms = sum(v["ms"] for k, v in prof.items() if k.startswith(("gemm", "attn")))
+    mfma_fl = sum(v["flops"] for k, v in prof.items() if k.startswith(("gemm", "attn")))
+    kernels = {k: {"launches": v["launches"] // args.steps, "ms_per_step": round(v["ms"] / args.steps, 3),
+                   "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2) if v["flops"] else None,
+                   "gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1) if v["bytes"] else None}
+               for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
+
+    out = {
+        "metric": "MASt3R image pairs/sec @512x384 fp32 on 1 MI355X; GEMM/attn % MFMA peak",
+        "value": round(value, 3),
+        "unit": "pairs/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded U(-1,1) images, seeded N(0,0.02) weights)",
+        "config": {"workload": f"config {args.config}: {B} image pairs at 3x{H}x{W}, full "
+                               f"MASt3R two-view inference (ViT-L encoder x2 views, ViT-B "
+                               f"decoder, 2 DPT heads, 2 local-feature heads)",
+                   "pairs_per_step": B, "img": [3, H, W], "parallelism": "single GPU"},
+        "gemm_attn_frac_fp32_mfma_peak": round(mfma_fl / (mfma_ms * 1e-3) / 1e12 /
+                                               MFMA_FP32_PEAK_TFLOPS, 4),
+        "kernel_share_of_step": round(sum(v["ms"] for v in prof.values()) / ms, 4),
+        "roofline": roof,
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    m.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,203 @@
+// Flash attention (online softmax) on gfx950 matrix cores, fp32, head dim 64.
+//
+// Replaces the reference's attention paths: the CPU loops of
+// MultiHeadAttention#scaled_dot_product_attention_cpu
+// (src/nn/attention.cr:215-325: scores, row max, exp, sum, divide, P.V) and the
+// Metal flash_attention kernel behind GPUOps.fused_attention
+// (src/nn/gpu_ops.cr:200-227). Self and cross attention (Nq != Nkv allowed).
+//
+// Workgroup = 4 wavefronts = 128 queries of one (batch, head). K/V tiles of
+// 64 keys are staged through LDS (shared by the 4 wavefronts) and prefetched
+// into registers one tile ahead. Each wavefront computes, per 32-key block:
+//   S^T (32 keys x 32 queries) = K . Q^T   -- 32 x v_mfma_f32_32x32x2_f32
+//   O^T (64 x 32)             += V^T . P^T -- 2 x 16 MFMAs
+// Computing S transposed puts all 16 scores a lane holds in one query column
+// (query = lane % 32), so the row max / row sum need one cross-half exchange
+// and the exponentiated scores are already the B operand of the P.V product:
+// MFMA step s takes key 8*(s/4) + 4*(lane/32) + s%4 -- exactly the key the
+// lane holds in accumulator register s. No LDS round trip for P.
+#include "internal.h"
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+namespace gs {
+namespace {
+
+constexpr int QT = 128;  // queries per workgroup
+constexpr int KT = 64;   // keys per LDS tile
+constexpr int HD = 64;
+
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32_t Bcount) {
+  const int grp = blockIdx.z / Bcount;
+  const int b = blockIdx.z - grp * Bcount;
+  const AttnArgs& p = batch.g[grp];
+  const int head = blockIdx.y;
+  const int Nq = p.Nq, Nkv = p.Nkv;
+
+  __shared__ __attribute__((aligned(16))) float Ks[KT][HD + 4];
+  __shared__ __attribute__((aligned(16))) float Vs[KT][HD];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  const float* qb = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh;
+  const float* kb = p.k + (int64_t)b * p.k_sb + (int64_t)head * p.k_sh;
+  const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)head * p.v_sh;
+  float* ob = p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh;
+
+  const int q0 = blockIdx.x * QT + wave * 32;
+  // Q fragment: lane holds q[query l32][32*hl .. 32*hl+31], pre-scaled so the
+  // softmax runs in base 2: exp(s - m) == exp2(s*log2e - m*log2e).
+  const float qscale = p.scale * 1.4426950408889634f;
+  float qf[32];
+  {
+    const int qrow = min(q0 + l32, Nq - 1);
+    const float* qr = qb + (int64_t)qrow * p.q_sn + hl * 32;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const fx4 v = *(const fx4*)(qr + 4 * t);
+      qf[4 * t + 0] = v.x * qscale;
+      qf[4 * t + 1] = v.y * qscale;
+      qf[4 * t + 2] = v.z * qscale;
+      qf[4 * t + 3] = v.w * qscale;
+    }
+  }
+
+  floatx16 o0 = {}, o1 = {};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // Tile load assignment: key rows tid/16 + 16*i, fx4 column tid%16.
+  const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
+  fx4 rk[4], rv[4];
+  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+  auto load_kv = [&](int kbase) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = kbase + lrow + 16 * i;
+      if (key < Nkv) {
+        rk[i] = *(const fx4*)(kb + (int64_t)key * p.k_sn + lc4);
+        rv[i] = *(const fx4*)(vb + (int64_t)key * p.v_sn + lc4);
+      } else {
+        rk[i] = zero4;
+        rv[i] = zero4;
+      }
+    }
+  };
+
+  load_kv(0);
+  for (int kbase = 0; kbase < Nkv; kbase += KT) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *(fx4*)&Ks[lrow + 16 * i][lc4] = rk[i];
+      *(fx4*)&Vs[lrow + 16 * i][lc4] = rv[i];
+    }
+    __syncthreads();
+    if (kbase + KT < Nkv) load_kv(kbase + KT);
+
+#pragma unroll
+    for (int sub = 0; sub < KT / 32; ++sub) {
+      const int sb = kbase + sub * 32;
+      if (sb >= Nkv) break;
+      // S^T block: A = K rows (key l32, k = 32*hl + t), B = Q^T.
+      floatx16 s = {};
+      const float* kr = &Ks[sub * 32 + l32][hl * 32];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const fx4 kf = *(const fx4*)(kr + 4 * t);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.x, qf[4 * t + 0], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.y, qf[4 * t + 1], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[4 * t + 2], s, 0, 0, 0);
+        s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[4 * t + 3], s, 0, 0, 0);
+      }
+      if (sb + 32 > Nkv) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = sb + 8 * (r >> 2) + 4 * hl + (r & 3);
+          if (key >= Nkv) s[r] = -INFINITY;
+        }
+      }
+      float mb = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
+      mb = fmaxf(mb, __shfl_xor(mb, 32));
+      const float m_new = fmaxf(m_run, mb);
+      const float alpha = exp2f(m_run - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = exp2f(s[r] - m_new);
+        ps += s[r];
+      }
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        o0[r] *= alpha;
+        o1[r] *= alpha;
+      }
+      // O^T += V^T P^T: A = V^T (hd row l32, k = key of register st).
+#pragma unroll
+      for (int st = 0; st < 16; ++st) {
+        const int kr2 = sub * 32 + 8 * (st >> 2) + 4 * hl + (st & 3);
+        const float v0 = Vs[kr2][l32];
+        const float v1 = Vs[kr2][32 + l32];
+        o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(v0, s[st], o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(v1, s[st], o1, 0, 0, 0);
+      }
+    }
+  }
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / l_tot;
+  const int q = q0 + l32;
+  if (q < Nq) {
+    float* orow = ob + (int64_t)q * p.o_sn;
+    // O^T layout: lane holds hd 8*g + 4*hl + {0..3} (+32 for o1) of query l32.
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      *(fx4*)(orow + 8 * g + 4 * hl) =
+          mk4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv,
+                      o0[4 * g + 3] * inv);
+      *(fx4*)(orow + 32 + 8 * g + 4 * hl) =
+          mk4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv,
+                      o1[4 * g + 3] * inv);
+    }
+  }
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+}  // namespace
+
+int launch_attention(const AttnBatch& bt, hipStream_t s) {
+  GS_REQUIRE(bt.ngroups >= 1 && bt.ngroups <= kMaxGroups, "attention: bad group count");
+  const AttnArgs& a0 = bt.g[0];
+  for (int i = 0; i < bt.ngroups; ++i) {
+    const AttnArgs& a = bt.g[i];
+    GS_REQUIRE(a.B == a0.B && a.H == a0.H && a.Nq == a0.Nq && a.Nkv == a0.Nkv,
+               "attention: grouped problems must share shapes");
+    GS_REQUIRE(a.q && a.k && a.v && a.o, "attention: null operand");
+    GS_REQUIRE(aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o),
+               "attention: operands must be 16-byte aligned");
+    const int64_t st[12] = {a.q_sb, a.q_sh, a.q_sn, a.k_sb, a.k_sh, a.k_sn,
+                            a.v_sb, a.v_sh, a.v_sn, a.o_sb, a.o_sh, a.o_sn};
+    for (int j = 0; j < 12; ++j)
+      GS_REQUIRE(st[j] % 4 == 0 && st[j] >= 0, "attention: strides must be multiples of 4");
+  }
+  GS_REQUIRE(a0.B > 0 && a0.H > 0 && a0.Nq > 0 && a0.Nkv > 0, "attention: bad sizes");
+  GS_REQUIRE((int64_t)a0.B * bt.ngroups <= 65535 && a0.H <= 65535, "attention: grid too large");
+  dim3 grid((a0.Nq + QT - 1) / QT, a0.H, a0.B * bt.ngroups), block(256);
+  hipEvent_t ev = prof_start(s);
+  hipLaunchKernelGGL(attn_fwd_kernel, grid, block, 0, s, bt, a0.B);
+  GS_CHECK_HIP(hipGetLastError());
+  if (ev) {
+    const double units = (double)a0.B * a0.H * bt.ngroups;
+    prof_stop(s, ev, "attn_fwd_kernel", units * 4.0 * a0.Nq * (double)a0.Nkv * 64.0,
+              units * 4.0 * 64.0 * (2.0 * a0.Nq + 2.0 * a0.Nkv));
+  }
+  return 0;
+}
+
+}  // namespace gs

@@ -1,0 +1,381 @@
+// HBM-bound kernels of the path: LayerNorm, patch unfold, bilinear x2
+// upsample, RoPE (standalone forms), and the DPT output head split.
+#include <math.h>
+
+#include "internal.h"
+
+namespace gs {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+// LayerNorm#forward_cpu (src/nn/layernorm.cr:192-240): two-pass mean /
+// variance, inv_std = 1/sqrt(var + eps), y = (x - mean)*inv_std*gamma + beta.
+// One wavefront per row, the row held in registers (D <= 256*NV).
+template <int NV>
+__global__ __launch_bounds__(256) void layernorm_kernel(LnBatch bt) {
+  const LnArgs& p = bt.g[blockIdx.y];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= p.rows) return;
+  const int D = p.D, nv = D >> 2;
+  const fx4* xr = (const fx4*)(p.x + row * D);
+  fx4 v[NV];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < nv) {
+      v[i] = xr[idx];
+      s += v[i].x + v[i].y + v[i].z + v[i].w;
+    } else {
+      v[i] = mk4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const float mean = wave_sum(s) / (float)D;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < nv) {
+      const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+      q += a * a + b * b + c * c + d * d;
+    }
+  }
+  const float var = wave_sum(q) / (float)D;
+  const float inv = 1.0f / sqrtf(var + p.eps);
+  const fx4* g4 = (const fx4*)p.gamma;
+  const fx4* b4 = (const fx4*)p.beta;
+  fx4* yr = (fx4*)(p.y + row * D);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < nv) {
+      const fx4 g = g4[idx], bb = b4[idx];
+      fx4 o;
+      o.x = (v[i].x - mean) * inv * g.x + bb.x;
+      o.y = (v[i].y - mean) * inv * g.y + bb.y;
+      o.z = (v[i].z - mean) * inv * g.z + bb.z;
+      o.w = (v[i].w - mean) * inv * g.w + bb.w;
+      yr[idx] = o;
+    }
+  }
+}
+
+// PatchEmbedding#forward unfold (src/nn/vit.cr:56-76): NCHW image -> rows of
+// C*p*p in (c, i, j) order. One thread per output fx4.
+__global__ void unfold_kernel(const float* __restrict__ img, int32_t B, int32_t H,
+                              int32_t W, int32_t p, float* __restrict__ out) {
+  const int gw = W / p, gh = H / p;
+  const int K = 3 * p * p, K4 = K >> 2;
+  const int64_t total = (int64_t)B * gh * gw * K4;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  const int64_t m = t / K4;
+  const int k = (int)(t - m * K4) * 4;
+  const int b = (int)(m / (gh * gw));
+  const int rem = (int)(m - (int64_t)b * gh * gw);
+  const int ty = rem / gw, tx = rem - ty * gw;
+  const int c = k / (p * p), ij = k - c * p * p, i = ij / p, j = ij - i * p;
+  const fx4 v = *(const fx4*)(img + (((int64_t)b * 3 + c) * H + ty * p + i) * W +
+                                    tx * p + j);
+  *(fx4*)(out + m * K + k) = v;
+}
+
+// Bilinear x2, align_corners=True (source = dst * (in-1)/(out-1)), NHWC.
+__global__ void upsample2x_kernel(const float* __restrict__ x, int32_t B, int32_t H,
+                                  int32_t W, int32_t C, float* __restrict__ y) {
+  const int Ho = 2 * H, Wo = 2 * W, C4 = C >> 2;
+  const int64_t total = (int64_t)B * Ho * Wo * C4;
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= total) return;
+  const int c = (int)(t % C4) * 4;
+  int64_t r = t / C4;
+  const int ox = (int)(r % Wo);
+  r /= Wo;
+  const int oy = (int)(r % Ho);
+  const int b = (int)(r / Ho);
+  const float sh = (float)(H - 1) / (float)(Ho - 1);
+  const float sw = (float)(W - 1) / (float)(Wo - 1);
+  const float fy = sh * (float)oy, fx = sw * (float)ox;
+  const int y0 = (int)fy, x0 = (int)fx;
+  const int y1 = y0 + (y0 < H - 1 ? 1 : 0), x1 = x0 + (x0 < W - 1 ? 1 : 0);
+  const float ly = fy - (float)y0, hy = 1.0f - ly;
+  const float lx = fx - (float)x0, hx = 1.0f - lx;
+  const float* base = x + (int64_t)b * H * W * C + c;
+  const fx4 a = *(const fx4*)(base + ((int64_t)y0 * W + x0) * C);
+  const fx4 bq = *(const fx4*)(base + ((int64_t)y0 * W + x1) * C);
+  const fx4 cq = *(const fx4*)(base + ((int64_t)y1 * W + x0) * C);
+  const fx4 d = *(const fx4*)(base + ((int64_t)y1 * W + x1) * C);
+  fx4 o;
+  o.x = hy * (hx * a.x + lx * bq.x) + ly * (hx * cq.x + lx * d.x);
+  o.y = hy * (hx * a.y + lx * bq.y) + ly * (hx * cq.y + lx * d.y);
+  o.z = hy * (hx * a.z + lx * bq.z) + ly * (hx * cq.z + lx * d.z);
+  o.w = hy * (hx * a.w + lx * bq.w) + ly * (hx * cq.w + lx * d.w);
+  *(fx4*)(y + t * 4) = o;
+}
+
+// 2D RoPE in place; one thread per rotated pair (token, head, axis, j < 16).
+__global__ void rope2d_kernel(float* t, int32_t B, int32_t N, int32_t H, int64_t ld,
+                              int32_t grid_w, const float* __restrict__ cos_t,
+                              const float* __restrict__ sin_t) {
+  const int64_t total = (int64_t)B * N * H * 32;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int j = (int)(id & 15);
+  const int ax = (int)((id >> 4) & 1);
+  const int64_t rest = id >> 5;
+  const int h = (int)(rest % H);
+  const int64_t tokg = rest / H;
+  const int n = (int)(tokg % N);
+  const int pos = ax ? n % grid_w : n / grid_w;
+  float* u = t + tokg * ld + h * 64 + ax * 32;
+  const float c = cos_t[pos * 16 + j], s = sin_t[pos * 16 + j];
+  const float a = u[j], b = u[j + 16];
+  u[j] = a * c - b * s;
+  u[j + 16] = b * c + a * s;
+}
+
+// Token-level RoPE of MASt3REncoderV2#apply_rope (src/mastr/encoder_v2.cr:
+// 204-254) with an explicit grid; one thread per element.
+__global__ void rope_ref_token_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                      int32_t B, int32_t gh, int32_t gw, int32_t D,
+                                      int32_t hd, const float* __restrict__ cos_t,
+                                      const float* __restrict__ sin_t) {
+  const int64_t total = (int64_t)B * gh * gw * D;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int d = (int)(id % D);
+  const int64_t tok = id / D;
+  const int n = (int)(tok % ((int64_t)gh * gw));
+  const int yy = n / gw, xi = n - yy * gw;
+  const int half = hd / 2, dh = d % hd;
+  if (dh < half) {
+    const float c = cos_t[yy * half + dh], s = sin_t[yy * half + dh];
+    y[id] = x[id] * c - x[id + half] * s;
+  } else {
+    const int f = dh - half;
+    const float c = cos_t[xi * half + f], s = sin_t[xi * half + f];
+    y[id] = x[id - half] * s + x[id] * c;
+  }
+}
+
+// DPT head tail: 1x1 conv Cin -> 4 (+bias), pts = ch 0..2, conf = 1 + exp(ch 3)
+// (the reference's split_output, src/mastr/decoder_v2.cr:619-655, with the
+// MASt3R confidence mapping).
+__global__ __launch_bounds__(256) void head_out_kernel(const float* __restrict__ x, int64_t P,
+                                                       int32_t Cin, const float* __restrict__ w,
+                                                       const float* __restrict__ b,
+                                                       float* __restrict__ pts,
+                                                       float* __restrict__ conf) {
+  extern __shared__ float ws[];  // [4][Cin]
+  for (int i = threadIdx.x; i < 4 * Cin; i += blockDim.x) ws[i] = w[i];
+  __syncthreads();
+  const int64_t px = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (px >= P) return;
+  const fx4* xr = (const fx4*)(x + px * Cin);
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+  for (int c4 = 0; c4 < (Cin >> 2); ++c4) {
+    const fx4 v = xr[c4];
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = c4 * 4 + u;
+      a0 += vv[u] * ws[c];
+      a1 += vv[u] * ws[Cin + c];
+      a2 += vv[u] * ws[2 * Cin + c];
+      a3 += vv[u] * ws[3 * Cin + c];
+    }
+  }
+  pts[px * 3 + 0] = a0 + b[0];
+  pts[px * 3 + 1] = a1 + b[1];
+  pts[px * 3 + 2] = a2 + b[2];
+  conf[px] = 1.0f + expf(a3 + b[3]);
+}
+
+inline unsigned nblocks(int64_t total, int per) { return (unsigned)((total + per - 1) / per); }
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+}  // namespace
+
+int launch_layernorm(const LnBatch& bt, hipStream_t s) {
+  GS_REQUIRE(bt.ngroups >= 1 && bt.ngroups <= kMaxGroups, "layernorm: bad group count");
+  int64_t max_rows = 0;
+  const int D = bt.g[0].D;
+  for (int i = 0; i < bt.ngroups; ++i) {
+    const LnArgs& a = bt.g[i];
+    GS_REQUIRE(a.D == D, "layernorm: grouped rows must share D");
+    GS_REQUIRE(a.x && a.y && a.gamma && a.beta, "layernorm: null operand");
+    GS_REQUIRE(aligned16(a.x) && aligned16(a.y) && aligned16(a.gamma) && aligned16(a.beta),
+               "layernorm: operands must be 16-byte aligned");
+    max_rows = a.rows > max_rows ? a.rows : max_rows;
+  }
+  GS_REQUIRE(D > 0 && D % 4 == 0 && D <= 4096, "layernorm: need 0 < D <= 4096, D % 4 == 0");
+  if (max_rows == 0) return 0;
+  dim3 grid(nblocks(max_rows, 4), bt.ngroups), block(256);
+  hipEvent_t ev = prof_start(s);
+  if (D <= 1024)
+    hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, s, bt);
+  else
+    hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, s, bt);
+  GS_CHECK_HIP(hipGetLastError());
+  if (ev) {
+    double rows = 0;
+    for (int i = 0; i < bt.ngroups; ++i) rows += (double)bt.g[i].rows;
+    prof_stop(s, ev, "layernorm_kernel", 8.0 * rows * D, 4.0 * rows * D * 2.0 + 8.0 * D);
+  }
+  return 0;
+}
+
+int launch_unfold(const float* img, int32_t B, int32_t H, int32_t W, int32_t p,
+                  float* out, hipStream_t s) {
+  GS_REQUIRE(p % 4 == 0 && H % p == 0 && W % p == 0, "unfold: H, W must be multiples of p, p % 4 == 0");
+  GS_REQUIRE(aligned16(img) && aligned16(out), "unfold: operands must be 16-byte aligned");
+  const int64_t total = (int64_t)B * (H / p) * (W / p) * (3 * p * p / 4);
+  if (total == 0) return 0;
+  hipEvent_t ev = prof_start(s);
+  hipLaunchKernelGGL(unfold_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, img, B, H, W,
+                     p, out);
+  GS_CHECK_HIP(hipGetLastError());
+  prof_stop(s, ev, "unfold_kernel", 0.0, 8.0 * (double)total * 4.0);
+  return 0;
+}
+
+int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C,
+                      float* y, hipStream_t s) {
+  GS_REQUIRE(C % 4 == 0 && H > 0 && W > 0, "upsample2x: need C % 4 == 0");
+  GS_REQUIRE(aligned16(x) && aligned16(y), "upsample2x: operands must be 16-byte aligned");
+  const int64_t total = (int64_t)B * 4 * H * W * (C / 4);
+  if (total == 0) return 0;
+  hipEvent_t ev = prof_start(s);
+  hipLaunchKernelGGL(upsample2x_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, x, B, H,
+                     W, C, y);
+  GS_CHECK_HIP(hipGetLastError());
+  prof_stop(s, ev, "upsample2x_kernel", 0.0, 4.0 * (double)B * H * W * C * 5.0);
+  return 0;
+}
+
+int launch_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld, int32_t grid_w,
+                  const float* cos_t, const float* sin_t, hipStream_t s) {
+  GS_REQUIRE(ld >= (int64_t)H * 64 && grid_w > 0, "rope2d: bad layout");
+  const int64_t total = (int64_t)B * N * H * 32;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(rope2d_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, t, B, N, H,
+                     ld, grid_w, cos_t, sin_t);
+  GS_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+int launch_rope_ref_token(const float* x, float* y, int32_t B, int32_t gh, int32_t gw,
+                          int32_t D, int32_t H, const float* cos_t, const float* sin_t,
+                          int32_t max_pos, hipStream_t s) {
+  GS_REQUIRE(H > 0 && D % H == 0 && (D / H) % 2 == 0, "rope_ref_token: bad head split");
+  GS_REQUIRE(gh <= max_pos && gw <= max_pos, "rope_ref_token: table too small");
+  const int64_t total = (int64_t)B * gh * gw * D;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(rope_ref_token_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, x, y,
+                     B, gh, gw, D, D / H, cos_t, sin_t);
+  GS_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+int launch_head_out(const float* x, int64_t P, int32_t Cin, const float* w, const float* b,
+                    float* pts, float* conf, hipStream_t s) {
+  GS_REQUIRE(Cin % 4 == 0 && Cin <= 4096, "head_out: need Cin % 4 == 0");
+  GS_REQUIRE(aligned16(x), "head_out: input must be 16-byte aligned");
+  if (P == 0) return 0;
+  hipEvent_t ev = prof_start(s);
+  hipLaunchKernelGGL(head_out_kernel, dim3(nblocks(P, 256)), dim3(256),
+                     4 * Cin * sizeof(float), s, x, P, Cin, w, b, pts, conf);
+  GS_CHECK_HIP(hipGetLastError());
+  prof_stop(s, ev, "head_out_kernel", 8.0 * (double)P * Cin, 4.0 * (double)P * (Cin + 4));
+  return 0;
+}
+
+void rope_table_host(int32_t max_pos, float base, float* cos_t, float* sin_t) {
+  // inv_freq_j = 1 / base^(2j/32) for the 16 frequency pairs of one 32-dim
+  // axis half; theta = pos * inv_freq_j in fp32, libm cos/sin.
+  for (int32_t p = 0; p < max_pos; ++p)
+    for (int32_t j = 0; j < 16; ++j) {
+      const float inv = 1.0f / powf(base, (float)(2 * j) / 32.0f);
+      const float th = (float)p * inv;
+      cos_t[p * 16 + j] = cosf(th);
+      sin_t[p * 16 + j] = sinf(th);
+    }
+}
+
+void rope_ref_table_host(int32_t max_pos, int32_t hd, float base, float* cos_t,
+                         float* sin_t) {
+  const int32_t half = hd / 2;
+  for (int32_t p = 0; p < max_pos; ++p)
+    for (int32_t i = 0; i < half; ++i) {
+      const float f = 1.0f / powf(base, (2.0f * (float)i) / (float)hd);
+      const float th = (float)p * f;
+      cos_t[p * half + i] = cosf(th);
+      sin_t[p * half + i] = sinf(th);
+    }
+}
+
+}  // namespace gs
+
+namespace gs {
+namespace {
+
+__global__ void oihw_to_ohwi_kernel(const float* __restrict__ w, int32_t Cout, int32_t Cin,
+                                    int32_t k, float* __restrict__ out) {
+  const int64_t total = (int64_t)Cout * Cin * k * k;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  // id indexes the OHWI output: ((oc*k + kh)*k + kw)*Cin + ic
+  const int ic = (int)(id % Cin);
+  int64_t r = id / Cin;
+  const int kw = (int)(r % k);
+  r /= k;
+  const int kh = (int)(r % k);
+  const int oc = (int)(r / k);
+  out[id] = w[(((int64_t)oc * Cin + ic) * k + kh) * k + kw];
+}
+
+__global__ void convt_relayout_kernel(const float* __restrict__ w, const float* __restrict__ b,
+                                      int32_t Cin, int32_t Cout, int32_t k,
+                                      float* __restrict__ wout, float* __restrict__ bout) {
+  const int64_t N = (int64_t)k * k * Cout;
+  const int64_t total = N * Cin;
+  const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= total) return;
+  const int ic = (int)(id % Cin);
+  const int64_t n = id / Cin;
+  const int oc = (int)(n % Cout);
+  const int ij = (int)(n / Cout);
+  const int i = ij / k, j = ij - i * k;
+  wout[id] = w[(((int64_t)ic * Cout + oc) * k + i) * k + j];
+  if (ic == 0 && bout) bout[n] = b ? b[oc] : 0.f;
+}
+
+}  // namespace
+
+int launch_oihw_to_ohwi(const float* w, int32_t Cout, int32_t Cin, int32_t k, float* out,
+                        hipStream_t s) {
+  const int64_t total = (int64_t)Cout * Cin * k * k;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(oihw_to_ohwi_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     s, w, Cout, Cin, k, out);
+  GS_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+int launch_convt_relayout(const float* w, const float* b, int32_t Cin, int32_t Cout, int32_t k,
+                          float* wout, float* bout, hipStream_t s) {
+  const int64_t total = (int64_t)k * k * Cout * Cin;
+  if (total == 0) return 0;
+  hipLaunchKernelGGL(convt_relayout_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     s, w, b, Cin, Cout, k, wout, bout);
+  GS_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // namespace gs

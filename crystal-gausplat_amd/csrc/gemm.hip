@@ -1,0 +1,322 @@
+// fp32 GEMM on gfx950 matrix cores (v_mfma_f32_32x32x2_f32), LDS-staged.
+//
+// Covers every Linear of the path (NN::Linear#forward, src/nn/linear.cr:41-63,
+// whose GPU seam is GPUOps.linear_forward, src/nn/gpu_ops.cr:39-78) and every
+// DPT convolution as an implicit GEMM (Conv2DBlock#forward,
+// src/mastr/decoder_v2.cr:241-344; GPUOps.conv2d_forward,
+// src/nn/gpu_ops.cr:478-527), with the reference's CPU-side passes (bias,
+// GELU, ReLU, residual add, RoPE) fused into the epilogue.
+//
+// Tiling: 256 threads = 4 wavefronts in a 2x2 arrangement, workgroup tile
+// 128x128, K step 32. Each wavefront owns a 64x64 sub-tile = 2x2 MFMA 32x32
+// blocks (64 accumulator registers per lane). Within one K step of 32, lane l
+// (half h = l/32) feeds MFMA step t (0..15) with k = 16h + t, so every lane
+// reads 16 contiguous k of its row: four ds_read_b128 per operand per step.
+// LDS rows are padded to 36 floats so the 8 lanes of each ds_read_b128 phase
+// hit 32 distinct banks. The next K step is prefetched into registers while
+// the current one runs on the matrix cores.
+#include "internal.h"
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+namespace gs {
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 32, LDS = BK + 4;
+constexpr int GROUP_M = 8;
+
+__device__ __forceinline__ float gelu_tanh(float v) {
+  // 0.5*v*(1+tanh(c*(v+0.044715*v^3))), c = (float)sqrt(2/pi), evaluated in
+  // the reference's operation order (src/nn/vit.cr:138-142).
+  const float c = 0.7978845608028654f;
+  float inner = 0.044715f * v;
+  inner = inner * v;
+  inner = inner * v;
+  inner = v + inner;
+  float t = tanhf(c * inner);
+  float h = 0.5f * v;
+  return h * (1.0f + t);
+}
+
+__device__ __forceinline__ fx4 relu4(fx4 v) {
+  return mk4(fmaxf(v.x, 0.f), fmaxf(v.y, 0.f), fmaxf(v.z, 0.f),
+                     fmaxf(v.w, 0.f));
+}
+
+template <int ALOAD, int BLAYOUT, bool A_RELU>
+__global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int M = p.M, N = p.N, K = p.K;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int ntiles = tiles_m * tiles_n;
+
+  // XCD-aware remap: workgroups are dealt round-robin to the 8 XCDs; give
+  // each XCD a contiguous range of logical tiles so neighbouring tiles (which
+  // share A rows / B columns) meet in the same L2.
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  if (bid >= ntiles) return;
+  // Grouped ordering: GROUP_M row tiles sweep the column tiles together.
+  const int per_group = GROUP_M * tiles_n;
+  const int gid = bid / per_group;
+  const int first_m = gid * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (bid % per_group) % gsz;
+  const int tn = (bid % per_group) / gsz;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  __shared__ __attribute__((aligned(16))) float As[BM][LDS];
+  __shared__ __attribute__((aligned(16))) float Bs[BN][LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  // Global->LDS assignment: rows tid/8 + 32*i, fx4 column tid%8.
+  const int lrow = tid >> 3, lc4 = (tid & 7) * 4;
+
+  // Implicit-conv row decode (output pixel -> image, oh, ow).
+  int cimg[4], coh[4], cow[4];
+  if (ALOAD == A_CONV) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = m0 + lrow + 32 * i;
+      const int hw = p.cHo * p.cWo;
+      cimg[i] = m / hw;
+      const int rem = m - cimg[i] * hw;
+      coh[i] = rem / p.cWo;
+      cow[i] = rem - coh[i] * p.cWo;
+    }
+  }
+
+  fx4 ra[4], rb[4];
+  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+
+// Global loads of one K step into registers (macro rather than lambda so the
+// register arrays stay in VGPRs).
+#define GS_GEMM_LOAD(K0)                                                                \
+  {                                                                                     \
+    const int k0_ = (K0);                                                               \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
+      const int m = m0 + lrow + 32 * i;                                                 \
+      fx4 v = zero4;                                                                 \
+      if (ALOAD == A_PLAIN) {                                                           \
+        if (m < M) v = *(const fx4*)(p.A + (int64_t)m * p.lda + k0_ + lc4);          \
+      } else if (ALOAD == A_CONCAT) {                                                   \
+        if (m < M) {                                                                    \
+          if (k0_ < p.K1)                                                               \
+            v = *(const fx4*)(p.A + (int64_t)m * p.lda + k0_ + lc4);                 \
+          else                                                                          \
+            v = *(const fx4*)(p.A2 + (int64_t)m * p.lda2 + (k0_ - p.K1) + lc4);      \
+        }                                                                               \
+      } else {                                                                          \
+        const int kk = k0_ / p.cCin;                                                    \
+        const int ic0 = k0_ - kk * p.cCin;                                              \
+        const int kh = kk / p.ck, kw = kk - kh * p.ck;                                  \
+        const int ih = coh[i] * p.cs + kh - p.cp;                                       \
+        const int iw = cow[i] * p.cs + kw - p.cp;                                       \
+        if (m < M && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW)                      \
+          v = *(const fx4*)(p.A + (((int64_t)cimg[i] * p.cH + ih) * p.cW + iw) *     \
+                                         p.cCin + ic0 + lc4);                           \
+      }                                                                                 \
+      if (A_RELU) v = relu4(v);                                                         \
+      ra[i] = v;                                                                        \
+      if (BLAYOUT == B_NT) {                                                            \
+        const int n = n0 + lrow + 32 * i;                                               \
+        rb[i] = n < N ? *(const fx4*)(p.B + (int64_t)n * p.ldb + k0_ + lc4) : zero4; \
+      } else {                                                                          \
+        const int kb = (tid >> 5) + 8 * i;                                              \
+        const int n = n0 + 4 * (tid & 31);                                              \
+        rb[i] = n < N ? *(const fx4*)(p.B + (int64_t)(k0_ + kb) * p.ldb + n) : zero4; \
+      }                                                                                 \
+    }                                                                                   \
+  }
+
+  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+
+  GS_GEMM_LOAD(0)
+  for (int k0 = 0; k0 < K; k0 += BK) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *(fx4*)&As[lrow + 32 * i][lc4] = ra[i];
+      if (BLAYOUT == B_NT) {
+        *(fx4*)&Bs[lrow + 32 * i][lc4] = rb[i];
+      } else {
+        const int kb = (tid >> 5) + 8 * i;
+        const int n = 4 * (tid & 31);
+        Bs[n + 0][kb] = rb[i].x;
+        Bs[n + 1][kb] = rb[i].y;
+        Bs[n + 2][kb] = rb[i].z;
+        Bs[n + 3][kb] = rb[i].w;
+      }
+    }
+    __syncthreads();
+    if (k0 + BK < K) GS_GEMM_LOAD(k0 + BK)
+    const float* a0p = &As[wm * 64 + l32][hl * 16];
+    const float* a1p = &As[wm * 64 + 32 + l32][hl * 16];
+    const float* b0p = &Bs[wn * 64 + l32][hl * 16];
+    const float* b1p = &Bs[wn * 64 + 32 + l32][hl * 16];
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) {
+      const fx4 a0 = *(const fx4*)(a0p + t4 * 4);
+      const fx4 a1 = *(const fx4*)(a1p + t4 * 4);
+      const fx4 b0 = *(const fx4*)(b0p + t4 * 4);
+      const fx4 b1 = *(const fx4*)(b1p + t4 * 4);
+#define GS_MFMA4(AX, BX)                                                           \
+  acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.AX, b0.BX, acc00, 0, 0, 0);     \
+  acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.AX, b1.BX, acc01, 0, 0, 0);     \
+  acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.AX, b0.BX, acc10, 0, 0, 0);     \
+  acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.AX, b1.BX, acc11, 0, 0, 0);
+      GS_MFMA4(x, x)
+      GS_MFMA4(y, y)
+      GS_MFMA4(z, z)
+      GS_MFMA4(w, w)
+#undef GS_MFMA4
+    }
+  }
+#undef GS_GEMM_LOAD
+
+  // ---- epilogue ----
+  // Accumulator layout of a 32x32 block: lane l, register r holds
+  // row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
+  const int flags = p.flags;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi) {
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+      const floatx16 c = bi == 0 ? (bj == 0 ? acc00 : acc01) : (bj == 0 ? acc10 : acc11);
+      const int cblk = n0 + wn * 64 + bj * 32;
+      const int col = cblk + l32;
+      const float bval = ((flags & EPI_BIAS) && col < N) ? p.bias[col] : 0.f;
+      const bool rope = (flags & EPI_ROPE) && cblk < p.rope_ncols;
+      // scatter column decode (wave-uniform kind, per-lane values)
+      int sc_i = 0, sc_j = 0, sc_c = 0;
+      if (flags & EPI_SCATTER) {
+        const int s = col / p.sc_C;
+        sc_c = col - s * p.sc_C;
+        sc_i = s / p.sc_r;
+        sc_j = s - sc_i * p.sc_r;
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + bi * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+        float v = c[r];
+        if (flags & EPI_BIAS) v = v + bval;
+        if (rope) {
+          const int tok = row % p.tok_per_img;
+          const int ty = tok / p.grid_w, tx = tok - ty * p.grid_w;
+          const int pos = ((cblk >> 5) & 1) ? tx : ty;
+          const int f = l32 & 15;
+          const float cs = p.rope_cos[pos * 16 + f], sn = p.rope_sin[pos * 16 + f];
+          const float partner = __shfl_xor(v, 16);
+          v = (l32 < 16) ? (v * cs - partner * sn) : (v * cs + partner * sn);
+        }
+        if (flags & EPI_GELU) v = gelu_tanh(v);
+        if (flags & EPI_RELU) v = fmaxf(v, 0.f);
+        if (row < M && col < N) {
+          if (flags & EPI_RES1) v = v + p.R1[(int64_t)row * p.ldr1 + col];
+          if (flags & EPI_RES2) v = p.R2[(int64_t)row * p.ldr2 + col] + v;
+          if (flags & EPI_SCATTER) {
+            if (sc_c < p.sc_Cout) {
+              const int hw = p.sc_gh * p.sc_gw;
+              const int img = row / hw;
+              const int rem = row - img * hw;
+              const int y = rem / p.sc_gw, x = rem - (rem / p.sc_gw) * p.sc_gw;
+              const int64_t oy = (int64_t)img * p.sc_gh * p.sc_r + y * p.sc_r + sc_i;
+              const int64_t ox = (int64_t)x * p.sc_r + sc_j;
+              p.C[(oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c] = v;
+            }
+          } else {
+            p.C[(int64_t)row * p.ldc + col] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
+
+}  // namespace
+
+int check_gemm(const GemmArgs& a, int aload, int blayout) {
+  GS_REQUIRE(a.M >= 0 && a.N > 0 && a.K > 0, "gemm: bad sizes");
+  GS_REQUIRE(a.K % BK == 0, "gemm: K must be a multiple of 32");
+  GS_REQUIRE(a.A && a.B && a.C, "gemm: null operand");
+  GS_REQUIRE(aligned16(a.A) && aligned16(a.B), "gemm: operands must be 16-byte aligned");
+  GS_REQUIRE(a.ldb % 4 == 0, "gemm: ldb must be a multiple of 4");
+  if (aload != A_CONV) GS_REQUIRE(a.lda % 4 == 0 && a.lda >= (aload == A_CONCAT ? a.K1 : a.K),
+                                  "gemm: bad lda");
+  if (aload == A_CONCAT)
+    GS_REQUIRE(a.A2 && aligned16(a.A2) && a.K1 % BK == 0 && a.K1 > 0 && a.K1 < a.K &&
+                   a.lda2 % 4 == 0 && a.lda2 >= a.K - a.K1,
+               "gemm: bad concat operand");
+  if (aload == A_CONV) {
+    GS_REQUIRE(a.cCin % BK == 0, "conv: Cin must be a multiple of 32");
+    GS_REQUIRE(a.K == a.ck * a.ck * a.cCin, "conv: K != k*k*Cin");
+    GS_REQUIRE(a.cHo == (a.cH + 2 * a.cp - a.ck) / a.cs + 1 &&
+                   a.cWo == (a.cW + 2 * a.cp - a.ck) / a.cs + 1,
+               "conv: output grid mismatch");
+    GS_REQUIRE(a.M % (a.cHo * a.cWo) == 0, "conv: M must be images*Ho*Wo");
+  }
+  if (blayout == B_NT) GS_REQUIRE(a.ldb >= a.K, "gemm: ldb < K");
+  else GS_REQUIRE(a.N % 4 == 0 && a.ldb >= a.N, "gemm: NN layout needs N % 4 == 0");
+  if (a.flags & EPI_BIAS) GS_REQUIRE(a.bias != nullptr, "gemm: null bias");
+  if (a.flags & EPI_RES1) GS_REQUIRE(a.R1 != nullptr, "gemm: null residual");
+  if (a.flags & EPI_RES2) GS_REQUIRE(a.R2 != nullptr, "gemm: null residual 2");
+  if (a.flags & EPI_ROPE)
+    GS_REQUIRE(a.rope_cos && a.rope_sin && a.rope_ncols % 64 == 0 &&
+                   a.rope_ncols <= a.N && a.tok_per_img > 0 && a.grid_w > 0,
+               "gemm: bad rope epilogue");
+  if (a.flags & EPI_SCATTER)
+    GS_REQUIRE(a.sc_r > 0 && a.sc_C > 0 && a.N == a.sc_r * a.sc_r * a.sc_C &&
+                   a.sc_Cout <= a.sc_C && a.sc_gh > 0 && a.sc_gw > 0 &&
+                   a.M % (a.sc_gh * a.sc_gw) == 0,
+               "gemm: bad scatter epilogue");
+  else
+    GS_REQUIRE(a.ldc >= a.N, "gemm: ldc < N");
+  return 0;
+}
+
+int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
+                hipStream_t s) {
+  GS_REQUIRE(b.ngroups >= 1 && b.ngroups <= kMaxGroups, "gemm: bad group count");
+  int max_tiles = 0;
+  for (int i = 0; i < b.ngroups; ++i) {
+    int rc = check_gemm(b.g[i], aload, blayout);
+    if (rc) return rc;
+    const int t = ((b.g[i].M + BM - 1) / BM) * ((b.g[i].N + BN - 1) / BN);
+    max_tiles = t > max_tiles ? t : max_tiles;
+  }
+  if (max_tiles == 0) return 0;
+  dim3 grid(max_tiles, 1, b.ngroups), block(256);
+  double flops = 0.0, bytes = 0.0;
+  if (prof_on())
+    for (int i = 0; i < b.ngroups; ++i) {
+      const GemmArgs& g = b.g[i];
+      flops += 2.0 * g.M * (double)g.N * g.K;
+      bytes += 4.0 * ((double)g.M * g.K + (double)g.N * g.K + (double)g.M * g.N);
+    }
+#define GS_GEMM_CASE(AL, BL, RL)                                              \
+  if (aload == AL && blayout == BL && a_relu == RL) {                         \
+    hipEvent_t ev = prof_start(s);                                            \
+    hipLaunchKernelGGL((gemm_f32_kernel<AL, BL, RL>), grid, block, 0, s, b);  \
+    GS_CHECK_HIP(hipGetLastError());                                          \
+    prof_stop(s, ev, "gemm_f32_kernel<" #AL "," #BL "," #RL ">", flops, bytes); \
+    return 0;                                                                 \
+  }
+  GS_GEMM_CASE(A_PLAIN, B_NT, false)
+  GS_GEMM_CASE(A_PLAIN, B_NN, false)
+  GS_GEMM_CASE(A_PLAIN, B_NT, true)
+  GS_GEMM_CASE(A_CONCAT, B_NT, false)
+  GS_GEMM_CASE(A_CONV, B_NT, false)
+  GS_GEMM_CASE(A_CONV, B_NT, true)
+#undef GS_GEMM_CASE
+  set_error("gemm: unsupported loader/layout combination");
+  return -1;
+}
+
+}  // namespace gs

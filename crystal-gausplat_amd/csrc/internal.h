@@ -1,0 +1,172 @@
+// Internal declarations shared by the HIP kernels, the C-ABI shim and the
+// MASt3R orchestration. Not part of the public ABI (include/gs_hip.h is).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace gs {
+
+// Native 4-wide float vector for kernels (HIP's float4 struct is copied via
+// memcpy, which keeps register arrays of it out of VGPRs).
+typedef float fx4 __attribute__((ext_vector_type(4)));
+__host__ __device__ inline fx4 mk4(float a, float b, float c, float d) {
+  fx4 r = {a, b, c, d};
+  return r;
+}
+
+// ---- error state (thread-local last error, see gs_hip_last_error) ----------
+void set_error(const std::string& msg);
+const char* last_error();
+hipStream_t default_stream();  // library stream; created by gs_init_device
+int ensure_device();           // 0 ok; lazily runs gs_init_device
+
+#define GS_CHECK_HIP(expr)                                                    \
+  do {                                                                        \
+    hipError_t e_ = (expr);                                                   \
+    if (e_ != hipSuccess) {                                                   \
+      ::gs::set_error(std::string(#expr " failed: ") + hipGetErrorString(e_)); \
+      return -3;                                                              \
+    }                                                                         \
+  } while (0)
+
+#define GS_REQUIRE(cond, msg)       \
+  do {                              \
+    if (!(cond)) {                  \
+      ::gs::set_error(msg);         \
+      return -1;                    \
+    }                               \
+  } while (0)
+
+// ---- per-kernel timing (gs_hip_profile_*) ------------------------------------
+// When enabled, launchers bracket each kernel with HIP events on its stream and
+// record (kernel name, algorithmic flops, algorithmic HBM bytes).
+bool prof_on();
+hipEvent_t prof_start(hipStream_t s);
+void prof_stop(hipStream_t s, hipEvent_t start, const char* kernel, double flops,
+               double bytes);
+
+// ---- GEMM ------------------------------------------------------------------
+// C[M,N] = A[M,K] . B (+ epilogue). One GEMM problem of a (possibly grouped)
+// launch. All pointers are device pointers.
+enum ALoad : int { A_PLAIN = 0, A_CONCAT = 1, A_CONV = 2 };
+enum BLayout : int { B_NT = 0, B_NN = 1 };
+
+enum EpiFlags : int {
+  EPI_BIAS = 1,
+  EPI_GELU = 2,
+  EPI_RELU = 4,
+  EPI_RES1 = 8,      // v = v + R1
+  EPI_RES2 = 16,     // v = R2 + v (applied after RES1)
+  EPI_ROPE = 32,     // RoPE on columns [0, rope_ncols)
+  EPI_SCATTER = 64,  // sub-pixel scatter store (ConvT / pixel shuffle)
+};
+
+struct GemmArgs {
+  const float* A;   // plain / concat first source / conv input (NHWC)
+  int64_t lda;
+  const float* A2;  // concat second source
+  int64_t lda2;
+  int32_t K1;       // concat split (multiple of 32)
+  // implicit convolution (A_CONV): input [Bimg, cH, cW, cCin], kernel ck,
+  // stride cs, pad cp, output grid cHo x cWo; K = ck*ck*cCin, k index =
+  // (kh*ck + kw)*cCin + ic
+  int32_t cH, cW, cCin, ck, cs, cp, cHo, cWo;
+  const float* B;   // NT: B[n*ldb + k]; NN: B[k*ldb + n]
+  int64_t ldb;
+  float* C;
+  int64_t ldc;
+  const float* bias;
+  const float* R1;
+  int64_t ldr1;
+  const float* R2;
+  int64_t ldr2;
+  int32_t M, N, K;
+  int32_t flags;
+  // RoPE epilogue: columns [0, rope_ncols) hold 64-wide heads; row m is token
+  // (m % tok_per_img) of a grid with grid_w columns; tables [pos][16].
+  const float* rope_cos;
+  const float* rope_sin;
+  int32_t rope_ncols, tok_per_img, grid_w;
+  // scatter epilogue: row m = (img, y, x) on a sc_gh x sc_gw grid; column
+  // n = (i*sc_r + j)*sc_C + c -> C[((img*sc_gh*sc_r + y*sc_r + i)*sc_gw*sc_r
+  // + x*sc_r + j)*sc_C + c]; columns with c >= sc_Cout are dropped.
+  int32_t sc_r, sc_C, sc_gh, sc_gw, sc_Cout;
+};
+
+constexpr int kMaxGroups = 2;
+struct GemmBatch {
+  GemmArgs g[kMaxGroups];
+  int32_t ngroups;
+};
+
+// Launch a grouped GEMM (all groups must share the loader / layout kinds).
+int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
+                hipStream_t s);
+int check_gemm(const GemmArgs& a, int aload, int blayout);
+
+// ---- attention -----------------------------------------------------------------
+struct AttnArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  float* o;
+  int64_t q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn;
+  int32_t B, H, Nq, Nkv;
+  float scale;
+};
+struct AttnBatch {
+  AttnArgs g[kMaxGroups];
+  int32_t ngroups;
+};
+int launch_attention(const AttnBatch& b, hipStream_t s);
+
+// ---- LayerNorm -----------------------------------------------------------------
+struct LnArgs {
+  const float* x;
+  const float* gamma;
+  const float* beta;
+  float* y;
+  int64_t rows;
+  int32_t D;
+  float eps;
+};
+struct LnBatch {
+  LnArgs g[kMaxGroups];
+  int32_t ngroups;
+};
+int launch_layernorm(const LnBatch& b, hipStream_t s);
+
+// ---- small kernels -----------------------------------------------------------
+int launch_unfold(const float* img, int32_t B, int32_t H, int32_t W, int32_t p,
+                  float* out, hipStream_t s);
+int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W,
+                      int32_t C, float* y, hipStream_t s);
+int launch_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld,
+                  int32_t grid_w, const float* cos_t, const float* sin_t,
+                  hipStream_t s);
+// Token-level RoPE of the reference; tables cos/sin [max_pos][hd/2].
+int launch_rope_ref_token(const float* x, float* y, int32_t B, int32_t gh,
+                          int32_t gw, int32_t D, int32_t H, const float* cos_t,
+                          const float* sin_t, int32_t max_pos, hipStream_t s);
+// conv 1x1 Cin->4 + split: pts [P,3] = y[0..2], conf [P] = 1 + exp(y[3]).
+int launch_head_out(const float* x, int64_t P, int32_t Cin, const float* w,
+                    const float* b, float* pts, float* conf, hipStream_t s);
+
+// Weight re-layouts (device): OIHW -> OHWI; ConvTranspose [Cin,Cout,k,k] ->
+// [(i*k+j)*Cout + oc][Cin] with the bias expanded to k*k*Cout columns.
+int launch_oihw_to_ohwi(const float* w, int32_t Cout, int32_t Cin, int32_t k,
+                        float* out, hipStream_t s);
+int launch_convt_relayout(const float* w, const float* b, int32_t Cin,
+                          int32_t Cout, int32_t k, float* wout, float* bout,
+                          hipStream_t s);
+
+// RoPE tables for 64-wide heads: cos/sin [max_pos][16], host computed.
+void rope_table_host(int32_t max_pos, float base, float* cos_t, float* sin_t);
+// Reference token-level RoPE tables: cos/sin [max_pos][hd/2] of
+// pos * 1/base^(2i/hd) (src/mastr/encoder_v2.cr:165-176).
+void rope_ref_table_host(int32_t max_pos, int32_t hd, float base, float* cos_t,
+                         float* sin_t);
+
+}  // namespace gs

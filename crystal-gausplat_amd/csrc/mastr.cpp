@@ -1,0 +1,1031 @@
+// MASt3R two-view inference on one GPU: the graph-level entry points.
+//
+// Host-side mirror of the reference model classes (same roles, same order of
+// operations) driving the gfx950 kernels as one launch sequence on a stream:
+//   MASt3REncoderV2 / MASt3REncoderBlockV2   src/mastr/encoder_v2.cr:15-259
+//   MASt3RDecoder / MASt3RDecoderBlock       src/mastr/decoder_v2.cr:16-201
+//   DPTHead / RefineNetBlock / RCU           src/mastr/decoder_v2.cr:356-656
+//   MASt3RInference#forward_pair             src/mastr/inference.cr:92-115
+// Differences from the reference's literal composition follow the MASt3R
+// configuration (per-attention 2D RoPE, cross-attention to the other view,
+// full DPT, 1+exp confidence, local-feature descriptors).
+//
+// Data layout in HBM: tokens are row-major [rows, dim] with the two views
+// stacked (view 1 rows first), i.e. NHWC on the patch grid; DPT activations
+// are NHWC; weights are stored once per context in one arena, linears as
+// [out, in], 3x3 convs re-laid to [out, kh, kw, in] (K contiguous for the
+// implicit GEMM), ConvTranspose to [(i*k+j)*out + oc, in], the cross-attention
+// k/v projections concatenated to one [2D, D] weight, and the descriptor MLP's
+// second layer permuted so its GEMM columns are (sub-pixel, channel) pairs of
+// the 24 kept channels.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/gs_hip.h"
+#include "internal.h"
+
+using namespace gs;
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Weight inventory (checkpoint naming, src/mastr/weight_loader.cr:43-123)
+// ---------------------------------------------------------------------------
+enum WKind { W_WEIGHT = 0, W_BIAS = 1, W_GAMMA = 2, W_BETA = 3 };
+// How a host tensor is placed on the device.
+enum Place {
+  P_PLAIN = 0,    // copied as is
+  P_CONV = 1,     // OIHW -> OHWI
+  P_CONVT_W = 2,  // [Cin,Cout,k,k] -> [(i*k+j)*Cout+oc][Cin]
+  P_CONVT_B = 3,  // bias expanded to k*k*Cout
+  P_KV = 4,       // rows [off, off+rows) of the concatenated k|v weight/bias
+  P_DESC_W = 5,   // descriptor fc2 rows permuted, channel >= desc dropped
+  P_DESC_B = 6,
+};
+
+struct WInfo {
+  std::string name;
+  int64_t shape[4];
+  int kind;
+};
+
+struct Inventory {
+  std::vector<WInfo> w;
+  void add(const std::string& n, std::initializer_list<int64_t> s, int kind) {
+    WInfo x;
+    x.name = n;
+    int i = 0;
+    for (int64_t v : s) x.shape[i++] = v;
+    for (; i < 4; ++i) x.shape[i] = 0;
+    x.kind = kind;
+    w.push_back(x);
+  }
+  void linear(const std::string& n, int64_t out, int64_t in, bool bias = true) {
+    add(n + ".weight", {out, in}, W_WEIGHT);
+    if (bias) add(n + ".bias", {out}, W_BIAS);
+  }
+  void conv(const std::string& n, int64_t out, int64_t in, int64_t k, bool bias = true) {
+    add(n + ".weight", {out, in, k, k}, W_WEIGHT);
+    if (bias) add(n + ".bias", {out}, W_BIAS);
+  }
+  void norm(const std::string& n, int64_t d) {
+    add(n + ".weight", {d}, W_GAMMA);
+    add(n + ".bias", {d}, W_BETA);
+  }
+};
+
+Inventory make_inventory(const gs_mastr_config& c) {
+  Inventory v;
+  const int64_t De = c.enc_dim, Dd = c.dec_dim, F = c.dpt_feat;
+  v.conv("patch_embed.proj", De, 3, c.patch);
+  for (int l = 0; l < c.enc_depth; ++l) {
+    const std::string p = "enc_blocks." + std::to_string(l);
+    v.norm(p + ".norm1", De);
+    v.linear(p + ".attn.qkv", 3 * De, De);
+    v.linear(p + ".attn.proj", De, De);
+    v.norm(p + ".norm2", De);
+    v.linear(p + ".mlp.fc1", c.enc_mlp, De);
+    v.linear(p + ".mlp.fc2", De, c.enc_mlp);
+  }
+  v.norm("enc_norm", De);
+  v.linear("decoder_embed", Dd, De);
+  for (int chain = 0; chain < 2; ++chain)
+    for (int l = 0; l < c.dec_depth; ++l) {
+      const std::string p = (chain ? "dec_blocks2." : "dec_blocks.") + std::to_string(l);
+      v.norm(p + ".norm1", Dd);
+      v.linear(p + ".attn.qkv", 3 * Dd, Dd);
+      v.linear(p + ".attn.proj", Dd, Dd);
+      v.norm(p + ".norm2", Dd);
+      v.norm(p + ".norm3", Dd);
+      v.norm(p + ".norm_y", Dd);
+      v.linear(p + ".cross_attn.projq", Dd, Dd);
+      v.linear(p + ".cross_attn.projk", Dd, Dd);
+      v.linear(p + ".cross_attn.projv", Dd, Dd);
+      v.linear(p + ".cross_attn.proj", Dd, Dd);
+      v.linear(p + ".mlp.fc1", c.dec_mlp, Dd);
+      v.linear(p + ".mlp.fc2", Dd, c.dec_mlp);
+    }
+  v.norm("dec_norm", Dd);
+  for (int hd = 1; hd <= 2; ++hd) {
+    const std::string p = "downstream_head" + std::to_string(hd);
+    const std::string ap = p + ".dpt.act_postprocess.";
+    const int64_t d[4] = {c.dpt_dims[0], c.dpt_dims[1], c.dpt_dims[2], c.dpt_dims[3]};
+    v.conv(ap + "0.0", d[0], De, 1);
+    v.conv(ap + "0.1", d[0], d[0], 4);  // ConvTranspose [in, out, 4, 4]
+    v.conv(ap + "1.0", d[1], Dd, 1);
+    v.conv(ap + "1.1", d[1], d[1], 2);  // ConvTranspose [in, out, 2, 2]
+    v.conv(ap + "2.0", d[2], Dd, 1);
+    v.conv(ap + "3.0", d[3], Dd, 1);
+    v.conv(ap + "3.1", d[3], d[3], 3);
+    for (int i = 0; i < 4; ++i)
+      v.conv(p + ".dpt.scratch.layer" + std::to_string(i + 1) + "_rn", F, d[i], 3, false);
+    for (int r = 1; r <= 4; ++r) {
+      const std::string rp = p + ".dpt.scratch.refinenet" + std::to_string(r);
+      for (int u = (r == 4 ? 2 : 1); u <= 2; ++u) {
+        v.conv(rp + ".resConfUnit" + std::to_string(u) + ".conv1", F, F, 3);
+        v.conv(rp + ".resConfUnit" + std::to_string(u) + ".conv2", F, F, 3);
+      }
+      v.conv(rp + ".out_conv", F, F, 1);
+    }
+    v.conv(p + ".dpt.head.0", F / 2, F, 3);
+    v.conv(p + ".dpt.head.2", c.head_mid, F / 2, 3);
+    v.conv(p + ".dpt.head.4", 4, c.head_mid, 1);
+    v.linear(p + ".head_local_features.fc1", c.lf_hidden, De + Dd);
+    v.linear(p + ".head_local_features.fc2", (int64_t)(c.desc_dim + 1) * c.patch * c.patch,
+             c.lf_hidden);
+  }
+  return v;
+}
+
+int64_t numel(const WInfo& w) {
+  int64_t n = 1;
+  for (int i = 0; i < 4 && w.shape[i]; ++i) n *= w.shape[i];
+  return n;
+}
+
+// ---------------------------------------------------------------------------
+// Context
+// ---------------------------------------------------------------------------
+struct DevW {
+  float* ptr = nullptr;
+  int place = P_PLAIN;
+  int64_t host_numel = 0;
+  int64_t a = 0, b = 0, c = 0, d = 0;  // placement parameters
+};
+
+struct Ctx {
+  gs_mastr_config cfg;
+  int max_pairs = 0;
+  int gh = 0, gw = 0, N = 0;
+  Inventory inv;
+  std::map<std::string, DevW> w;
+  std::map<std::string, float*> derived;  // kv weights etc. by name
+  char* warena = nullptr;
+  size_t warena_size = 0;
+  char* arena = nullptr;
+  size_t arena_size = 0;
+  // workspaces
+  float *P, *x, *h, *qkv, *att, *mlp, *enc, *d, *ym, *kv, *q, *hook1, *hook2, *dfin;
+  float *t0, *act[4], *L[4], *u, *s, *t, *up, *rA, *rB, *hd0, *hup, *hd2, *lf;
+  float *rope_cos, *rope_sin, *ref_cos, *ref_sin;
+  int ref_maxpos = 0;
+  int last_B = 0;
+};
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+GemmArgs blank() {
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  return a;
+}
+
+GemmArgs lin(const float* A, int64_t lda, const float* W, const float* bias, float* C,
+             int64_t ldc, int64_t M, int N, int K, int flags) {
+  GemmArgs a = blank();
+  a.A = A;
+  a.lda = lda;
+  a.B = W;
+  a.ldb = K;
+  a.C = C;
+  a.ldc = ldc;
+  a.bias = bias;
+  a.M = (int32_t)M;
+  a.N = N;
+  a.K = K;
+  a.flags = flags | (bias ? EPI_BIAS : 0);
+  return a;
+}
+
+void with_rope(GemmArgs& a, const Ctx& c, int ncols) {
+  a.flags |= EPI_ROPE;
+  a.rope_cos = c.rope_cos;
+  a.rope_sin = c.rope_sin;
+  a.rope_ncols = ncols;
+  a.tok_per_img = c.N;
+  a.grid_w = c.gw;
+}
+
+int run1(const GemmArgs& a, int aload, hipStream_t s, bool relu_in = false) {
+  GemmBatch b;
+  b.g[0] = a;
+  b.ngroups = 1;
+  return launch_gemm(b, aload, B_NT, relu_in, s);
+}
+
+int run2(const GemmArgs& a0, const GemmArgs& a1, int aload, hipStream_t s) {
+  GemmBatch b;
+  b.g[0] = a0;
+  b.g[1] = a1;
+  b.ngroups = 2;
+  return launch_gemm(b, aload, B_NT, false, s);
+}
+
+#define RC(expr)              \
+  do {                        \
+    int rc_ = (expr);         \
+    if (rc_) return rc_;      \
+  } while (0)
+
+const float* W(Ctx& c, const std::string& n) {
+  auto it = c.w.find(n);
+  return it == c.w.end() ? nullptr : it->second.ptr;
+}
+
+// Linear under the context's layout mode (D1). groups > 1 splits a fused
+// weight into that many reference Linear modules for the literal layout.
+int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, float* C,
+                int64_t ldc, int64_t M, int N, int K, int flags, hipStream_t s, int groups = 1,
+                int rope_cols = 0) {
+  const float* Wt = W(c, name + ".weight");
+  const float* b = W(c, name + ".bias");
+  if (c.cfg.linear_layout == 0) {
+    GemmArgs a = lin(A, lda, Wt, b, C, ldc, M, N, K, flags);
+    if (rope_cols) with_rope(a, c, rope_cols);
+    if (flags & EPI_RES1) {
+      a.R1 = C;
+      a.ldr1 = ldc;
+    }
+    return run1(a, A_PLAIN, s);
+  }
+  const int Ng = N / groups;
+  for (int g = 0; g < groups; ++g) {
+    GemmArgs a = lin(A, lda, Wt + (int64_t)g * Ng * K, b ? b + (int64_t)g * Ng : nullptr,
+                     C + (int64_t)g * Ng, ldc, M, Ng, K, flags);
+    a.ldb = Ng;  // literal: the [Ng, K] buffer read as [K, Ng]
+    const int rc_cols = rope_cols - g * Ng;
+    if (rc_cols > 0) with_rope(a, c, rc_cols > Ng ? Ng : rc_cols);
+    if (flags & EPI_RES1) {
+      a.R1 = C + (int64_t)g * Ng;
+      a.ldr1 = ldc;
+    }
+    GemmBatch bt;
+    bt.g[0] = a;
+    bt.ngroups = 1;
+    RC(launch_gemm(bt, A_PLAIN, B_NN, false, s));
+  }
+  return 0;
+}
+
+int layernorm1(const float* x, const float* g, const float* b, float* y, int64_t rows, int D,
+               float eps, hipStream_t s) {
+  LnBatch bt;
+  bt.g[0] = LnArgs{x, g, b, y, rows, D, eps};
+  bt.ngroups = 1;
+  return launch_layernorm(bt, s);
+}
+
+AttnArgs attn_args(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
+                   int64_t ldv, float* o, int64_t ldo, int B, int H, int N) {
+  AttnArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.q_sb = (int64_t)N * ldq;
+  a.q_sh = 64;
+  a.q_sn = ldq;
+  a.k_sb = (int64_t)N * ldk;
+  a.k_sh = 64;
+  a.k_sn = ldk;
+  a.v_sb = (int64_t)N * ldv;
+  a.v_sh = 64;
+  a.v_sn = ldv;
+  a.o_sb = (int64_t)N * ldo;
+  a.o_sh = 64;
+  a.o_sn = ldo;
+  a.B = B;
+  a.H = H;
+  a.Nq = N;
+  a.Nkv = N;
+  a.scale = 1.0f / sqrtf(64.0f);
+  return a;
+}
+
+// MASt3REncoderBlockV2#forward, in place on x [M, De] (M = images * N).
+int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
+  const gs_mastr_config& f = c.cfg;
+  const int D = f.enc_dim, H = f.enc_heads;
+  const std::string p = "enc_blocks." + std::to_string(l);
+  const int rope = f.rope_mode == 1 ? 2 * D : 0;
+  RC(layernorm1(x, W(c, p + ".norm1.weight"), W(c, p + ".norm1.bias"), c.h, M, D, f.ln_eps, s));
+  RC(linear_mode(c, p + ".attn.qkv", c.h, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope));
+  AttnBatch ab;
+  ab.g[0] = attn_args(c.qkv, 3 * D, c.qkv + D, 3 * D, c.qkv + 2 * D, 3 * D, c.att, D,
+                      (int)(M / c.N), H, c.N);
+  ab.ngroups = 1;
+  RC(launch_attention(ab, s));
+  RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s));
+  RC(layernorm1(x, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias"), c.h, M, D, f.ln_eps, s));
+  RC(linear_mode(c, p + ".mlp.fc1", c.h, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D, EPI_GELU, s));
+  RC(linear_mode(c, p + ".mlp.fc2", c.mlp, f.enc_mlp, x, D, M, D, f.enc_mlp, EPI_RES1, s));
+  return 0;
+}
+
+// MASt3REncoderV2#forward over `nimg` images already unfolded in c.P.
+int encoder_from_patches(Ctx& c, int64_t nimg, float* out, hipStream_t s) {
+  const gs_mastr_config& f = c.cfg;
+  const int D = f.enc_dim, K = 3 * f.patch * f.patch;
+  const int64_t M = nimg * c.N;
+  RC(linear_mode(c, "patch_embed.proj", c.P, K, c.x, D, M, D, K, 0, s));
+  if (f.rope_mode == 2) {
+    RC(launch_rope_ref_token(c.x, c.h, (int)nimg, c.gh, c.gw, D, f.enc_heads, c.ref_cos,
+                             c.ref_sin, c.ref_maxpos, s));
+    GS_CHECK_HIP(hipMemcpyAsync(c.x, c.h, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
+  }
+  for (int l = 0; l < f.enc_depth; ++l) RC(encoder_block(c, l, c.x, M, s));
+  RC(layernorm1(c.x, W(c, "enc_norm.weight"), W(c, "enc_norm.bias"), out, M, D, f.ln_eps, s));
+  return 0;
+}
+
+// Decoder over both chains. enc [2*B*N, De] (view 1 rows first).
+int decoder(Ctx& c, int B, hipStream_t s) {
+  const gs_mastr_config& f = c.cfg;
+  const int D = f.dec_dim, H = f.dec_heads, De = f.enc_dim;
+  const int64_t Mv = (int64_t)B * c.N, M = 2 * Mv;
+  const float eps = f.ln_eps;
+  const bool rope = f.rope_mode == 1;
+  RC(run1(lin(c.enc, De, W(c, "decoder_embed.weight"), W(c, "decoder_embed.bias"), c.d, D, M, D,
+              De, 0),
+          A_PLAIN, s));
+  for (int l = 0; l < f.dec_depth; ++l) {
+    std::string p[2] = {"dec_blocks." + std::to_string(l), "dec_blocks2." + std::to_string(l)};
+    float* dc[2] = {c.d, c.d + Mv * D};
+    float* hc[2] = {c.h, c.h + Mv * D};
+    float* yc[2] = {c.ym, c.ym + Mv * D};
+    float* kvc[2] = {c.kv, c.kv + Mv * 2 * D};
+    float* qkvc[2] = {c.qkv, c.qkv + Mv * 3 * D};
+    float* qc[2] = {c.q, c.q + Mv * D};
+    float* ac[2] = {c.att, c.att + Mv * D};
+    float* mc[2] = {c.mlp, c.mlp + Mv * f.dec_mlp};
+    auto ln2 = [&](const char* nm, float* const* src, float* const* dst) {
+      LnBatch bt;
+      for (int k = 0; k < 2; ++k)
+        bt.g[k] = LnArgs{src[k], W(c, p[k] + nm + ".weight"), W(c, p[k] + nm + ".bias"), dst[k],
+                         Mv, D, eps};
+      bt.ngroups = 2;
+      return launch_layernorm(bt, s);
+    };
+    // Cross-attention memory = the other view's state before this block.
+    float* other[2] = {dc[1], dc[0]};
+    RC(ln2(".norm_y", other, yc));
+    {
+      GemmArgs a[2];
+      for (int k = 0; k < 2; ++k) {
+        a[k] = lin(yc[k], D, c.derived[p[k] + ".kv.weight"], c.derived[p[k] + ".kv.bias"], kvc[k],
+                   2 * D, Mv, 2 * D, D, 0);
+        if (rope) with_rope(a[k], c, D);
+      }
+      RC(run2(a[0], a[1], A_PLAIN, s));
+    }
+    // self-attention
+    RC(ln2(".norm1", dc, hc));
+    {
+      GemmArgs a[2];
+      for (int k = 0; k < 2; ++k) {
+        a[k] = lin(hc[k], D, W(c, p[k] + ".attn.qkv.weight"), W(c, p[k] + ".attn.qkv.bias"),
+                   qkvc[k], 3 * D, Mv, 3 * D, D, 0);
+        if (rope) with_rope(a[k], c, 2 * D);
+      }
+      RC(run2(a[0], a[1], A_PLAIN, s));
+      AttnBatch ab;
+      for (int k = 0; k < 2; ++k)
+        ab.g[k] = attn_args(qkvc[k], 3 * D, qkvc[k] + D, 3 * D, qkvc[k] + 2 * D, 3 * D, ac[k], D, B,
+                            H, c.N);
+      ab.ngroups = 2;
+      RC(launch_attention(ab, s));
+      for (int k = 0; k < 2; ++k) {
+        a[k] = lin(ac[k], D, W(c, p[k] + ".attn.proj.weight"), W(c, p[k] + ".attn.proj.bias"),
+                   dc[k], D, Mv, D, D, EPI_RES1);
+        a[k].R1 = dc[k];
+        a[k].ldr1 = D;
+      }
+      RC(run2(a[0], a[1], A_PLAIN, s));
+    }
+    // cross-attention (query norm3, reference role naming)
+    RC(ln2(".norm3", dc, hc));
+    {
+      GemmArgs a[2];
+      for (int k = 0; k < 2; ++k) {
+        a[k] = lin(hc[k], D, W(c, p[k] + ".cross_attn.projq.weight"),
+                   W(c, p[k] + ".cross_attn.projq.bias"), qc[k], D, Mv, D, D, 0);
+        if (rope) with_rope(a[k], c, D);
+      }
+      RC(run2(a[0], a[1], A_PLAIN, s));
+      AttnBatch ab;
+      for (int k = 0; k < 2; ++k)
+        ab.g[k] = attn_args(qc[k], D, kvc[k], 2 * D, kvc[k] + D, 2 * D, ac[k], D, B, H, c.N);
+      ab.ngroups = 2;
+      RC(launch_attention(ab, s));
+      for (int k = 0; k < 2; ++k) {
+        a[k] = lin(ac[k], D, W(c, p[k] + ".cross_attn.proj.weight"),
+                   W(c, p[k] + ".cross_attn.proj.bias"), dc[k], D, Mv, D, D, EPI_RES1);
+        a[k].R1 = dc[k];
+        a[k].ldr1 = D;
+      }
+      RC(run2(a[0], a[1], A_PLAIN, s));
+    }
+    // MLP (norm2, reference role naming)
+    RC(ln2(".norm2", dc, hc));
+    {
+      GemmArgs a[2];
+      for (int k = 0; k < 2; ++k)
+        a[k] = lin(hc[k], D, W(c, p[k] + ".mlp.fc1.weight"), W(c, p[k] + ".mlp.fc1.bias"), mc[k],
+                   f.dec_mlp, Mv, f.dec_mlp, D, EPI_GELU);
+      RC(run2(a[0], a[1], A_PLAIN, s));
+      for (int k = 0; k < 2; ++k) {
+        a[k] = lin(mc[k], f.dec_mlp, W(c, p[k] + ".mlp.fc2.weight"), W(c, p[k] + ".mlp.fc2.bias"),
+                   dc[k], D, Mv, D, f.dec_mlp, EPI_RES1);
+        a[k].R1 = dc[k];
+        a[k].ldr1 = D;
+      }
+      RC(run2(a[0], a[1], A_PLAIN, s));
+    }
+    if (f.dpt_hooks[1] == l + 1)
+      GS_CHECK_HIP(hipMemcpyAsync(c.hook1, c.d, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
+    if (f.dpt_hooks[2] == l + 1)
+      GS_CHECK_HIP(hipMemcpyAsync(c.hook2, c.d, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
+  }
+  RC(layernorm1(c.d, W(c, "dec_norm.weight"), W(c, "dec_norm.bias"), c.dfin, M, D, eps, s));
+  return 0;
+}
+
+// Conv as implicit GEMM on an NHWC tensor [imgs, H, W, Cin] with a context
+// weight (already OHWI for k > 1).
+int conv(Ctx& c, const std::string& name, const float* x, int imgs, int H, int W_, int Cin,
+         int Cout, int k, int stride, int pad, bool bias, float* y, int flags, bool relu_in,
+         hipStream_t s, const float* r1 = nullptr, const float* r2 = nullptr) {
+  const int Ho = (H + 2 * pad - k) / stride + 1, Wo = (W_ + 2 * pad - k) / stride + 1;
+  GemmArgs a = lin(x, Cin, W(c, name + ".weight"), bias ? W(c, name + ".bias") : nullptr, y, Cout,
+                   (int64_t)imgs * Ho * Wo, Cout, k * k * Cin, flags);
+  a.cH = H;
+  a.cW = W_;
+  a.cCin = Cin;
+  a.ck = k;
+  a.cs = stride;
+  a.cp = pad;
+  a.cHo = Ho;
+  a.cWo = Wo;
+  if (r1) {
+    a.flags |= EPI_RES1;
+    a.R1 = r1;
+    a.ldr1 = Cout;
+  }
+  if (r2) {
+    a.flags |= EPI_RES2;
+    a.R2 = r2;
+    a.ldr2 = Cout;
+  }
+  const bool pointwise = (k == 1 && stride == 1 && pad == 0);
+  return run1(a, pointwise ? A_PLAIN : A_CONV, s, relu_in);
+}
+
+// ConvTranspose (k == s) from a [rows, Cin] token tensor on the gh x gw grid.
+int convt(Ctx& c, const std::string& name, const float* x, int imgs, int Cin, int Cout, int k,
+          float* y, hipStream_t s) {
+  GemmArgs a = lin(x, Cin, c.derived[name + ".weight"], c.derived[name + ".bias"], y, 0,
+                   (int64_t)imgs * c.N, k * k * Cout, Cin, EPI_SCATTER);
+  a.sc_r = k;
+  a.sc_C = Cout;
+  a.sc_Cout = Cout;
+  a.sc_gh = c.gh;
+  a.sc_gw = c.gw;
+  return run1(a, A_PLAIN, s);
+}
+
+// FeatureFusionBlock: out = out_conv(up2(RCU2(x0 (+ RCU1(x1))))).
+int fusion(Ctx& c, const std::string& name, const float* x0, const float* x1, int B, int H,
+           int W_, float* out, hipStream_t s) {
+  const int F = c.cfg.dpt_feat;
+  const float* sum = x0;
+  if (x1) {
+    RC(conv(c, name + ".resConfUnit1.conv1", x1, B, H, W_, F, F, 3, 1, 1, true, c.u, EPI_RELU, true,
+            s));
+    RC(conv(c, name + ".resConfUnit1.conv2", c.u, B, H, W_, F, F, 3, 1, 1, true, c.s, 0, false, s,
+            x1, x0));
+    sum = c.s;
+  }
+  RC(conv(c, name + ".resConfUnit2.conv1", sum, B, H, W_, F, F, 3, 1, 1, true, c.u, EPI_RELU, true,
+          s));
+  RC(conv(c, name + ".resConfUnit2.conv2", c.u, B, H, W_, F, F, 3, 1, 1, true, c.t, 0, false, s,
+          sum));
+  RC(launch_upsample2x(c.t, B, H, W_, F, c.up, s));
+  RC(conv(c, name + ".out_conv", c.up, B, 2 * H, 2 * W_, F, F, 1, 1, 0, true, out, 0, false, s));
+  return 0;
+}
+
+// DPT head of one view: hooks are row blocks of [B*N, dim] tensors.
+int dpt_head(Ctx& c, int head, const float* e, const float* h6, const float* h9,
+             const float* dfin, int B, float* pts, float* conf, hipStream_t s) {
+  const gs_mastr_config& f = c.cfg;
+  const int F = f.dpt_feat, gh = c.gh, gw = c.gw;
+  const std::string p = "downstream_head" + std::to_string(head);
+  const std::string ap = p + ".dpt.act_postprocess.";
+  const int* d = f.dpt_dims;
+  // act_postprocess
+  RC(conv(c, ap + "0.0", e, B, gh, gw, f.enc_dim, d[0], 1, 1, 0, true, c.t0, 0, false, s));
+  RC(convt(c, ap + "0.1", c.t0, B, d[0], d[0], 4, c.act[0], s));
+  RC(conv(c, ap + "1.0", h6, B, gh, gw, f.dec_dim, d[1], 1, 1, 0, true, c.t0, 0, false, s));
+  RC(convt(c, ap + "1.1", c.t0, B, d[1], d[1], 2, c.act[1], s));
+  RC(conv(c, ap + "2.0", h9, B, gh, gw, f.dec_dim, d[2], 1, 1, 0, true, c.act[2], 0, false, s));
+  RC(conv(c, ap + "3.0", dfin, B, gh, gw, f.dec_dim, d[3], 1, 1, 0, true, c.t0, 0, false, s));
+  RC(conv(c, ap + "3.1", c.t0, B, gh, gw, d[3], d[3], 3, 2, 1, true, c.act[3], 0, false, s));
+  const int ah[4] = {4 * gh, 2 * gh, gh, gh / 2}, aw[4] = {4 * gw, 2 * gw, gw, gw / 2};
+  for (int i = 0; i < 4; ++i)
+    RC(conv(c, p + ".dpt.scratch.layer" + std::to_string(i + 1) + "_rn", c.act[i], B, ah[i], aw[i],
+            d[i], F, 3, 1, 1, false, c.L[i], 0, false, s));
+  const std::string rp = p + ".dpt.scratch.refinenet";
+  RC(fusion(c, rp + "4", c.L[3], nullptr, B, ah[3], aw[3], c.rA, s));
+  RC(fusion(c, rp + "3", c.rA, c.L[2], B, ah[2], aw[2], c.rB, s));
+  RC(fusion(c, rp + "2", c.rB, c.L[1], B, ah[1], aw[1], c.rA, s));
+  RC(fusion(c, rp + "1", c.rA, c.L[0], B, ah[0], aw[0], c.rB, s));
+  const int h1 = 2 * ah[0], w1 = 2 * aw[0];
+  RC(conv(c, p + ".dpt.head.0", c.rB, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s));
+  RC(launch_upsample2x(c.hd0, B, h1, w1, F / 2, c.hup, s));
+  RC(conv(c, p + ".dpt.head.2", c.hup, B, 2 * h1, 2 * w1, F / 2, f.head_mid, 3, 1, 1, true, c.hd2,
+          EPI_RELU, false, s));
+  RC(launch_head_out(c.hd2, (int64_t)B * 4 * h1 * w1, f.head_mid, W(c, p + ".dpt.head.4.weight"),
+                     W(c, p + ".dpt.head.4.bias"), pts, conf, s));
+  return 0;
+}
+
+// Local-feature descriptors of one view: MLP(concat(enc, dec)) + shuffle.
+int local_features(Ctx& c, int head, const float* e, const float* dfin, int B, float* desc,
+                   hipStream_t s) {
+  const gs_mastr_config& f = c.cfg;
+  const std::string p = "downstream_head" + std::to_string(head) + ".head_local_features";
+  const int Din = f.enc_dim + f.dec_dim;
+  const int64_t Mv = (int64_t)B * c.N;
+  GemmArgs a = lin(e, f.enc_dim, W(c, p + ".fc1.weight"), W(c, p + ".fc1.bias"), c.lf, f.lf_hidden,
+                   Mv, f.lf_hidden, Din, EPI_GELU);
+  a.A2 = dfin;
+  a.lda2 = f.dec_dim;
+  a.K1 = f.enc_dim;
+  RC(run1(a, A_CONCAT, s));
+  const int r = f.patch;
+  GemmArgs b = lin(c.lf, f.lf_hidden, c.derived[p + ".fc2.weight"], c.derived[p + ".fc2.bias"],
+                   desc, 0, Mv, r * r * f.desc_dim, f.lf_hidden, EPI_SCATTER);
+  b.sc_r = r;
+  b.sc_C = f.desc_dim;
+  b.sc_Cout = f.desc_dim;
+  b.sc_gh = c.gh;
+  b.sc_gw = c.gw;
+  return run1(b, A_PLAIN, s);
+}
+
+// ---------------------------------------------------------------------------
+// Weight placement
+// ---------------------------------------------------------------------------
+int place_weight(Ctx& c, const std::string& name, const float* host, int64_t n) {
+  auto it = c.w.find(name);
+  GS_REQUIRE(it != c.w.end(), "set_weight: unknown weight " + name);
+  DevW& dw = it->second;
+  GS_REQUIRE(n == dw.host_numel, "set_weight: numel mismatch for " + name);
+  std::vector<float> tmp;
+  const float* src = host;
+  int64_t count = n;
+  float* dst = dw.ptr;
+  switch (dw.place) {
+    case P_PLAIN:
+      break;
+    case P_CONV: {  // a = Cout, b = Cin, c = k
+      const int64_t Co = dw.a, Ci = dw.b, k = dw.c;
+      tmp.resize(n);
+      for (int64_t oc = 0; oc < Co; ++oc)
+        for (int64_t ic = 0; ic < Ci; ++ic)
+          for (int64_t kh = 0; kh < k; ++kh)
+            for (int64_t kw = 0; kw < k; ++kw)
+              tmp[((oc * k + kh) * k + kw) * Ci + ic] = host[((oc * Ci + ic) * k + kh) * k + kw];
+      src = tmp.data();
+      break;
+    }
+    case P_CONVT_W: {  // a = Cin, b = Cout, c = k
+      const int64_t Ci = dw.a, Co = dw.b, k = dw.c;
+      tmp.resize(n);
+      for (int64_t ic = 0; ic < Ci; ++ic)
+        for (int64_t oc = 0; oc < Co; ++oc)
+          for (int64_t i = 0; i < k; ++i)
+            for (int64_t j = 0; j < k; ++j)
+              tmp[((i * k + j) * Co + oc) * Ci + ic] = host[((ic * Co + oc) * k + i) * k + j];
+      src = tmp.data();
+      break;
+    }
+    case P_CONVT_B: {  // a = Cout, c = k
+      const int64_t Co = dw.a, k = dw.c;
+      tmp.resize(k * k * Co);
+      for (int64_t s = 0; s < k * k; ++s)
+        for (int64_t oc = 0; oc < Co; ++oc) tmp[s * Co + oc] = host[oc];
+      src = tmp.data();
+      count = (int64_t)tmp.size();
+      break;
+    }
+    case P_KV:  // a = element offset within the concatenated buffer
+      dst = dw.ptr + dw.a;
+      break;
+    case P_DESC_W:    // a = r (patch), b = desc channels, c = K
+    case P_DESC_B: {  // rows c*r*r + s (s = i*r + j) -> s*desc + c, c < desc
+      const int64_t r2 = dw.a * dw.a, C = dw.b, K = dw.place == P_DESC_W ? dw.c : 1;
+      tmp.resize(r2 * C * K);
+      for (int64_t s = 0; s < r2; ++s)
+        for (int64_t ch = 0; ch < C; ++ch)
+          memcpy(&tmp[(s * C + ch) * K], host + (ch * r2 + s) * K, K * sizeof(float));
+      src = tmp.data();
+      count = (int64_t)tmp.size();
+      break;
+    }
+  }
+  GS_CHECK_HIP(hipMemcpy(dst, src, count * sizeof(float), hipMemcpyHostToDevice));
+  return 0;
+}
+
+int build_weights(Ctx& c) {
+  const gs_mastr_config& f = c.cfg;
+  // sizes: placed tensors + derived buffers
+  size_t total = 0;
+  std::vector<std::pair<std::string, int64_t>> derived_sizes;
+  for (int chain = 0; chain < 2; ++chain)
+    for (int l = 0; l < f.dec_depth; ++l) {
+      const std::string p = (chain ? "dec_blocks2." : "dec_blocks.") + std::to_string(l);
+      derived_sizes.push_back({p + ".kv.weight", (int64_t)2 * f.dec_dim * f.dec_dim});
+      derived_sizes.push_back({p + ".kv.bias", (int64_t)2 * f.dec_dim});
+    }
+  for (int hd = 1; hd <= 2; ++hd) {
+    const std::string p = "downstream_head" + std::to_string(hd);
+    const int64_t r2 = (int64_t)f.patch * f.patch;
+    derived_sizes.push_back({p + ".head_local_features.fc2.weight", r2 * f.desc_dim * f.lf_hidden});
+    derived_sizes.push_back({p + ".head_local_features.fc2.bias", r2 * f.desc_dim});
+    for (int i = 0; i < 2; ++i) {
+      const int64_t d = f.dpt_dims[i], k = i == 0 ? 4 : 2;
+      const std::string n = p + ".dpt.act_postprocess." + std::to_string(i) + ".1";
+      derived_sizes.push_back({n + ".weight", k * k * d * d});
+      derived_sizes.push_back({n + ".bias", k * k * d});
+    }
+  }
+  for (auto& wi : c.inv.w) total += align256(numel(wi) * sizeof(float));
+  for (auto& ds : derived_sizes) total += align256(ds.second * sizeof(float));
+  GS_CHECK_HIP(hipMalloc(&c.warena, total));
+  c.warena_size = total;
+  char* cur = c.warena;
+  auto take = [&](int64_t nfl) {
+    float* p = (float*)cur;
+    cur += align256(nfl * sizeof(float));
+    return p;
+  };
+  for (auto& ds : derived_sizes) c.derived[ds.first] = take(ds.second);
+  for (auto& wi : c.inv.w) {
+    DevW dw;
+    dw.host_numel = numel(wi);
+    const std::string& n = wi.name;
+    auto ends = [&](const std::string& suf) {
+      return n.size() >= suf.size() && n.compare(n.size() - suf.size(), suf.size(), suf) == 0;
+    };
+    const bool is_kv = n.find(".cross_attn.projk.") != std::string::npos ||
+                       n.find(".cross_attn.projv.") != std::string::npos;
+    const bool is_desc = n.find(".head_local_features.fc2.") != std::string::npos;
+    const bool is_convt = n.find(".act_postprocess.0.1.") != std::string::npos ||
+                          n.find(".act_postprocess.1.1.") != std::string::npos;
+    if (is_kv) {
+      const bool is_v = n.find(".projv.") != std::string::npos;
+      const std::string blk = n.substr(0, n.find(".cross_attn."));
+      const bool w = ends(".weight");
+      dw.ptr = c.derived[blk + (w ? ".kv.weight" : ".kv.bias")];
+      dw.place = P_KV;
+      dw.a = is_v ? dw.host_numel : 0;
+      // also register the plain name so W() finds projk / projv directly
+      c.w[n] = dw;
+      continue;
+    }
+    if (is_desc) {
+      const bool w = ends(".weight");
+      dw.ptr = c.derived[n];
+      dw.place = w ? P_DESC_W : P_DESC_B;
+      dw.a = f.patch;
+      dw.b = f.desc_dim;
+      dw.c = f.lf_hidden;
+      c.w[n] = dw;
+      continue;
+    }
+    if (is_convt) {
+      const bool w = ends(".weight");
+      dw.ptr = c.derived[n];
+      dw.place = w ? P_CONVT_W : P_CONVT_B;
+      dw.a = wi.shape[0];
+      dw.b = w ? wi.shape[1] : 0;
+      dw.c = n.find(".0.1.") != std::string::npos ? 4 : 2;
+      if (!w) dw.a = wi.shape[0];
+      c.w[n] = dw;
+      continue;
+    }
+    dw.ptr = take(dw.host_numel);
+    if (wi.shape[3] > 1 && n != "patch_embed.proj.weight") {
+      dw.place = P_CONV;
+      dw.a = wi.shape[0];
+      dw.b = wi.shape[1];
+      dw.c = wi.shape[2];
+    }
+    c.w[n] = dw;
+  }
+  return 0;
+}
+
+int build_workspace(Ctx& c) {
+  const gs_mastr_config& f = c.cfg;
+  const int64_t B = c.max_pairs, N = c.N;
+  const int64_t M = 2 * B * N;  // both views' tokens
+  const int64_t De = f.enc_dim, Dd = f.dec_dim, F = f.dpt_feat;
+  const int64_t dmax = std::max(std::max(f.dpt_dims[0], f.dpt_dims[1]),
+                                std::max(f.dpt_dims[2], f.dpt_dims[3]));
+  const int64_t Dm = std::max(De, Dd);
+  std::vector<std::pair<float**, int64_t>> req = {
+      {&c.P, M * 3 * f.patch * f.patch},
+      {&c.x, M * De},
+      {&c.h, M * Dm},
+      {&c.qkv, M * 3 * Dm},
+      {&c.att, M * Dm},
+      {&c.mlp, M * std::max(f.enc_mlp, f.dec_mlp)},
+      {&c.enc, M * De},
+      {&c.d, M * Dd},
+      {&c.ym, M * Dd},
+      {&c.kv, M * 2 * Dd},
+      {&c.q, M * Dd},
+      {&c.hook1, M * Dd},
+      {&c.hook2, M * Dd},
+      {&c.dfin, M * Dd},
+      // DPT (one head at a time, B images)
+      {&c.t0, B * N * dmax},
+      {&c.act[0], B * 16 * N * f.dpt_dims[0]},
+      {&c.act[1], B * 4 * N * f.dpt_dims[1]},
+      {&c.act[2], B * N * f.dpt_dims[2]},
+      {&c.act[3], B * N / 4 * f.dpt_dims[3]},
+      {&c.L[0], B * 16 * N * F},
+      {&c.L[1], B * 4 * N * F},
+      {&c.L[2], B * N * F},
+      {&c.L[3], B * N / 4 * F},
+      {&c.u, B * 16 * N * F},
+      {&c.s, B * 16 * N * F},
+      {&c.t, B * 16 * N * F},
+      {&c.up, B * 64 * N * F},
+      {&c.rA, B * 64 * N * F},
+      {&c.rB, B * 64 * N * F},
+      {&c.hd0, B * 64 * N * (F / 2)},
+      {&c.hup, B * 256 * N * (F / 2)},
+      {&c.hd2, B * 256 * N * f.head_mid},
+      {&c.lf, B * N * f.lf_hidden},
+      {&c.rope_cos, 512 * 16},
+      {&c.rope_sin, 512 * 16},
+      {&c.ref_cos, 512 * (De / f.enc_heads / 2)},
+      {&c.ref_sin, 512 * (De / f.enc_heads / 2)},
+  };
+  size_t total = 0;
+  for (auto& r : req) total += align256(r.second * sizeof(float));
+  GS_CHECK_HIP(hipMalloc(&c.arena, total));
+  c.arena_size = total;
+  char* cur = c.arena;
+  for (auto& r : req) {
+    *r.first = (float*)cur;
+    cur += align256(r.second * sizeof(float));
+  }
+  std::vector<float> hc(512 * 16), hs(512 * 16);
+  rope_table_host(512, f.rope_base, hc.data(), hs.data());
+  GS_CHECK_HIP(hipMemcpy(c.rope_cos, hc.data(), hc.size() * 4, hipMemcpyHostToDevice));
+  GS_CHECK_HIP(hipMemcpy(c.rope_sin, hs.data(), hs.size() * 4, hipMemcpyHostToDevice));
+  const int hd = f.enc_dim / f.enc_heads;
+  c.ref_maxpos = 512;
+  std::vector<float> rc(512 * (hd / 2)), rs(512 * (hd / 2));
+  rope_ref_table_host(512, hd, f.rope_base, rc.data(), rs.data());
+  GS_CHECK_HIP(hipMemcpy(c.ref_cos, rc.data(), rc.size() * 4, hipMemcpyHostToDevice));
+  GS_CHECK_HIP(hipMemcpy(c.ref_sin, rs.data(), rs.size() * 4, hipMemcpyHostToDevice));
+  return 0;
+}
+
+int validate_config(const gs_mastr_config& f) {
+  GS_REQUIRE(f.patch > 0 && f.patch % 4 == 0 && f.img_h % f.patch == 0 && f.img_w % f.patch == 0,
+             "config: image must be a multiple of the patch size (patch % 4 == 0)");
+  const int gh = f.img_h / f.patch, gw = f.img_w / f.patch;
+  GS_REQUIRE(gh % 2 == 0 && gw % 2 == 0 && gh <= 512 && gw <= 512, "config: patch grid must be even");
+  GS_REQUIRE(f.enc_heads > 0 && f.enc_dim == 64 * f.enc_heads, "config: encoder head dim must be 64");
+  GS_REQUIRE(f.dec_heads > 0 && f.dec_dim == 64 * f.dec_heads, "config: decoder head dim must be 64");
+  GS_REQUIRE(f.enc_mlp % 32 == 0 && f.dec_mlp % 32 == 0 && f.lf_hidden % 32 == 0,
+             "config: hidden sizes must be multiples of 32");
+  GS_REQUIRE(f.dpt_feat % 64 == 0 && f.head_mid % 32 == 0, "config: DPT widths must be multiples of 64/32");
+  for (int i = 0; i < 4; ++i) GS_REQUIRE(f.dpt_dims[i] % 32 == 0, "config: DPT dims must be multiples of 32");
+  GS_REQUIRE(f.dpt_hooks[0] == 0 && f.dpt_hooks[3] == f.dec_depth && f.dpt_hooks[1] >= 1 &&
+                 f.dpt_hooks[1] <= f.dec_depth && f.dpt_hooks[2] >= 1 && f.dpt_hooks[2] <= f.dec_depth,
+             "config: hooks must be {0, a, b, dec_depth}");
+  GS_REQUIRE(f.desc_dim > 0 && (f.patch * f.patch * f.desc_dim) % 32 == 0, "config: bad desc_dim");
+  GS_REQUIRE(f.linear_layout == 0 || f.linear_layout == 1, "config: linear_layout must be 0 or 1");
+  GS_REQUIRE(f.rope_mode >= 0 && f.rope_mode <= 2, "config: rope_mode must be 0, 1 or 2");
+  GS_REQUIRE(f.enc_dim % 32 == 0 && f.dec_dim % 32 == 0, "config: dims must be multiples of 32");
+  return 0;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+void gs_mastr_default_config(gs_mastr_config* c) {
+  memset(c, 0, sizeof(*c));
+  c->img_h = 384;
+  c->img_w = 512;
+  c->patch = 16;
+  c->enc_dim = 1024;
+  c->enc_depth = 24;
+  c->enc_heads = 16;
+  c->enc_mlp = 4096;
+  c->dec_dim = 768;
+  c->dec_depth = 12;
+  c->dec_heads = 12;
+  c->dec_mlp = 3072;
+  c->dpt_feat = 256;
+  c->dpt_dims[0] = 96;
+  c->dpt_dims[1] = 192;
+  c->dpt_dims[2] = 384;
+  c->dpt_dims[3] = 768;
+  c->dpt_hooks[0] = 0;
+  c->dpt_hooks[1] = 6;
+  c->dpt_hooks[2] = 9;
+  c->dpt_hooks[3] = 12;
+  c->head_mid = 128;
+  c->lf_hidden = 7168;
+  c->desc_dim = 24;
+  c->ln_eps = 1e-6f;
+  c->rope_base = 100.0f;
+  c->linear_layout = 0;
+  c->rope_mode = 1;
+}
+
+int32_t gs_mastr_weight_count(const gs_mastr_config* cfg) {
+  return (int32_t)make_inventory(*cfg).w.size();
+}
+
+int32_t gs_mastr_weight_info(const gs_mastr_config* cfg, int32_t i, char* name_out,
+                             int32_t name_cap, int64_t shape_out[4], int32_t* kind_out) {
+  Inventory inv = make_inventory(*cfg);
+  if (i < 0 || i >= (int32_t)inv.w.size()) return -1;
+  const WInfo& w = inv.w[i];
+  if (name_out && name_cap > 0) {
+    strncpy(name_out, w.name.c_str(), name_cap - 1);
+    name_out[name_cap - 1] = 0;
+  }
+  if (shape_out)
+    for (int k = 0; k < 4; ++k) shape_out[k] = w.shape[k];
+  if (kind_out) *kind_out = w.kind;
+  return 0;
+}
+
+static void weight_values(const WInfo& w, uint64_t seed, float bias_std, float ln_std, float* out,
+                          int64_t n) {
+  switch (w.kind) {
+    case W_WEIGHT:
+      gs_seed_normal(seed, w.name.c_str(), 0.0f, 0.02f, out, n);
+      break;
+    case W_BIAS:
+      if (bias_std > 0) gs_seed_normal(seed, w.name.c_str(), 0.0f, bias_std, out, n);
+      else memset(out, 0, n * sizeof(float));
+      break;
+    case W_GAMMA:
+      if (ln_std > 0) gs_seed_normal(seed, w.name.c_str(), 1.0f, ln_std, out, n);
+      else
+        for (int64_t i = 0; i < n; ++i) out[i] = 1.0f;
+      break;
+    default:
+      if (ln_std > 0) gs_seed_normal(seed, w.name.c_str(), 0.0f, ln_std, out, n);
+      else memset(out, 0, n * sizeof(float));
+  }
+}
+
+int32_t gs_mastr_weight_values(const gs_mastr_config* cfg, int32_t i, uint64_t seed,
+                               float bias_std, float ln_std, float* out, int64_t n) {
+  Inventory inv = make_inventory(*cfg);
+  GS_REQUIRE(i >= 0 && i < (int32_t)inv.w.size(), "weight_values: index out of range");
+  GS_REQUIRE(n == numel(inv.w[i]), "weight_values: numel mismatch");
+  weight_values(inv.w[i], seed, bias_std, ln_std, out, n);
+  return 0;
+}
+
+int32_t gs_hip_mastr_create(const gs_mastr_config* cfg, int32_t max_pairs, void** ctx_out) {
+  GS_REQUIRE(cfg && ctx_out && max_pairs > 0, "mastr_create: bad arguments");
+  int rc = validate_config(*cfg);
+  if (rc) return rc;
+  if (ensure_device()) return -2;
+  Ctx* c = new Ctx();
+  c->cfg = *cfg;
+  c->max_pairs = max_pairs;
+  c->gh = cfg->img_h / cfg->patch;
+  c->gw = cfg->img_w / cfg->patch;
+  c->N = c->gh * c->gw;
+  c->inv = make_inventory(*cfg);
+  rc = build_weights(*c);
+  if (!rc) rc = build_workspace(*c);
+  if (rc) {
+    gs_hip_mastr_destroy(c);
+    return rc;
+  }
+  *ctx_out = c;
+  return 0;
+}
+
+void gs_hip_mastr_destroy(void* ctx) {
+  if (!ctx) return;
+  Ctx* c = (Ctx*)ctx;
+  hipDeviceSynchronize();
+  if (c->warena) hipFree(c->warena);
+  if (c->arena) hipFree(c->arena);
+  delete c;
+}
+
+int32_t gs_hip_mastr_init_seeded(void* ctx, uint64_t seed, float bias_std, float ln_std) {
+  GS_REQUIRE(ctx, "init_seeded: null context");
+  Ctx* c = (Ctx*)ctx;
+  std::vector<float> buf;
+  for (auto& wi : c->inv.w) {
+    const int64_t n = numel(wi);
+    buf.resize(n);
+    weight_values(wi, seed, bias_std, ln_std, buf.data(), n);
+    int rc = place_weight(*c, wi.name, buf.data(), n);
+    if (rc) return rc;
+  }
+  return 0;
+}
+
+int32_t gs_hip_mastr_set_weight(void* ctx, const char* name, const float* host, int64_t numel_) {
+  GS_REQUIRE(ctx && name && host, "set_weight: null argument");
+  return place_weight(*(Ctx*)ctx, name, host, numel_);
+}
+
+int32_t gs_hip_mastr_encoder_block(void* ctx, int32_t layer, float* x, int32_t B, void* stream) {
+  GS_REQUIRE(ctx && x, "encoder_block: null argument");
+  Ctx* c = (Ctx*)ctx;
+  GS_REQUIRE(layer >= 0 && layer < c->cfg.enc_depth, "encoder_block: layer out of range");
+  GS_REQUIRE(B > 0 && B <= 2 * c->max_pairs, "encoder_block: B exceeds context capacity");
+  hipStream_t s = stream ? (hipStream_t)stream : default_stream();
+  return encoder_block(*c, layer, x, (int64_t)B * c->N, s);
+}
+
+int32_t gs_hip_mastr_encoder(void* ctx, const float* img, int32_t B, float* enc, void* stream) {
+  GS_REQUIRE(ctx && img && enc, "encoder: null argument");
+  Ctx* c = (Ctx*)ctx;
+  GS_REQUIRE(B > 0 && B <= 2 * c->max_pairs, "encoder: B exceeds context capacity");
+  hipStream_t s = stream ? (hipStream_t)stream : default_stream();
+  RC(launch_unfold(img, B, c->cfg.img_h, c->cfg.img_w, c->cfg.patch, c->P, s));
+  return encoder_from_patches(*c, B, enc, s);
+}
+
+int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2, int32_t B, float* pts1,
+                          float* conf1, float* desc1, float* pts2, float* conf2, float* desc2,
+                          void* stream) {
+  GS_REQUIRE(ctx && img1 && img2, "pair: null image");
+  Ctx* c = (Ctx*)ctx;
+  GS_REQUIRE(B > 0 && B <= c->max_pairs, "pair: B exceeds context capacity");
+  GS_REQUIRE(c->cfg.linear_layout == 0, "pair: the literal linear layout is encoder-only");
+  GS_REQUIRE(!pts1 == !conf1 && !pts2 == !conf2, "pair: pts and conf must be given together");
+  hipStream_t s = stream ? (hipStream_t)stream : default_stream();
+  const gs_mastr_config& f = c->cfg;
+  const int64_t Mv = (int64_t)B * c->N;
+  const int64_t K = 3 * f.patch * f.patch;
+  RC(launch_unfold(img1, B, f.img_h, f.img_w, f.patch, c->P, s));
+  RC(launch_unfold(img2, B, f.img_h, f.img_w, f.patch, c->P + Mv * K, s));
+  RC(encoder_from_patches(*c, 2 * B, c->enc, s));
+  RC(decoder(*c, B, s));
+  c->last_B = B;
+  const float* e[2] = {c->enc, c->enc + Mv * f.enc_dim};
+  const float* h6[2] = {c->hook1, c->hook1 + Mv * f.dec_dim};
+  const float* h9[2] = {c->hook2, c->hook2 + Mv * f.dec_dim};
+  const float* df[2] = {c->dfin, c->dfin + Mv * f.dec_dim};
+  float* pts[2] = {pts1, pts2};
+  float* conf[2] = {conf1, conf2};
+  float* desc[2] = {desc1, desc2};
+  for (int v = 0; v < 2; ++v) {
+    if (pts[v]) RC(dpt_head(*c, v + 1, e[v], h6[v], h9[v], df[v], B, pts[v], conf[v], s));
+    if (desc[v]) RC(local_features(*c, v + 1, e[v], df[v], B, desc[v], s));
+  }
+  return 0;
+}
+
+int32_t gs_hip_mastr_pair_taps(void* ctx, int32_t B, float* enc1, float* enc2, float* dec1,
+                               float* dec2, void* stream) {
+  GS_REQUIRE(ctx, "pair_taps: null context");
+  Ctx* c = (Ctx*)ctx;
+  GS_REQUIRE(B > 0 && B <= c->last_B, "pair_taps: B exceeds the last pair call");
+  hipStream_t s = stream ? (hipStream_t)stream : default_stream();
+  const int64_t Mv = (int64_t)c->last_B * c->N;
+  const int64_t ne = (int64_t)B * c->N * c->cfg.enc_dim, nd = (int64_t)B * c->N * c->cfg.dec_dim;
+  if (enc1) GS_CHECK_HIP(hipMemcpyAsync(enc1, c->enc, ne * 4, hipMemcpyDeviceToDevice, s));
+  if (enc2)
+    GS_CHECK_HIP(hipMemcpyAsync(enc2, c->enc + Mv * c->cfg.enc_dim, ne * 4, hipMemcpyDeviceToDevice, s));
+  if (dec1) GS_CHECK_HIP(hipMemcpyAsync(dec1, c->dfin, nd * 4, hipMemcpyDeviceToDevice, s));
+  if (dec2)
+    GS_CHECK_HIP(hipMemcpyAsync(dec2, c->dfin + Mv * c->cfg.dec_dim, nd * 4, hipMemcpyDeviceToDevice, s));
+  return 0;
+}
+
+}  // extern "C"

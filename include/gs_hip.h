@@ -1,0 +1,252 @@
+/*
+ * gs_hip.h -- C ABI of libgsplat_hip.so, the MI355X (gfx950) backend that
+ * replaces crystal-gausplat's Metal bridge for the MASt3R inference path.
+ *
+ * Three groups of entry points:
+ *
+ *  1. Kept gs_* buffer/device symbols, same C signatures as the Metal bridge
+ *     exports (src/metal/bridge.mm:362-482), declared on the Crystal side in
+ *     `lib MetalFFI` (src/core/buffer.cr:214-222) and `lib MetalDeviceFFI`
+ *     (src/metal/device.cr:206-251). Buffers are explicit device allocations;
+ *     gs_buffer_contents returns a DEVICE pointer (not host-dereferenceable).
+ *     The pipeline / command-buffer / encoder symbols of the bridge
+ *     (gs_create_pipeline*, gs_create_command_buffer, gs_commit*,
+ *     gs_create_compute_encoder, gs_encoder_*) have no counterpart: kernels are
+ *     precompiled for gfx950 and are reached through the op-level entry points.
+ *
+ *  2. Op-level entry points: one per NN::GPUOps operation on the path
+ *     (src/nn/gpu_ops.cr), plus the operations the reference runs on the CPU
+ *     between GPU calls (RoPE, resampling, head split).
+ *
+ *  3. Graph-level entry points: a MASt3R context holding device weights and
+ *     workspaces, running whole encoder / pair forwards as one launch
+ *     sequence on a stream (MASt3RInference#forward_pair,
+ *     src/mastr/inference.cr:92-115).
+ *
+ * Conventions (new): every gs_hip_* call returns int32 status, 0 = ok, < 0 =
+ * error, with gs_hip_last_error() describing the last failure of the calling
+ * thread. Pointers passed to gs_hip_* compute calls are device pointers
+ * (hipMalloc'd or gs_buffer_contents) unless named host_*. `stream` is a
+ * hipStream_t; NULL means the library's own stream (the one
+ * gs_get_command_queue returns). All compute calls are asynchronous on that
+ * stream. All tensors are fp32, row-major, contiguous unless strides are given.
+ */
+#ifndef GS_HIP_H
+#define GS_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ------------------------------------------------------------------------ */
+/* 1. Kept buffer / device symbols                                           */
+/* ------------------------------------------------------------------------ */
+
+/* src/metal/bridge.mm:363 (gs_create_buffer). storage_mode is accepted and
+ * ignored: every buffer is device memory. Returns NULL on failure. */
+void* gs_create_buffer(int64_t size, int32_t storage_mode);
+/* src/metal/bridge.mm:367. Synchronises the library stream, then frees. */
+void gs_release_buffer(void* handle);
+/* src/metal/bridge.mm:371. Device pointer of the buffer. */
+void* gs_buffer_contents(void* handle);
+/* src/metal/bridge.mm:375 / 379. Host <-> device copy, synchronous. */
+void gs_buffer_write(void* handle, void* data, int64_t size);
+void gs_buffer_read(void* handle, void* dest, int64_t size);
+/* src/metal/bridge.mm:383. No-op (no managed storage). */
+void gs_buffer_sync(void* handle);
+/* src/metal/bridge.mm:387. Device-to-device copy on the library stream. */
+void gs_buffer_copy(void* src_handle, void* dst_handle, int64_t size);
+
+/* src/metal/bridge.mm:392. 0 = ok, -1 = no device, -2 = stream failure. */
+int32_t gs_init_device(void);
+/* src/metal/bridge.mm:396 / 400. Opaque device handle / the hipStream_t. */
+void* gs_get_device(void);
+void* gs_get_command_queue(void);
+/* src/metal/bridge.mm:404. hipStreamSynchronize on the library stream. */
+void gs_synchronize(void);
+/* src/metal/bridge.mm:408-422. */
+const char* gs_device_name(void);
+int32_t gs_max_threads_per_threadgroup(void);
+int64_t gs_recommended_working_set_size(void);
+int32_t gs_has_unified_memory(void);
+
+/* ------------------------------------------------------------------------ */
+/* Errors                                                                    */
+/* ------------------------------------------------------------------------ */
+const char* gs_hip_last_error(void);
+
+/* ------------------------------------------------------------------------ */
+/* Seeded synthetic data (host side, shared by tests and the context)        */
+/* ------------------------------------------------------------------------ */
+/* SplitMix64 stream keyed by (seed, FNV-1a(name)); normal by Box-Muller from
+ * 24-bit uniforms; values rounded to fp32. Deterministic across hosts. */
+void gs_seed_normal(uint64_t seed, const char* name, float mean, float std,
+                    float* host_out, int64_t n);
+void gs_seed_uniform(uint64_t seed, const char* name, float lo, float hi,
+                     float* host_out, int64_t n);
+
+/* ------------------------------------------------------------------------ */
+/* 2. Op-level entry points                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* Epilogue flags for gs_hip_linear. */
+#define GS_EPI_GELU 1     /* y = gelu_tanh(x.W + b)                          */
+#define GS_EPI_RESIDUAL 2 /* y = residual + (x.W + b)                        */
+#define GS_EPI_RELU 4     /* y = max(x.W + b, 0)                             */
+
+/* NN::GPUOps.linear_forward (src/nn/gpu_ops.cr:39-78) plus the bias add the
+ * reference does on the CPU (src/nn/linear.cr:206-230).
+ * y[M,N] = x[M,K] . W (+ b) with the epilogue above.
+ * w_layout 0: W is [N,K] (y = x W^T, the GPU path's semantics);
+ * w_layout 1: W buffer read as [K,N] (the reference CPU path's literal
+ * indexing, src/nn/linear.cr:194). K must be a multiple of 32. b, residual
+ * nullable. residual may alias y. */
+int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y,
+                      int64_t M, int32_t K, int32_t N, int32_t w_layout,
+                      int32_t epilogue, const float* residual, void* stream);
+
+/* NN::GPUOps.layernorm_forward (src/nn/gpu_ops.cr:114-138), the arithmetic of
+ * LayerNorm#forward_cpu (src/nn/layernorm.cr:192-240). D <= 4096, D % 4 == 0. */
+int32_t gs_hip_layernorm(const float* x, const float* gamma, const float* beta,
+                         float* y, int64_t rows, int32_t D, float eps,
+                         void* stream);
+
+/* NN::GPUOps.fused_attention (src/nn/gpu_ops.cr:200-227) generalised to
+ * cross-attention with Nq != Nkv (the CPU path's semantics,
+ * src/nn/attention.cr:215-325). head_dim must be 64. Element (b,h,n,d) of q
+ * is at q[b*q_sb + h*q_sh + n*q_sn + d]; likewise for k, v, o. The
+ * reference layout [B,H,N,64] is q_sb = H*N*64, q_sh = N*64, q_sn = 64;
+ * token-major [B,N,H*64] is q_sb = N*H*64, q_sh = 64, q_sn = H*64. */
+int32_t gs_hip_attention(const float* q, const float* k, const float* v,
+                         float* o, int32_t B, int32_t H, int32_t Nq,
+                         int32_t Nkv, int32_t head_dim, float scale,
+                         int64_t q_sb, int64_t q_sh, int64_t q_sn,
+                         int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                         int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                         int64_t o_sb, int64_t o_sh, int64_t o_sn,
+                         void* stream);
+
+/* 2D RoPE in place on t [B, N, ld], columns [0, H*64): per 64-wide head,
+ * dims [0,32) rotate by the token's row y and [32,64) by its column x
+ * (token n at (n / grid_w, n % grid_w)); within each 32-dim half, pairs
+ * (j, j+16) rotate by pos * base^(-2j/32). Replaces the token-level CPU pass
+ * MASt3REncoderV2#apply_rope (src/mastr/encoder_v2.cr:180-258). */
+int32_t gs_hip_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld,
+                      int32_t grid_w, float base, void* stream);
+
+/* NN::GPUOps.conv2d_forward (src/nn/gpu_ops.cr:478-527); the arithmetic of
+ * Conv2DBlock#forward_cpu (src/mastr/decoder_v2.cr:281-344). x NHWC
+ * [B,H,W,Cin], w OIHW [Cout,Cin,k,k] (w_layout 0) or OHWI [Cout,k,k,Cin]
+ * (w_layout 1), y NHWC. Cin must be a multiple of 32 for k > 1 (any multiple
+ * of 32 for k == 1). flags: GS_CONV_RELU_IN applies ReLU to x on load,
+ * GS_CONV_RELU_OUT after the bias, residual (nullable) is added last. */
+#define GS_CONV_RELU_IN 1
+#define GS_CONV_RELU_OUT 2
+int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W,
+                      int32_t Cin, const float* w, const float* b, float* y,
+                      int32_t Cout, int32_t k, int32_t stride, int32_t pad,
+                      int32_t w_layout, int32_t flags, const float* residual,
+                      void* stream);
+
+/* ConvTranspose2d with kernel == stride (no padding), NHWC, weight in the
+ * PyTorch layout [Cin, Cout, k, k]. Cin % 32 == 0, Cout % 32 == 0. */
+int32_t gs_hip_conv_transpose(const float* x, int32_t B, int32_t H, int32_t W,
+                              int32_t Cin, const float* w, const float* b,
+                              float* y, int32_t Cout, int32_t k, void* stream);
+
+/* Bilinear x2 upsample, align_corners=True, NHWC, C % 4 == 0. */
+int32_t gs_hip_upsample2x(const float* x, int32_t B, int32_t H, int32_t W,
+                          int32_t C, float* y, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* 3. Graph-level entry points (MASt3R)                                      */
+/* ------------------------------------------------------------------------ */
+
+typedef struct gs_mastr_config {
+  int32_t img_h, img_w, patch;
+  int32_t enc_dim, enc_depth, enc_heads, enc_mlp;
+  int32_t dec_dim, dec_depth, dec_heads, dec_mlp;
+  int32_t dpt_feat;
+  int32_t dpt_dims[4];
+  int32_t dpt_hooks[4];
+  int32_t head_mid;
+  int32_t lf_hidden;
+  int32_t desc_dim;
+  float ln_eps;
+  float rope_base;
+  int32_t linear_layout; /* 0 = x W^T; 1 = reference CPU literal layout */
+  int32_t rope_mode;     /* 0 none, 1 per-attention q/k 2D, 2 ref-token */
+} gs_mastr_config;
+
+/* MASt3R ViT-L/ViT-B at 384x512 (24x32 patch grid), eps 1e-6, RoPE base 100,
+ * DPT hooks {0,6,9,12}, fusion width 256, 24-channel descriptors. Mirrors
+ * MASt3RInference#initialize (src/mastr/inference.cr:25-57). */
+void gs_mastr_default_config(gs_mastr_config* cfg);
+
+/* Weight inventory of a configuration, in checkpoint naming
+ * (src/mastr/weight_loader.cr:43-123). kind: 0 weight ~ N(0, 0.02),
+ * 1 bias (0), 2 LayerNorm gamma (1), 3 LayerNorm beta (0). shape has up to 4
+ * dims, unused dims are 0. Returns -1 for i out of range. */
+int32_t gs_mastr_weight_count(const gs_mastr_config* cfg);
+int32_t gs_mastr_weight_info(const gs_mastr_config* cfg, int32_t i,
+                             char* name_out, int32_t name_cap,
+                             int64_t shape_out[4], int32_t* kind_out);
+/* The host values of weight i for a seed: kind 0 -> N(0, 0.02); bias ->
+ * N(0, bias_std) (0 when bias_std == 0); gamma -> 1 + N(0, ln_std); beta ->
+ * N(0, ln_std). The configs' weights are seed 0, bias_std = ln_std = 0. */
+int32_t gs_mastr_weight_values(const gs_mastr_config* cfg, int32_t i,
+                               uint64_t seed, float bias_std, float ln_std,
+                               float* host_out, int64_t n);
+
+/* Context: device weights (re-laid for the kernels) + workspaces for up to
+ * max_pairs pairs. Weights start uninitialised. */
+int32_t gs_hip_mastr_create(const gs_mastr_config* cfg, int32_t max_pairs,
+                            void** ctx_out);
+void gs_hip_mastr_destroy(void* ctx);
+/* Fill every weight from the seeded generator (see gs_mastr_weight_values). */
+int32_t gs_hip_mastr_init_seeded(void* ctx, uint64_t seed, float bias_std,
+                                 float ln_std);
+/* Set one weight from host memory by checkpoint name (numel must match). */
+int32_t gs_hip_mastr_set_weight(void* ctx, const char* name,
+                                const float* host_values, int64_t numel);
+
+/* MASt3REncoderBlockV2#forward (src/mastr/encoder_v2.cr:38-48), in place on
+ * x [B, N, enc_dim] (device), block `layer` of the context. */
+int32_t gs_hip_mastr_encoder_block(void* ctx, int32_t layer, float* x,
+                                   int32_t B, void* stream);
+/* MASt3REncoderV2#forward (src/mastr/encoder_v2.cr:135-148):
+ * img [B,3,H,W] -> enc [B, N, enc_dim] (after enc_norm). B <= 2*max_pairs. */
+int32_t gs_hip_mastr_encoder(void* ctx, const float* img, int32_t B,
+                             float* enc, void* stream);
+/* MASt3RInference#forward_pair (src/mastr/inference.cr:92-115) for B pairs:
+ * img1, img2 [B,3,H,W] -> per view pts [B,H,W,3], conf [B,H,W,1] (1+exp),
+ * desc [B,H,W,desc_dim]. Any output pointer may be NULL to skip that head. */
+int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2,
+                          int32_t B, float* pts1, float* conf1, float* desc1,
+                          float* pts2, float* conf2, float* desc2,
+                          void* stream);
+/* Intermediate taps of the last gs_hip_mastr_pair call, copied to device
+ * buffers: enc1/enc2 [B,N,enc_dim], dec1/dec2 = dec_norm output
+ * [B,N,dec_dim]. Any pointer may be NULL. */
+int32_t gs_hip_mastr_pair_taps(void* ctx, int32_t B, float* enc1, float* enc2,
+                               float* dec1, float* dec2, void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* 4. Measurement (no reference counterpart: the reference only wall-clocks  */
+/*    whole ops, src/main.cr:860-909)                                         */
+/* ------------------------------------------------------------------------ */
+/* Between begin and end, every kernel launch is bracketed by HIP events on
+ * its own stream. end synchronises those events and returns the number of
+ * distinct kernels; entry i gives its launches, summed event time (ms),
+ * summed algorithmic flops and algorithmic HBM bytes. */
+int32_t gs_hip_profile_begin(void);
+int32_t gs_hip_profile_end(void);
+int32_t gs_hip_profile_entry(int32_t i, char* name_out, int32_t name_cap,
+                             int64_t* launches, double* ms, double* flops,
+                             double* bytes);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,962 @@
+/*
+ * oracle.cpp -- CPU restatement of the MASt3R inference arithmetic of
+ * skuznetsov/crystal-gausplat (Crystal). TEST INFRASTRUCTURE ONLY: it is the
+ * parity checker for the HIP path and the host-CPU baseline in bench.py; the
+ * product library never links or calls it.
+ *
+ * Which reference lines each function restates, and what pins it (the checks
+ * live in tests/test_oracle.py unless noted):
+ *
+ *   orc_linear          src/nn/linear.cr:41-63 (flatten), 167-203 (i-j-k loop,
+ *                       serial fp32 sum), 206-230 (bias added after the sum).
+ *                       layout 0 = x.W^T (src/nn/linear.cr:149-164 GPU path,
+ *                       nn.metal linear_forward_tiled); layout 1 = literal CPU
+ *                       indexing b_d[kk*n+j] (src/nn/linear.cr:194).
+ *                       Pinned: fp64 brute force, identity/zero weights, the
+ *                       D1 identity literal(W) == standard(reshape(W,[K,N])^T),
+ *                       torch.nn.functional.linear, bit-equality with the naive
+ *                       loop.
+ *   orc_layernorm       src/nn/layernorm.cr:192-240 (two-pass mean/var,
+ *                       1/sqrt(var+eps), affine). Pinned: closed form on a
+ *                       2-value row, mean~0/var~1, constant row -> beta,
+ *                       torch layer_norm.
+ *   orc_gelu            src/nn/vit.cr:130-148 (tanh form, c = (f32)sqrt(2/pi)).
+ *                       Pinned: GELU(0)=0, odd-part identity, torch
+ *                       gelu(approximate='tanh').
+ *   orc_sdpa            src/nn/attention.cr:215-325 (scores, scale after the
+ *                       dot, row max, expf, sum, divide, then P.V).
+ *                       Pinned: rows-sum-to-one via q=0 => mean(V), dominant
+ *                       score => one-hot, fp64 brute force, torch
+ *                       scaled_dot_product_attention.
+ *   orc_rope2d          2D RoPE applied to q and k in every attention (the
+ *                       per-attention RoPE2D of MASt3R; the reference applies a
+ *                       token-level variant only, see orc_rope_ref_token).
+ *                       Pinned: identity at (0,0), per-pair norm preservation,
+ *                       q.k depends only on the position difference, brute
+ *                       force on a 2x3 grid.
+ *   orc_rope_ref_token  src/mastr/encoder_v2.cr:165-176 (freqs), 180-258
+ *                       (apply), with explicit (grid_h, grid_w) instead of the
+ *                       square-only early return at 189-190. Pinned: identity
+ *                       at (0,0), hand-computed 1-token cases.
+ *   orc_unfold          src/nn/vit.cr:38-83 ((c,i,j) patch order). Pinned:
+ *                       equals torch unfold / a 16x16 stride-16 conv.
+ *   orc_conv2d          src/mastr/decoder_v2.cr:281-344 (NHWC x OIHW, sum order
+ *                       kh, kw, ic, OOB taps skipped, bias added after).
+ *                       Pinned: 6-loop naive variant (bit-equal), 1x1 conv ==
+ *                       linear, delta kernel identity, torch conv2d.
+ *   orc_conv_transpose  no reference kernel (ConvTranspose k == s of the DPT
+ *                       act_postprocess). Pinned: torch conv_transpose2d,
+ *                       GEMM + pixel shuffle identity.
+ *   orc_upsample2x      no reference kernel (bilinear x2, align_corners=True).
+ *                       Pinned: exact on constant and affine fields, corners
+ *                       preserved, torch interpolate(align_corners=True).
+ *   orc_pixel_shuffle   no reference kernel. Pinned: torch pixel_shuffle.
+ *   composites          src/mastr/encoder_v2.cr:38-48 (pre-norm block),
+ *                       135-154 (encoder), src/mastr/decoder_v2.cr:47-63
+ *                       (decoder block), 170-191 (pair decoder),
+ *                       356-437 (RCU / RefineNet), 502-530 + 619-655 (head).
+ *                       Composition follows the MASt3R configuration (other
+ *                       view as cross-attention memory, full DPT, 1+exp
+ *                       confidence, local-feature descriptors). Pinned: every
+ *                       primitive above, view-swap symmetry with shared
+ *                       decoder weights, determinism, and hand-composed
+ *                       torch CPU reference of an encoder block.
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <string>
+#include <vector>
+#include <algorithm>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int g_threads = 0;
+
+extern "C" void orc_set_threads(int32_t n) {
+  g_threads = n;
+#ifdef _OPENMP
+  if (n > 0) omp_set_num_threads(n);
+  else omp_set_num_threads(omp_get_num_procs());
+#endif
+}
+
+extern "C" int32_t orc_get_threads(void) {
+#ifdef _OPENMP
+  return omp_get_max_threads();
+#else
+  return 1;
+#endif
+}
+
+/* ======================================================================== */
+/* Linear                                                                    */
+/* ======================================================================== */
+
+/* Literal reference loop (src/nn/linear.cr:190-198 + 223-227). */
+extern "C" void orc_linear_naive(const float* x, int64_t M, int32_t K,
+                                 const float* W, const float* b, int32_t N,
+                                 float* y, int32_t layout) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < M; ++i) {
+    for (int32_t j = 0; j < N; ++j) {
+      float sum = 0.0f;
+      for (int32_t kk = 0; kk < K; ++kk) {
+        float w = layout == 0 ? W[(int64_t)j * K + kk] : W[(int64_t)kk * N + j];
+        sum += x[i * K + kk] * w;
+      }
+      y[i * N + j] = b ? sum + b[j] : sum;
+    }
+  }
+}
+
+/* Same per-element operation sequence as orc_linear_naive (sum over kk in
+ * increasing order, one rounding per mul and per add), blocked over rows and
+ * columns so the j loop vectorises. Bit-identical by construction. */
+extern "C" void orc_linear(const float* x, int64_t M, int32_t K, const float* W,
+                           const float* b, int32_t N, float* y, int32_t layout) {
+  std::vector<float> tmp;
+  const float* Wt = W; /* [K][N] */
+  if (layout == 0) {
+    tmp.resize((size_t)K * N);
+#pragma omp parallel for schedule(static)
+    for (int32_t kk = 0; kk < K; ++kk)
+      for (int32_t j = 0; j < N; ++j) tmp[(size_t)kk * N + j] = W[(size_t)j * K + kk];
+    Wt = tmp.data();
+  }
+  const int RB = 8, CB = 256;
+  const int64_t nrb = (M + RB - 1) / RB;
+  const int64_t ncb = (N + CB - 1) / CB;
+#pragma omp parallel for schedule(dynamic, 1) collapse(2)
+  for (int64_t rb = 0; rb < nrb; ++rb) {
+    for (int64_t cb = 0; cb < ncb; ++cb) {
+      float acc[RB][CB];
+      const int64_t i0 = rb * RB;
+      const int ri = (int)std::min<int64_t>(RB, M - i0);
+      const int32_t j0 = (int32_t)(cb * CB);
+      const int cj = std::min<int32_t>(CB, N - j0);
+      for (int r = 0; r < RB; ++r)
+        for (int jj = 0; jj < CB; ++jj) acc[r][jj] = 0.0f;
+      for (int32_t kk = 0; kk < K; ++kk) {
+        const float* wrow = Wt + (size_t)kk * N + j0;
+        for (int r = 0; r < ri; ++r) {
+          const float xv = x[(i0 + r) * K + kk];
+          float* a = acc[r];
+          for (int jj = 0; jj < cj; ++jj) {
+            float p = xv * wrow[jj];
+            a[jj] = a[jj] + p;
+          }
+        }
+      }
+      for (int r = 0; r < ri; ++r)
+        for (int jj = 0; jj < cj; ++jj)
+          y[(i0 + r) * N + j0 + jj] = b ? acc[r][jj] + b[j0 + jj] : acc[r][jj];
+    }
+  }
+}
+
+/* ======================================================================== */
+/* LayerNorm / GELU / ReLU / add                                             */
+/* ======================================================================== */
+
+extern "C" void orc_layernorm(const float* x, int64_t rows, int32_t D,
+                              const float* g, const float* bt, float eps,
+                              float* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* xr = x + r * D;
+    float mean = 0.0f;
+    for (int32_t i = 0; i < D; ++i) mean += xr[i];
+    mean /= (float)D;
+    float var = 0.0f;
+    for (int32_t i = 0; i < D; ++i) {
+      float diff = xr[i] - mean;
+      var += diff * diff;
+    }
+    var /= (float)D;
+    float inv_std = 1.0f / sqrtf(var + eps);
+    float* yr = y + r * D;
+    for (int32_t i = 0; i < D; ++i) {
+      float normalized = (xr[i] - mean) * inv_std;
+      yr[i] = normalized * g[i] + bt[i];
+    }
+  }
+}
+
+extern "C" void orc_gelu(const float* x, int64_t n, float* y) {
+  const float c = (float)sqrt(2.0 / M_PI);
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) {
+    float v = x[i];
+    float inner = 0.044715f * v;
+    inner = inner * v;
+    inner = inner * v;
+    inner = v + inner;
+    float t = tanhf(c * inner);
+    float h = 0.5f * v;
+    y[i] = h * (1.0f + t);
+  }
+}
+
+extern "C" void orc_relu(const float* x, int64_t n, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = x[i] > 0 ? x[i] : 0.0f;
+}
+
+extern "C" void orc_add(const float* a, const float* b, int64_t n, float* y) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) y[i] = a[i] + b[i];
+}
+
+/* ======================================================================== */
+/* Attention                                                                 */
+/* ======================================================================== */
+
+/* src/nn/attention.cr:240-321. The dot over d and the P.V sum over j keep
+ * their sequential order per output element; the loops are arranged so the
+ * independent j (scores) and d (outputs) lanes vectorise. */
+extern "C" void orc_sdpa(const float* q, const float* k, const float* v,
+                         float* o, int32_t B, int32_t H, int32_t Nq,
+                         int32_t Nkv, int32_t hd, float scale) {
+  const int64_t BH = (int64_t)B * H;
+#pragma omp parallel
+  {
+    std::vector<float> kT((size_t)hd * Nkv);
+    std::vector<float> s(Nkv);
+    std::vector<float> acc(hd);
+    int64_t last_bh = -1;
+#pragma omp for schedule(static) collapse(2)
+    for (int64_t bh = 0; bh < BH; ++bh) {
+      for (int32_t i = 0; i < Nq; ++i) {
+        const float* kb = k + bh * Nkv * hd;
+        const float* vb = v + bh * Nkv * hd;
+        if (bh != last_bh) {
+          for (int32_t j = 0; j < Nkv; ++j)
+            for (int32_t d = 0; d < hd; ++d) kT[(size_t)d * Nkv + j] = kb[(size_t)j * hd + d];
+          last_bh = bh;
+        }
+        const float* qi = q + (bh * Nq + i) * hd;
+        for (int32_t j = 0; j < Nkv; ++j) s[j] = 0.0f;
+        for (int32_t d = 0; d < hd; ++d) {
+          const float qv = qi[d];
+          const float* kr = &kT[(size_t)d * Nkv];
+          for (int32_t j = 0; j < Nkv; ++j) {
+            float p = qv * kr[j];
+            s[j] = s[j] + p;
+          }
+        }
+        for (int32_t j = 0; j < Nkv; ++j) s[j] = s[j] * scale;
+        float mx = s[0];
+        for (int32_t j = 1; j < Nkv; ++j) mx = std::max(mx, s[j]);
+        float sum = 0.0f;
+        for (int32_t j = 0; j < Nkv; ++j) {
+          s[j] = expf(s[j] - mx);
+          sum += s[j];
+        }
+        for (int32_t j = 0; j < Nkv; ++j) s[j] /= sum;
+        for (int32_t d = 0; d < hd; ++d) acc[d] = 0.0f;
+        for (int32_t j = 0; j < Nkv; ++j) {
+          const float sj = s[j];
+          const float* vr = vb + (size_t)j * hd;
+          for (int32_t d = 0; d < hd; ++d) {
+            float p = sj * vr[d];
+            acc[d] = acc[d] + p;
+          }
+        }
+        float* oi = o + (bh * Nq + i) * hd;
+        for (int32_t d = 0; d < hd; ++d) oi[d] = acc[d];
+      }
+    }
+  }
+}
+
+/* Literal loops of src/nn/attention.cr:240-321 (scores materialised per row,
+ * dot over d innermost, P.V sum over j innermost). */
+extern "C" void orc_sdpa_naive(const float* q, const float* k, const float* v,
+                               float* o, int32_t B, int32_t H, int32_t Nq,
+                               int32_t Nkv, int32_t hd, float scale) {
+  const int64_t BH = (int64_t)B * H;
+#pragma omp parallel
+  {
+    std::vector<float> s(Nkv);
+#pragma omp for schedule(static) collapse(2)
+    for (int64_t bh = 0; bh < BH; ++bh) {
+      for (int32_t i = 0; i < Nq; ++i) {
+        const float* qi = q + (bh * Nq + i) * hd;
+        for (int32_t j = 0; j < Nkv; ++j) {
+          const float* kj = k + (bh * Nkv + j) * hd;
+          float dot = 0.0f;
+          for (int32_t d = 0; d < hd; ++d) dot += qi[d] * kj[d];
+          s[j] = dot * scale;
+        }
+        float mx = s[0];
+        for (int32_t j = 1; j < Nkv; ++j) mx = std::max(mx, s[j]);
+        float sum = 0.0f;
+        for (int32_t j = 0; j < Nkv; ++j) {
+          s[j] = expf(s[j] - mx);
+          sum += s[j];
+        }
+        for (int32_t j = 0; j < Nkv; ++j) s[j] /= sum;
+        for (int32_t d = 0; d < hd; ++d) {
+          float acc = 0.0f;
+          for (int32_t j = 0; j < Nkv; ++j) acc += s[j] * v[(bh * Nkv + j) * hd + d];
+          o[(bh * Nq + i) * hd + d] = acc;
+        }
+      }
+    }
+  }
+}
+
+static int g_naive = 0;
+extern "C" void orc_set_naive(int32_t on) { g_naive = on; }
+
+/* ======================================================================== */
+/* RoPE                                                                      */
+/* ======================================================================== */
+
+extern "C" void orc_rope_table(int32_t max_pos, int32_t hd, float base,
+                               float* cos_t, float* sin_t) {
+  const int32_t half = hd / 2;   /* one spatial axis */
+  const int32_t nf = half / 2;   /* frequencies per axis */
+  for (int32_t p = 0; p < max_pos; ++p) {
+    for (int32_t j = 0; j < nf; ++j) {
+      float inv = 1.0f / powf(base, (float)(2 * j) / (float)half);
+      float th = (float)p * inv;
+      cos_t[p * nf + j] = cosf(th);
+      sin_t[p * nf + j] = sinf(th);
+    }
+  }
+}
+
+extern "C" void orc_rope2d(float* t, int32_t B, int32_t N, int32_t H,
+                           int32_t hd, int32_t grid_w, float base) {
+  const int32_t grid_h = (N + grid_w - 1) / grid_w;
+  const int32_t maxp = std::max(grid_h, grid_w);
+  const int32_t half = hd / 2, nf = hd / 4;
+  std::vector<float> ct((size_t)maxp * nf), st((size_t)maxp * nf);
+  orc_rope_table(maxp, hd, base, ct.data(), st.data());
+  const int64_t D = (int64_t)H * hd;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int32_t b = 0; b < B; ++b) {
+    for (int32_t n = 0; n < N; ++n) {
+      const int32_t py = n / grid_w, px = n % grid_w;
+      float* tr = t + ((int64_t)b * N + n) * D;
+      for (int32_t h = 0; h < H; ++h) {
+        for (int32_t ax = 0; ax < 2; ++ax) {
+          const int32_t pos = ax == 0 ? py : px;
+          float* u = tr + h * hd + ax * half;
+          for (int32_t j = 0; j < nf; ++j) {
+            const float c = ct[pos * nf + j], s = st[pos * nf + j];
+            const float a = u[j], bb = u[j + nf];
+            u[j] = a * c - bb * s;
+            u[j + nf] = bb * c + a * s;
+          }
+        }
+      }
+    }
+  }
+}
+
+extern "C" void orc_rope_ref_token(const float* x, float* y, int32_t B,
+                                   int32_t grid_h, int32_t grid_w, int32_t D,
+                                   int32_t H, float base) {
+  const int32_t hd = D / H, half = hd / 2;
+  std::vector<float> fr(half);
+  for (int32_t i = 0; i < half; ++i)
+    fr[i] = 1.0f / powf(base, (2.0f * (float)i) / (float)hd);
+  const int32_t N = grid_h * grid_w;
+  for (int32_t b = 0; b < B; ++b)
+    for (int32_t yy = 0; yy < grid_h; ++yy)
+      for (int32_t xi = 0; xi < grid_w; ++xi) {
+        const int64_t pos = yy * grid_w + xi;
+        const float* xr = x + ((int64_t)b * N + pos) * D;
+        float* yr = y + ((int64_t)b * N + pos) * D;
+        for (int32_t d = 0; d < D; ++d) {
+          const int32_t dh = d % hd;
+          if (dh < half) {
+            float th = (float)yy * fr[dh];
+            float c = cosf(th), s = sinf(th);
+            yr[d] = xr[d] * c - xr[d + half] * s;
+          } else {
+            float th = (float)xi * fr[dh - half];
+            float c = cosf(th), s = sinf(th);
+            yr[d] = xr[d - half] * s + xr[d] * c;
+          }
+        }
+      }
+}
+
+/* ======================================================================== */
+/* Convolutions and resampling                                               */
+/* ======================================================================== */
+
+extern "C" void orc_unfold(const float* img, int32_t B, int32_t C, int32_t H,
+                           int32_t W, int32_t p, float* out) {
+  const int32_t ph = H / p, pw = W / p, np = ph * pw, pd = C * p * p;
+  for (int32_t b = 0; b < B; ++b)
+    for (int32_t y = 0; y < ph; ++y)
+      for (int32_t x = 0; x < pw; ++x)
+        for (int32_t c = 0; c < C; ++c)
+          for (int32_t i = 0; i < p; ++i)
+            for (int32_t j = 0; j < p; ++j)
+              out[((int64_t)b * np + y * pw + x) * pd + c * p * p + i * p + j] =
+                  img[(((int64_t)b * C + c) * H + y * p + i) * W + x * p + j];
+}
+
+extern "C" void orc_conv2d_naive(const float* x, int32_t B, int32_t H, int32_t W,
+                                 int32_t Cin, const float* w, const float* b,
+                                 int32_t Cout, int32_t k, int32_t stride,
+                                 int32_t pad, float* y) {
+  const int32_t Ho = (H + 2 * pad - k) / stride + 1;
+  const int32_t Wo = (W + 2 * pad - k) / stride + 1;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int32_t bb = 0; bb < B; ++bb)
+    for (int32_t oh = 0; oh < Ho; ++oh)
+      for (int32_t ow = 0; ow < Wo; ++ow)
+        for (int32_t oc = 0; oc < Cout; ++oc) {
+          float sum = 0.0f;
+          for (int32_t kh = 0; kh < k; ++kh)
+            for (int32_t kw = 0; kw < k; ++kw) {
+              const int32_t ih = oh * stride + kh - pad, iw = ow * stride + kw - pad;
+              if (ih < 0 || ih >= H || iw < 0 || iw >= W) continue;
+              for (int32_t ic = 0; ic < Cin; ++ic)
+                sum += x[(((int64_t)bb * H + ih) * W + iw) * Cin + ic] *
+                       w[(((int64_t)oc * Cin + ic) * k + kh) * k + kw];
+            }
+          float* r = &y[(((int64_t)bb * Ho + oh) * Wo + ow) * Cout + oc];
+          *r = sum;
+          if (b) *r += b[oc];
+        }
+}
+
+/* Same per-element sequence as orc_conv2d_naive, vectorised across output
+ * channels and blocked over output pixels. */
+extern "C" void orc_conv2d(const float* x, int32_t B, int32_t H, int32_t W,
+                           int32_t Cin, const float* w, const float* b,
+                           int32_t Cout, int32_t k, int32_t stride, int32_t pad,
+                           float* y) {
+  const int32_t Ho = (H + 2 * pad - k) / stride + 1;
+  const int32_t Wo = (W + 2 * pad - k) / stride + 1;
+  /* wt[kh][kw][ic][oc] */
+  std::vector<float> wt((size_t)k * k * Cin * Cout);
+#pragma omp parallel for schedule(static)
+  for (int32_t oc = 0; oc < Cout; ++oc)
+    for (int32_t ic = 0; ic < Cin; ++ic)
+      for (int32_t kh = 0; kh < k; ++kh)
+        for (int32_t kw = 0; kw < k; ++kw)
+          wt[(((size_t)kh * k + kw) * Cin + ic) * Cout + oc] =
+              w[(((size_t)oc * Cin + ic) * k + kh) * k + kw];
+  const int PB = 16, CB = 64;
+  const int64_t npix = (int64_t)B * Ho * Wo;
+  const int64_t npb = (npix + PB - 1) / PB;
+  const int32_t ncb = (Cout + CB - 1) / CB;
+#pragma omp parallel for schedule(dynamic, 1) collapse(2)
+  for (int32_t cb = 0; cb < ncb; ++cb) {
+    for (int64_t pb = 0; pb < npb; ++pb) {
+      float acc[PB][CB];
+      const int32_t oc0 = cb * CB;
+      const int32_t nc = std::min(CB, Cout - oc0);
+      const int64_t p0 = pb * PB;
+      const int np = (int)std::min<int64_t>(PB, npix - p0);
+      int32_t pbb[PB], poh[PB], pow_[PB];
+      for (int q = 0; q < np; ++q) {
+        int64_t pix = p0 + q;
+        pow_[q] = (int32_t)(pix % Wo);
+        poh[q] = (int32_t)((pix / Wo) % Ho);
+        pbb[q] = (int32_t)(pix / ((int64_t)Wo * Ho));
+        for (int c = 0; c < CB; ++c) acc[q][c] = 0.0f;
+      }
+      for (int32_t kh = 0; kh < k; ++kh)
+        for (int32_t kw = 0; kw < k; ++kw) {
+          const float* wk = &wt[(((size_t)kh * k + kw) * Cin) * Cout + oc0];
+          for (int q = 0; q < np; ++q) {
+            const int32_t ih = poh[q] * stride + kh - pad;
+            const int32_t iw = pow_[q] * stride + kw - pad;
+            if (ih < 0 || ih >= H || iw < 0 || iw >= W) continue;
+            const float* xp = x + (((int64_t)pbb[q] * H + ih) * W + iw) * Cin;
+            float* a = acc[q];
+            for (int32_t ic = 0; ic < Cin; ++ic) {
+              const float xv = xp[ic];
+              const float* wr = wk + (size_t)ic * Cout;
+              for (int c = 0; c < nc; ++c) {
+                float pr = xv * wr[c];
+                a[c] = a[c] + pr;
+              }
+            }
+          }
+        }
+      for (int q = 0; q < np; ++q) {
+        float* yo = y + (p0 + q) * Cout + oc0;
+        for (int c = 0; c < nc; ++c) yo[c] = b ? acc[q][c] + b[oc0 + c] : acc[q][c];
+      }
+    }
+  }
+}
+
+extern "C" void orc_conv_transpose(const float* x, int32_t B, int32_t H,
+                                   int32_t W, int32_t Cin, const float* w,
+                                   const float* b, int32_t Cout, int32_t k,
+                                   float* y) {
+  const int32_t Ho = H * k, Wo = W * k;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int32_t bb = 0; bb < B; ++bb)
+    for (int32_t ih = 0; ih < H; ++ih)
+      for (int32_t iw = 0; iw < W; ++iw) {
+        const float* xp = x + (((int64_t)bb * H + ih) * W + iw) * Cin;
+        for (int32_t i = 0; i < k; ++i)
+          for (int32_t j = 0; j < k; ++j)
+            for (int32_t oc = 0; oc < Cout; ++oc) {
+              float sum = 0.0f;
+              for (int32_t ic = 0; ic < Cin; ++ic)
+                sum += xp[ic] * w[(((int64_t)ic * Cout + oc) * k + i) * k + j];
+              float* r = &y[(((int64_t)bb * Ho + ih * k + i) * Wo + iw * k + j) * Cout + oc];
+              *r = b ? sum + b[oc] : sum;
+            }
+      }
+}
+
+extern "C" void orc_upsample2x(const float* x, int32_t B, int32_t H, int32_t W,
+                               int32_t C, float* y) {
+  const int32_t Ho = 2 * H, Wo = 2 * W;
+  const float sh = Ho > 1 ? (float)(H - 1) / (float)(Ho - 1) : 0.0f;
+  const float sw = Wo > 1 ? (float)(W - 1) / (float)(Wo - 1) : 0.0f;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int32_t bb = 0; bb < B; ++bb)
+    for (int32_t oy = 0; oy < Ho; ++oy) {
+      const float fy = sh * (float)oy;
+      const int32_t y0 = (int32_t)fy;
+      const int32_t y1 = y0 + (y0 < H - 1 ? 1 : 0);
+      const float ly = fy - (float)y0, hy = 1.0f - ly;
+      for (int32_t ox = 0; ox < Wo; ++ox) {
+        const float fx = sw * (float)ox;
+        const int32_t x0 = (int32_t)fx;
+        const int32_t x1 = x0 + (x0 < W - 1 ? 1 : 0);
+        const float lx = fx - (float)x0, hx = 1.0f - lx;
+        const float* r0 = x + ((int64_t)bb * H + y0) * W * C;
+        const float* r1 = x + ((int64_t)bb * H + y1) * W * C;
+        float* o = y + (((int64_t)bb * Ho + oy) * Wo + ox) * C;
+        for (int32_t c = 0; c < C; ++c) {
+          float top = hx * r0[(int64_t)x0 * C + c] + lx * r0[(int64_t)x1 * C + c];
+          float bot = hx * r1[(int64_t)x0 * C + c] + lx * r1[(int64_t)x1 * C + c];
+          o[c] = hy * top + ly * bot;
+        }
+      }
+    }
+}
+
+extern "C" void orc_pixel_shuffle(const float* f, int32_t B, int32_t h,
+                                  int32_t w, int32_t Cf, int32_t r, int32_t C,
+                                  float* desc) {
+  const int32_t Ho = h * r, Wo = w * r;
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int32_t bb = 0; bb < B; ++bb)
+    for (int32_t oy = 0; oy < Ho; ++oy)
+      for (int32_t ox = 0; ox < Wo; ++ox) {
+        const int32_t ty = oy / r, i = oy % r, tx = ox / r, j = ox % r;
+        const float* fr = f + (((int64_t)bb * h + ty) * w + tx) * Cf;
+        float* o = desc + (((int64_t)bb * Ho + oy) * Wo + ox) * C;
+        for (int32_t c = 0; c < C; ++c) o[c] = fr[c * r * r + i * r + j];
+      }
+}
+
+/* ======================================================================== */
+/* Composites                                                                */
+/* ======================================================================== */
+
+namespace {
+
+struct Ctx {
+  const orc_config* cfg;
+  orc_weight_fn wf;
+  void* user;
+  const float* get(const std::string& name) const {
+    const float* p = wf(name.c_str(), user);
+    if (!p) {
+      fprintf(stderr, "oracle: missing weight %s\n", name.c_str());
+      abort();
+    }
+    return p;
+  }
+};
+
+typedef std::vector<float> Buf;
+
+/* Linear over a reference-style module: y = x.W^T + b (or the literal CPU
+ * layout). `groups` > 1 treats a fused weight [groups*Nout_g, K] as that many
+ * separate Linear modules (q/k/v split in src/mastr/weight_loader.cr:206-242),
+ * which only matters for the literal layout. */
+void linear_mod(const Ctx& c, const std::string& name, const float* x, int64_t M,
+                int32_t K, int32_t N, float* y, int groups = 1,
+                bool has_bias = true) {
+  const float* W = c.get(name + ".weight");
+  const float* b = has_bias ? c.get(name + ".bias") : nullptr;
+  if (c.cfg->linear_layout == 0 || groups == 1) {
+    (g_naive ? orc_linear_naive : orc_linear)(x, M, K, W, b, N, y, c.cfg->linear_layout);
+    return;
+  }
+  const int32_t Ng = N / groups;
+  Buf tmp((size_t)M * Ng);
+  for (int g = 0; g < groups; ++g) {
+    (g_naive ? orc_linear_naive : orc_linear)(x, M, K, W + (size_t)g * Ng * K,
+                                              b ? b + (size_t)g * Ng : nullptr, Ng,
+                                              tmp.data(), 1);
+    for (int64_t i = 0; i < M; ++i)
+      memcpy(y + i * N + (size_t)g * Ng, tmp.data() + i * Ng, sizeof(float) * Ng);
+  }
+}
+
+void layernorm_mod(const Ctx& c, const std::string& name, const float* x,
+                   int64_t rows, int32_t D, float* y) {
+  orc_layernorm(x, rows, D, c.get(name + ".weight"), c.get(name + ".bias"),
+                c.cfg->ln_eps, y);
+}
+
+/* [B,N,H*hd] (column offset col0 within rows of width ld) -> [B,H,N,hd] */
+void split_heads(const float* t, int64_t ld, int32_t col0, int32_t B, int32_t N,
+                 int32_t H, int32_t hd, float* out) {
+  for (int32_t b = 0; b < B; ++b)
+    for (int32_t n = 0; n < N; ++n)
+      for (int32_t h = 0; h < H; ++h)
+        for (int32_t d = 0; d < hd; ++d)
+          out[(((int64_t)b * H + h) * N + n) * hd + d] =
+              t[((int64_t)b * N + n) * ld + col0 + h * hd + d];
+}
+
+void merge_heads(const float* t, int32_t B, int32_t N, int32_t H, int32_t hd,
+                 float* out) {
+  for (int32_t b = 0; b < B; ++b)
+    for (int32_t n = 0; n < N; ++n)
+      for (int32_t h = 0; h < H; ++h)
+        for (int32_t d = 0; d < hd; ++d)
+          out[((int64_t)b * N + n) * (H * hd) + h * hd + d] =
+              t[(((int64_t)b * H + h) * N + n) * hd + d];
+}
+
+/* RoPE on the column range [col0, col0+D) of rows of width ld. */
+void rope_cols(const Ctx& c, float* t, int64_t ld, int32_t col0, int32_t B,
+               int32_t N, int32_t H, int32_t hd, int32_t grid_w) {
+  const int32_t D = H * hd;
+  Buf tmp((size_t)B * N * D);
+  for (int64_t r = 0; r < (int64_t)B * N; ++r)
+    memcpy(&tmp[r * D], t + r * ld + col0, sizeof(float) * D);
+  orc_rope2d(tmp.data(), B, N, H, hd, grid_w, c.cfg->rope_base);
+  for (int64_t r = 0; r < (int64_t)B * N; ++r)
+    memcpy(t + r * ld + col0, &tmp[r * D], sizeof(float) * D);
+}
+
+/* Attention core on projected q (ldq, col offset) and k/v. */
+void attention_core(const Ctx& c, float* qsrc, int64_t ldq, int32_t qcol,
+                    float* ksrc, int64_t ldk, int32_t kcol, const float* vsrc,
+                    int64_t ldv, int32_t vcol, int32_t B, int32_t Nq,
+                    int32_t Nkv, int32_t H, int32_t hd, int32_t grid_w,
+                    float* out /* [B,Nq,H*hd] */) {
+  if (c.cfg->rope_mode == 1) {
+    rope_cols(c, qsrc, ldq, qcol, B, Nq, H, hd, grid_w);
+    rope_cols(c, ksrc, ldk, kcol, B, Nkv, H, hd, grid_w);
+  }
+  Buf q((size_t)B * H * Nq * hd), k((size_t)B * H * Nkv * hd),
+      v((size_t)B * H * Nkv * hd), o((size_t)B * H * Nq * hd);
+  split_heads(qsrc, ldq, qcol, B, Nq, H, hd, q.data());
+  split_heads(ksrc, ldk, kcol, B, Nkv, H, hd, k.data());
+  split_heads(vsrc, ldv, vcol, B, Nkv, H, hd, v.data());
+  const float scale = 1.0f / sqrtf((float)hd);
+  (g_naive ? orc_sdpa_naive : orc_sdpa)(q.data(), k.data(), v.data(), o.data(), B, H, Nq,
+                                        Nkv, hd, scale);
+  merge_heads(o.data(), B, Nq, H, hd, out);
+}
+
+void mlp_mod(const Ctx& c, const std::string& name, const float* x, int64_t M,
+             int32_t D, int32_t F, int32_t Dout, float* y) {
+  Buf h((size_t)M * F);
+  linear_mod(c, name + ".fc1", x, M, D, F, h.data());
+  orc_gelu(h.data(), (int64_t)h.size(), h.data());
+  linear_mod(c, name + ".fc2", h.data(), M, F, Dout, y);
+}
+
+/* src/mastr/encoder_v2.cr:38-48 */
+void encoder_block(const Ctx& c, const std::string& pre, float* x, int32_t B,
+                   int32_t N, int32_t grid_w) {
+  const orc_config* cf = c.cfg;
+  const int32_t D = cf->enc_dim, H = cf->enc_heads, hd = D / H;
+  const int64_t M = (int64_t)B * N;
+  Buf h((size_t)M * D), qkv((size_t)M * 3 * D), a((size_t)M * D), p((size_t)M * D);
+  layernorm_mod(c, pre + ".norm1", x, M, D, h.data());
+  linear_mod(c, pre + ".attn.qkv", h.data(), M, D, 3 * D, qkv.data(), 3);
+  attention_core(c, qkv.data(), 3 * D, 0, qkv.data(), 3 * D, D, qkv.data(), 3 * D,
+                 2 * D, B, N, N, H, hd, grid_w, a.data());
+  linear_mod(c, pre + ".attn.proj", a.data(), M, D, D, p.data());
+  orc_add(x, p.data(), M * D, x);
+  layernorm_mod(c, pre + ".norm2", x, M, D, h.data());
+  mlp_mod(c, pre + ".mlp", h.data(), M, D, cf->enc_mlp, D, p.data());
+  orc_add(x, p.data(), M * D, x);
+}
+
+/* src/mastr/decoder_v2.cr:47-63; mem is the cross-attention memory. */
+void decoder_block(const Ctx& c, const std::string& pre, float* x,
+                   const float* mem, int32_t B, int32_t N, int32_t grid_w) {
+  const orc_config* cf = c.cfg;
+  const int32_t D = cf->dec_dim, H = cf->dec_heads, hd = D / H;
+  const int64_t M = (int64_t)B * N;
+  Buf h((size_t)M * D), qkv((size_t)M * 3 * D), a((size_t)M * D), p((size_t)M * D);
+  Buf ym((size_t)M * D), kk((size_t)M * D), vv((size_t)M * D), qq((size_t)M * D);
+  /* self-attention */
+  layernorm_mod(c, pre + ".norm1", x, M, D, h.data());
+  linear_mod(c, pre + ".attn.qkv", h.data(), M, D, 3 * D, qkv.data(), 3);
+  attention_core(c, qkv.data(), 3 * D, 0, qkv.data(), 3 * D, D, qkv.data(), 3 * D,
+                 2 * D, B, N, N, H, hd, grid_w, a.data());
+  linear_mod(c, pre + ".attn.proj", a.data(), M, D, D, p.data());
+  orc_add(x, p.data(), M * D, x);
+  /* cross-attention: query norm3 (reference role naming), memory norm_y */
+  layernorm_mod(c, pre + ".norm3", x, M, D, h.data());
+  layernorm_mod(c, pre + ".norm_y", mem, M, D, ym.data());
+  linear_mod(c, pre + ".cross_attn.projq", h.data(), M, D, D, qq.data());
+  linear_mod(c, pre + ".cross_attn.projk", ym.data(), M, D, D, kk.data());
+  linear_mod(c, pre + ".cross_attn.projv", ym.data(), M, D, D, vv.data());
+  attention_core(c, qq.data(), D, 0, kk.data(), D, 0, vv.data(), D, 0, B, N, N, H,
+                 hd, grid_w, a.data());
+  linear_mod(c, pre + ".cross_attn.proj", a.data(), M, D, D, p.data());
+  orc_add(x, p.data(), M * D, x);
+  /* MLP: norm2 (reference role naming) */
+  layernorm_mod(c, pre + ".norm2", x, M, D, h.data());
+  mlp_mod(c, pre + ".mlp", h.data(), M, D, cf->dec_mlp, D, p.data());
+  orc_add(x, p.data(), M * D, x);
+}
+
+void conv_mod(const Ctx& c, const std::string& name, const float* x, int32_t B,
+              int32_t H, int32_t W, int32_t Cin, int32_t Cout, int32_t k,
+              int32_t stride, int32_t pad, bool bias, float* y) {
+  (g_naive ? orc_conv2d_naive : orc_conv2d)(x, B, H, W, Cin, c.get(name + ".weight"),
+             bias ? c.get(name + ".bias") : nullptr, Cout, k, stride, pad, y);
+}
+
+/* RCU = ReLU -> conv3x3 -> ReLU -> conv3x3 + x (DPT ResidualConvUnit; the
+ * reference's unit at src/mastr/decoder_v2.cr:365-370 omits the first ReLU). */
+void rcu(const Ctx& c, const std::string& name, const float* x, int32_t B,
+         int32_t H, int32_t W, int32_t F, float* y) {
+  const int64_t n = (int64_t)B * H * W * F;
+  Buf t(n), u(n);
+  orc_relu(x, n, t.data());
+  conv_mod(c, name + ".conv1", t.data(), B, H, W, F, F, 3, 1, 1, true, u.data());
+  orc_relu(u.data(), n, u.data());
+  conv_mod(c, name + ".conv2", u.data(), B, H, W, F, F, 3, 1, 1, true, t.data());
+  orc_add(t.data(), x, n, y);
+}
+
+/* Feature fusion: out = x0 (+ RCU1(x1)); RCU2; bilinear x2; 1x1 out_conv. */
+Buf fusion(const Ctx& c, const std::string& name, const float* x0,
+           const float* x1, int32_t B, int32_t H, int32_t W, int32_t F) {
+  const int64_t n = (int64_t)B * H * W * F;
+  Buf s(x0, x0 + n), t(n);
+  if (x1) {
+    rcu(c, name + ".resConfUnit1", x1, B, H, W, F, t.data());
+    orc_add(s.data(), t.data(), n, s.data());
+  }
+  rcu(c, name + ".resConfUnit2", s.data(), B, H, W, F, t.data());
+  Buf up((size_t)n * 4), out((size_t)n * 4);
+  orc_upsample2x(t.data(), B, H, W, F, up.data());
+  conv_mod(c, name + ".out_conv", up.data(), B, 2 * H, 2 * W, F, F, 1, 1, 0, true,
+           out.data());
+  return out;
+}
+
+/* Full DPT head on hooks; writes pts [B,Hi,Wi,3], conf [B,Hi,Wi,1]. */
+void dpt_head(const Ctx& c, const std::string& pre, const float* const hooks[4],
+              int32_t B, int32_t gh, int32_t gw, float* pts, float* conf) {
+  const orc_config* cf = c.cfg;
+  const int32_t F = cf->dpt_feat;
+  const int32_t in_dims[4] = {cf->enc_dim, cf->dec_dim, cf->dec_dim, cf->dec_dim};
+  const int64_t N = (int64_t)gh * gw;
+  Buf act[4];
+  int32_t ah[4], aw[4];
+  const std::string ap = pre + ".dpt.act_postprocess.";
+  for (int i = 0; i < 4; ++i) {
+    const int32_t Cd = cf->dpt_dims[i];
+    Buf t((size_t)B * N * Cd);
+    conv_mod(c, ap + std::to_string(i) + ".0", hooks[i], B, gh, gw, in_dims[i], Cd,
+             1, 1, 0, true, t.data());
+    if (i == 0 || i == 1) {
+      const int32_t k = i == 0 ? 4 : 2;
+      ah[i] = gh * k;
+      aw[i] = gw * k;
+      act[i].resize((size_t)B * ah[i] * aw[i] * Cd);
+      const std::string nm = ap + std::to_string(i) + ".1";
+      orc_conv_transpose(t.data(), B, gh, gw, Cd, c.get(nm + ".weight"),
+                         c.get(nm + ".bias"), Cd, k, act[i].data());
+    } else if (i == 2) {
+      ah[i] = gh;
+      aw[i] = gw;
+      act[i].swap(t);
+    } else {
+      ah[i] = (gh + 2 - 3) / 2 + 1;
+      aw[i] = (gw + 2 - 3) / 2 + 1;
+      act[i].resize((size_t)B * ah[i] * aw[i] * Cd);
+      conv_mod(c, ap + "3.1", t.data(), B, gh, gw, Cd, Cd, 3, 2, 1, true,
+               act[i].data());
+    }
+  }
+  Buf L[4];
+  for (int i = 0; i < 4; ++i) {
+    L[i].resize((size_t)B * ah[i] * aw[i] * F);
+    conv_mod(c, pre + ".dpt.scratch.layer" + std::to_string(i + 1) + "_rn", act[i].data(),
+             B, ah[i], aw[i], cf->dpt_dims[i], F, 3, 1, 1, false, L[i].data());
+  }
+  const std::string sp = pre + ".dpt.scratch.refinenet";
+  Buf r4 = fusion(c, sp + "4", L[3].data(), nullptr, B, ah[3], aw[3], F);
+  Buf r3 = fusion(c, sp + "3", r4.data(), L[2].data(), B, ah[2], aw[2], F);
+  Buf r2 = fusion(c, sp + "2", r3.data(), L[1].data(), B, ah[1], aw[1], F);
+  Buf r1 = fusion(c, sp + "1", r2.data(), L[0].data(), B, ah[0], aw[0], F);
+  const int32_t h1 = 2 * ah[0], w1 = 2 * aw[0];
+  const int32_t Hm = cf->head_mid, Fh = F / 2;
+  Buf t1((size_t)B * h1 * w1 * Fh);
+  conv_mod(c, pre + ".dpt.head.0", r1.data(), B, h1, w1, F, Fh, 3, 1, 1, true, t1.data());
+  Buf t2((size_t)B * h1 * w1 * Fh * 4);
+  orc_upsample2x(t1.data(), B, h1, w1, Fh, t2.data());
+  const int32_t Hi = 2 * h1, Wi = 2 * w1;
+  Buf t3((size_t)B * Hi * Wi * Hm);
+  conv_mod(c, pre + ".dpt.head.2", t2.data(), B, Hi, Wi, Fh, Hm, 3, 1, 1, true, t3.data());
+  orc_relu(t3.data(), (int64_t)t3.size(), t3.data());
+  Buf t4((size_t)B * Hi * Wi * 4);
+  conv_mod(c, pre + ".dpt.head.4", t3.data(), B, Hi, Wi, Hm, 4, 1, 1, 0, true, t4.data());
+  const int64_t P = (int64_t)B * Hi * Wi;
+  for (int64_t i = 0; i < P; ++i) {
+    pts[i * 3 + 0] = t4[i * 4 + 0];
+    pts[i * 3 + 1] = t4[i * 4 + 1];
+    pts[i * 3 + 2] = t4[i * 4 + 2];
+    conf[i] = 1.0f + expf(t4[i * 4 + 3]);
+  }
+}
+
+/* Local features: MLP(concat(enc, dec_final)) -> pixel shuffle -> desc. */
+void local_features(const Ctx& c, const std::string& pre, const float* enc,
+                    const float* dec, int32_t B, int32_t gh, int32_t gw,
+                    float* desc) {
+  const orc_config* cf = c.cfg;
+  const int64_t M = (int64_t)B * gh * gw;
+  const int32_t Din = cf->enc_dim + cf->dec_dim;
+  const int32_t r = cf->patch;
+  const int32_t Fo = (cf->desc_dim + 1) * r * r;
+  Buf cat((size_t)M * Din), f((size_t)M * Fo);
+  for (int64_t i = 0; i < M; ++i) {
+    memcpy(&cat[i * Din], enc + i * cf->enc_dim, sizeof(float) * cf->enc_dim);
+    memcpy(&cat[i * Din + cf->enc_dim], dec + i * cf->dec_dim, sizeof(float) * cf->dec_dim);
+  }
+  mlp_mod(c, pre + ".head_local_features", cat.data(), M, Din, cf->lf_hidden, Fo,
+          f.data());
+  orc_pixel_shuffle(f.data(), B, gh, gw, Fo, r, cf->desc_dim, desc);
+}
+
+void encoder(const Ctx& c, const float* img, int32_t B, float* enc) {
+  const orc_config* cf = c.cfg;
+  const int32_t gh = cf->img_h / cf->patch, gw = cf->img_w / cf->patch;
+  const int32_t N = gh * gw, pd = 3 * cf->patch * cf->patch, D = cf->enc_dim;
+  const int64_t M = (int64_t)B * N;
+  Buf pt((size_t)M * pd), x((size_t)M * D);
+  orc_unfold(img, B, 3, cf->img_h, cf->img_w, cf->patch, pt.data());
+  linear_mod(c, "patch_embed.proj", pt.data(), M, pd, D, x.data());
+  if (cf->rope_mode == 2) {
+    Buf y(x.size());
+    orc_rope_ref_token(x.data(), y.data(), B, gh, gw, D, cf->enc_heads, cf->rope_base);
+    x.swap(y);
+  }
+  for (int32_t l = 0; l < cf->enc_depth; ++l)
+    encoder_block(c, "enc_blocks." + std::to_string(l), x.data(), B, N, gw);
+  layernorm_mod(c, "enc_norm", x.data(), M, D, enc);
+}
+
+void pair(const Ctx& c, const float* img1, const float* img2, int32_t B,
+          float* pts1, float* conf1, float* desc1, float* pts2, float* conf2,
+          float* desc2, float* tap_enc1, float* tap_enc2, float* tap_dec1,
+          float* tap_dec2) {
+  const orc_config* cf = c.cfg;
+  const int32_t gh = cf->img_h / cf->patch, gw = cf->img_w / cf->patch;
+  const int32_t N = gh * gw, De = cf->enc_dim, Dd = cf->dec_dim;
+  const int64_t M = (int64_t)B * N;
+  Buf e1((size_t)M * De), e2((size_t)M * De);
+  encoder(c, img1, B, e1.data());
+  encoder(c, img2, B, e2.data());
+  if (tap_enc1) memcpy(tap_enc1, e1.data(), sizeof(float) * e1.size());
+  if (tap_enc2) memcpy(tap_enc2, e2.data(), sizeof(float) * e2.size());
+  Buf d1((size_t)M * Dd), d2((size_t)M * Dd), m1, m2;
+  linear_mod(c, "decoder_embed", e1.data(), M, De, Dd, d1.data());
+  linear_mod(c, "decoder_embed", e2.data(), M, De, Dd, d2.data());
+  /* hooks: index 0 = encoder output, l = state after decoder block l */
+  Buf hook1[4], hook2[4];
+  for (int32_t l = 0; l < cf->dec_depth; ++l) {
+    m1 = d2; /* each chain attends to the other view's previous state */
+    m2 = d1;
+    decoder_block(c, "dec_blocks." + std::to_string(l), d1.data(), m1.data(), B, N, gw);
+    decoder_block(c, "dec_blocks2." + std::to_string(l), d2.data(), m2.data(), B, N, gw);
+    for (int i = 1; i < 3; ++i)
+      if (cf->dpt_hooks[i] == l + 1) {
+        hook1[i] = d1;
+        hook2[i] = d2;
+      }
+  }
+  Buf f1((size_t)M * Dd), f2((size_t)M * Dd);
+  layernorm_mod(c, "dec_norm", d1.data(), M, Dd, f1.data());
+  layernorm_mod(c, "dec_norm", d2.data(), M, Dd, f2.data());
+  if (tap_dec1) memcpy(tap_dec1, f1.data(), sizeof(float) * f1.size());
+  if (tap_dec2) memcpy(tap_dec2, f2.data(), sizeof(float) * f2.size());
+  if (!pts1 && !pts2 && !desc1 && !desc2) return;
+  const float* h1[4] = {e1.data(), hook1[1].data(), hook1[2].data(), f1.data()};
+  const float* h2[4] = {e2.data(), hook2[1].data(), hook2[2].data(), f2.data()};
+  if (pts1) dpt_head(c, "downstream_head1", h1, B, gh, gw, pts1, conf1);
+  if (pts2) dpt_head(c, "downstream_head2", h2, B, gh, gw, pts2, conf2);
+  if (desc1) local_features(c, "downstream_head1", e1.data(), f1.data(), B, gh, gw, desc1);
+  if (desc2) local_features(c, "downstream_head2", e2.data(), f2.data(), B, gh, gw, desc2);
+}
+
+}  // namespace
+
+extern "C" int32_t orc_encoder_block(const orc_config* cfg, const char* prefix,
+                                     orc_weight_fn wf, void* user, float* x,
+                                     int32_t B, int32_t grid_h, int32_t grid_w) {
+  Ctx c{cfg, wf, user};
+  encoder_block(c, prefix, x, B, grid_h * grid_w, grid_w);
+  return 0;
+}
+
+extern "C" int32_t orc_encoder(const orc_config* cfg, orc_weight_fn wf,
+                               void* user, const float* img, int32_t B,
+                               float* enc) {
+  Ctx c{cfg, wf, user};
+  encoder(c, img, B, enc);
+  return 0;
+}
+
+static int32_t check_pair_cfg(const orc_config* cf) {
+  if (cf->dpt_hooks[0] != 0 || cf->dpt_hooks[3] != cf->dec_depth) return -1;
+  if (cf->dpt_hooks[1] < 1 || cf->dpt_hooks[2] < 1) return -1;
+  const int32_t gh = cf->img_h / cf->patch, gw = cf->img_w / cf->patch;
+  if ((gh & 1) || (gw & 1)) return -1;
+  return 0;
+}
+
+extern "C" int32_t orc_mastr_pair(const orc_config* cfg, orc_weight_fn wf,
+                                  void* user, const float* img1,
+                                  const float* img2, int32_t B, float* pts1,
+                                  float* conf1, float* desc1, float* pts2,
+                                  float* conf2, float* desc2) {
+  if (check_pair_cfg(cfg)) return -1;
+  Ctx c{cfg, wf, user};
+  pair(c, img1, img2, B, pts1, conf1, desc1, pts2, conf2, desc2, nullptr, nullptr,
+       nullptr, nullptr);
+  return 0;
+}
+
+extern "C" int32_t orc_mastr_pair_taps(const orc_config* cfg, orc_weight_fn wf,
+                                       void* user, const float* img1,
+                                       const float* img2, int32_t B, float* enc1,
+                                       float* enc2, float* dec1, float* dec2) {
+  if (check_pair_cfg(cfg)) return -1;
+  Ctx c{cfg, wf, user};
+  pair(c, img1, img2, B, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, enc1,
+       enc2, dec1, dec2);
+  return 0;
+}

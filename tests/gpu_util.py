@@ -1,0 +1,50 @@
+"""Helpers for the GPU parity tests (device tensors via torch, checks vs the
+oracle)."""
+import sys
+
+import numpy as np
+import torch
+
+DEV = "cuda"
+
+# fp32 path tolerance of the north star: 1e-3 relative / 1e-4 absolute.
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def case(msg):
+    """Name the case before any GPU step, flushed, so a fault names it."""
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(DEV)
+
+
+def empty(*shape):
+    return torch.empty(shape, device=DEV, dtype=torch.float32)
+
+
+def host(t):
+    torch.cuda.synchronize()
+    return t.detach().cpu().numpy()
+
+
+def stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def assert_close(got, ref, rtol=RTOL, atol=ATOL, name=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    assert np.isfinite(got).all(), f"{name}: non-finite output"
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = err > bound
+    if bad.any():
+        i = np.unravel_index(np.argmax(err - bound), err.shape)
+        raise AssertionError(
+            f"{name}: {int(bad.sum())}/{bad.size} elements outside rtol={rtol} atol={atol}; "
+            f"worst at {i}: got {got[i]!r} ref {ref[i]!r}; max abs err {err.max():.3e}")
+    return float(err.max())

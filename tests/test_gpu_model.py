@@ -1,0 +1,172 @@
+"""Model-level parity of the graph entry points (gs_hip_mastr_*) against the
+oracle composites: config 0 (one ViT-L block), config 1 (full encoder),
+config 2 (full pair) at full size, the reduced TINY pair, and size-independent
+properties (batch invariance, determinism) for the batched configs 3/4."""
+import numpy as np
+import pytest
+import torch
+
+import gsplat_hip as G
+import pyoracle as O
+from gpu_util import assert_close, case, dev, empty, host, stream
+
+pytestmark = pytest.mark.gpu
+
+
+def weights_for(cfg, seed=0, bias_std=0.0, ln_std=0.0, prefix=None):
+    w = {}
+    for i, (n, s, k) in enumerate(G.weight_inventory(cfg)):
+        if prefix and not any(n.startswith(pf) for pf in prefix):
+            continue
+        w[n] = G.weight_values(cfg, i, int(np.prod(s)), seed, bias_std, ln_std).reshape(s)
+    return w
+
+
+def load_ctx(cfg, w, max_pairs=1):
+    m = G.Mastr(cfg, max_pairs)
+    m.init_seeded(0)
+    for n, a in w.items():
+        m.set_weight(n, a)
+    return m
+
+
+@pytest.mark.parametrize("variant", ["spec", "biased", "literal"])
+def test_config0_encoder_block(variant):
+    """Config 0: one ViT-L block, 768 tokens on the 24x32 grid, RoPE2D base 100,
+    eps 1e-6, N(0,0.02) weights; 'biased' adds nonzero biases and LN affine
+    so those epilogues are exercised; 'literal' uses the reference CPU
+    path's linear layout (D1)."""
+    case(f"config0 block {variant}")
+    cfg = G.default_config(enc_depth=1, dec_depth=1, linear_layout=1 if variant == "literal" else 0)
+    bias_std, ln_std = (0.02, 0.1) if variant == "biased" else (0.0, 0.0)
+    w = weights_for(cfg, 0, bias_std, ln_std, prefix=["enc_blocks.0."])
+    x = G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)
+    ref = O.encoder_block(cfg.as_dict(), w, "enc_blocks.0", x, 24, 32)
+    m = load_ctx(cfg, w)
+    xd = dev(x)
+    m.encoder_block(0, xd, 1, stream())
+    err = assert_close(host(xd), ref, name="config0")
+    print(f"config0 {variant}: max abs err {err:.3e}")
+    m.close()
+
+
+def test_config1_encoder():
+    """Config 1: full ViT-L encoder (24 blocks + enc_norm) on one 384x512 image."""
+    case("config1 encoder")
+    cfg = G.default_config()
+    w = weights_for(cfg, prefix=["patch_embed.", "enc_blocks.", "enc_norm."])
+    img = G.seed_uniform(0, "view1", 3 * 384 * 512, -1.0, 1.0).reshape(1, 3, 384, 512)
+    ref = O.encoder(cfg.as_dict(), w, img)
+    m = G.Mastr(cfg, 1)
+    m.init_seeded(0)
+    enc = empty(1, 768, 1024)
+    m.encoder(dev(img), 1, enc, stream())
+    err = assert_close(host(enc), ref, name="config1")
+    print(f"config1: max abs err {err:.3e}")
+    m.close()
+
+
+def run_pair(m, cfg, img1, img2, B):
+    H, W = cfg.img_h, cfg.img_w
+    out = {}
+    for v in (1, 2):
+        out[f"pts{v}"] = empty(B, H, W, 3)
+        out[f"conf{v}"] = empty(B, H, W, 1)
+        out[f"desc{v}"] = empty(B, H, W, cfg.desc_dim)
+    m.pair(dev(img1), dev(img2), B, out["pts1"], out["conf1"], out["desc1"], out["pts2"],
+           out["conf2"], out["desc2"], stream())
+    return {k: host(v) for k, v in out.items()}
+
+
+def check_pair(got, ref, tag):
+    for k in ("pts1", "conf1", "desc1", "pts2", "conf2", "desc2"):
+        err = assert_close(got[k], ref[k], name=f"{tag} {k}")
+        print(f"{tag} {k}: max abs err {err:.3e}, |ref| max {np.abs(ref[k]).max():.3e}")
+
+
+def test_tiny_pair_parity_and_taps(tiny_cfg):
+    case("tiny pair")
+    cfg = G.default_config(**tiny_cfg)
+    w = weights_for(cfg, 0, bias_std=0.02, ln_std=0.1)
+    B = 2
+    n = B * 3 * cfg.img_h * cfg.img_w
+    i1 = G.seed_uniform(0, "view1", n).reshape(B, 3, cfg.img_h, cfg.img_w)
+    i2 = G.seed_uniform(0, "view2", n).reshape(B, 3, cfg.img_h, cfg.img_w)
+    m = load_ctx(cfg, w, max_pairs=B)
+    got = run_pair(m, cfg, i1, i2, B)
+    d = cfg.as_dict()
+    check_pair(got, O.mastr_pair(d, w, i1, i2), "tiny")
+    e1, e2, d1, d2 = O.mastr_pair_taps(d, w, i1, i2)
+    N = (cfg.img_h // 16) * (cfg.img_w // 16)
+    te = [empty(B, N, cfg.enc_dim) for _ in range(2)]
+    td = [empty(B, N, cfg.dec_dim) for _ in range(2)]
+    m.pair_taps(B, te[0], te[1], td[0], td[1], stream())
+    for got_t, ref_t, nm in zip(te + td, [e1, e2, d1, d2], ["enc1", "enc2", "dec1", "dec2"]):
+        assert_close(host(got_t), ref_t, name=nm)
+    m.close()
+
+
+def test_tiny_batch_invariance_and_determinism(tiny_cfg):
+    """Pair p of a batch equals the same pair run alone, bit for bit, and a
+    rerun is bit-identical (no split reductions, no atomics)."""
+    case("tiny batch invariance")
+    cfg = G.default_config(**tiny_cfg)
+    B = 3
+    n = B * 3 * cfg.img_h * cfg.img_w
+    i1 = G.seed_uniform(1, "view1", n).reshape(B, 3, cfg.img_h, cfg.img_w)
+    i2 = G.seed_uniform(1, "view2", n).reshape(B, 3, cfg.img_h, cfg.img_w)
+    m = G.Mastr(cfg, B)
+    m.init_seeded(0, 0.02, 0.1)
+    full = run_pair(m, cfg, i1, i2, B)
+    again = run_pair(m, cfg, i1, i2, B)
+    for k in full:
+        np.testing.assert_array_equal(full[k], again[k])
+    for b in (0, B - 1):
+        one = run_pair(m, cfg, i1[b:b + 1], i2[b:b + 1], 1)
+        for k in full:
+            np.testing.assert_array_equal(one[k][0], full[k][b], err_msg=f"{k} pair {b}")
+    m.close()
+
+
+def test_config2_full_pair():
+    """Config 2: full MASt3R two-view inference at 384x512, seed-0 weights."""
+    case("config2 full pair")
+    cfg = G.default_config()
+    w = weights_for(cfg)
+    n = 3 * 384 * 512
+    i1 = G.seed_uniform(0, "view1", n).reshape(1, 3, 384, 512)
+    i2 = G.seed_uniform(0, "view2", n).reshape(1, 3, 384, 512)
+    m = G.Mastr(cfg, 1)
+    m.init_seeded(0)
+    got = run_pair(m, cfg, i1, i2, 1)
+    m.close()
+    del m
+    torch.cuda.empty_cache()
+    O.set_threads(0)
+    ref = O.mastr_pair(cfg.as_dict(), w, i1, i2)
+    check_pair(got, ref, "config2")
+
+
+def test_view_swap_symmetry_full_size():
+    """With the second decoder chain and head sharing the first's weights,
+    swapping the views swaps the outputs (bit for bit) at the config-2 size."""
+    case("config2 view swap")
+    cfg = G.default_config(enc_depth=2, dec_depth=2, dpt_hooks=[0, 1, 2, 2])
+    inv = G.weight_inventory(cfg)
+    m = G.Mastr(cfg, 1)
+    w = {}
+    for i, (nme, s, k) in enumerate(inv):
+        src = nme.replace("dec_blocks2.", "dec_blocks.").replace("downstream_head2.",
+                                                                  "downstream_head1.")
+        j = [x[0] for x in inv].index(src)
+        a = G.weight_values(cfg, j, int(np.prod(s)), 0, 0.02, 0.1)
+        m.set_weight(nme, a)
+    n = 3 * 384 * 512
+    i1 = G.seed_uniform(3, "view1", n).reshape(1, 3, 384, 512)
+    i2 = G.seed_uniform(3, "view2", n).reshape(1, 3, 384, 512)
+    a = run_pair(m, cfg, i1, i2, 1)
+    b = run_pair(m, cfg, i2, i1, 1)
+    for k in ("pts", "conf", "desc"):
+        np.testing.assert_array_equal(a[k + "1"], b[k + "2"])
+        np.testing.assert_array_equal(a[k + "2"], b[k + "1"])
+    m.close()

@@ -1,0 +1,234 @@
+"""Per-op parity of the HIP kernels (through the C ABI) against the oracle,
+at the shapes the MASt3R configs use and at ragged edge shapes."""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+import gsplat_hip as G
+import pyoracle as O
+from gpu_util import assert_close, case, dev, empty, host, stream
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(7)
+
+
+def rnd(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+def L():
+    return G.lib()
+
+
+def p(t):
+    return G.ptr(t)
+
+
+# ---------------------------------------------------------------- linear
+
+LINEAR_CASES = [
+    # config-0 shapes (M = 768 tokens)
+    (768, 1024, 3072), (768, 1024, 1024), (768, 1024, 4096), (768, 4096, 1024),
+    # decoder / embed / descriptor shapes
+    (768, 768, 2304), (768, 3072, 768), (768, 1024, 768), (300, 1792, 7168),
+    # ragged
+    (1, 32, 32), (37, 64, 100), (129, 96, 130),
+]
+
+
+@pytest.mark.parametrize("M,K,N", LINEAR_CASES)
+def test_linear_parity(M, K, N):
+    case(f"linear M={M} K={K} N={N}")
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.02), rnd(N, scale=0.1)
+    y = empty(M, N)
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, 0, 0, None,
+                              stream()))
+    assert_close(host(y), O.linear(x, W, b), name="linear")
+
+
+@pytest.mark.parametrize("epi", ["gelu", "residual", "relu", "nobias"])
+def test_linear_epilogues(epi):
+    case(f"linear epilogue {epi}")
+    M, K, N = 200, 256, 384
+    x, W, b, r = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1), rnd(M, N)
+    ref = O.linear(x, W, None if epi == "nobias" else b)
+    flags = 0
+    if epi == "gelu":
+        flags, ref = G.EPI_GELU, O.gelu(ref)
+    elif epi == "relu":
+        flags, ref = G.EPI_RELU, np.maximum(ref, 0)
+    elif epi == "residual":
+        flags, ref = G.EPI_RESIDUAL, r + ref
+    y = dev(r) if epi == "residual" else empty(M, N)  # residual in place
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), None if epi == "nobias" else p(dev(b)), p(y),
+                              M, K, N, 0, flags, p(y) if epi == "residual" else None, stream()))
+    assert_close(host(y), ref, name=epi)
+
+
+@pytest.mark.parametrize("M,K,N", [(768, 1024, 1024), (50, 64, 96)])
+def test_linear_literal_layout(M, K, N):
+    # D1: the reference CPU path's [out,in] buffer read as [in,out]
+    case(f"linear literal M={M} K={K} N={N}")
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.02), rnd(N, scale=0.1)
+    y = empty(M, N)
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, 1, 0, None,
+                              stream()))
+    assert_close(host(y), O.linear(x, W, b, layout=1), name="literal")
+
+
+def test_linear_rejects_bad_shapes_without_launch():
+    case("linear validation")
+    x = empty(4, 33)
+    rc = L().gs_hip_linear(p(x), p(x), None, p(x), 4, 33, 4, 0, 0, None, stream())
+    assert rc != 0 and b"multiple of 32" in L().gs_hip_last_error()
+    rc = L().gs_hip_linear(p(x), p(x), None, p(x), 4, 32, 4, 2, 0, None, stream())
+    assert rc != 0
+
+
+# ---------------------------------------------------------------- layernorm
+
+
+@pytest.mark.parametrize("rows,D", [(768, 1024), (1536, 768), (5, 132), (3, 4096)])
+def test_layernorm_parity(rows, D):
+    case(f"layernorm rows={rows} D={D}")
+    x, g, b = rnd(rows, D, scale=2.0) + 0.5, rnd(D, scale=0.2) + 1, rnd(D, scale=0.2)
+    y = empty(rows, D)
+    G.check(L().gs_hip_layernorm(p(dev(x)), p(dev(g)), p(dev(b)), p(y), rows, D, 1e-6, stream()))
+    assert_close(host(y), O.layernorm(x, g, b, 1e-6), name="layernorm")
+
+
+# ---------------------------------------------------------------- attention
+
+
+def attn_call(q, k, v, o, B, H, Nq, Nkv, qs, ks, vs, os_):
+    G.check(L().gs_hip_attention(p(q), p(k), p(v), p(o), B, H, Nq, Nkv, 64, 0.125, *qs, *ks, *vs,
+                                 *os_, stream()))
+
+
+@pytest.mark.parametrize("B,H,Nq,Nkv", [(2, 16, 768, 768), (1, 12, 768, 768), (1, 2, 100, 77),
+                                        (2, 3, 1, 5), (1, 1, 33, 1024)])
+def test_attention_token_major(B, H, Nq, Nkv):
+    case(f"attention token-major B={B} H={H} Nq={Nq} Nkv={Nkv}")
+    D = H * 64
+    q, k, v = rnd(B, Nq, D), rnd(B, Nkv, D), rnd(B, Nkv, D)
+    o = empty(B, Nq, D)
+    attn_call(dev(q), dev(k), dev(v), o, B, H, Nq, Nkv, (Nq * D, 64, D), (Nkv * D, 64, D),
+              (Nkv * D, 64, D), (Nq * D, 64, D))
+    sh = lambda a, n: a.reshape(B, n, H, 64).transpose(0, 2, 1, 3)
+    ref = O.sdpa(sh(q, Nq), sh(k, Nkv), sh(v, Nkv)).transpose(0, 2, 1, 3).reshape(B, Nq, D)
+    assert_close(host(o), ref, name="attention")
+
+
+def test_attention_bhnd_layout_and_large_scores():
+    # the reference GPU layout [B*H, N, 64] (src/nn/gpu_ops.cr:200-227) and
+    # scores large enough that an unstabilised softmax would overflow
+    case("attention BHND layout")
+    B, H, N = 2, 3, 130
+    q, k, v = rnd(B, H, N, 64, scale=4.0), rnd(B, H, N, 64, scale=4.0), rnd(B, H, N, 64)
+    o = empty(B, H, N, 64)
+    st = (H * N * 64, N * 64, 64)
+    attn_call(dev(q), dev(k), dev(v), o, B, H, N, N, st, st, st, st)
+    assert_close(host(o), O.sdpa(q, k, v), name="attention bhnd")
+
+
+def test_attention_rejects_bad_head_dim():
+    case("attention validation")
+    x = empty(64)
+    rc = L().gs_hip_attention(p(x), p(x), p(x), p(x), 1, 1, 1, 1, 32, 0.1, *([0] * 12), stream())
+    assert rc != 0 and b"head_dim" in L().gs_hip_last_error()
+
+
+# ---------------------------------------------------------------- rope
+
+
+@pytest.mark.parametrize("gh,gw,H", [(24, 32, 16), (3, 5, 2)])
+def test_rope2d_parity(gh, gw, H):
+    case(f"rope2d {gh}x{gw} H={H}")
+    B, N = 2, gh * gw
+    ld = 3 * H * 64
+    t = rnd(B, N, ld)
+    td = dev(t)
+    G.check(L().gs_hip_rope2d(p(td), B, N, H, ld, gw, 100.0, stream()))
+    ref = t.copy()
+    ref[:, :, :H * 64] = O.rope2d(t[:, :, :H * 64].copy(), H, gw, 100.0)
+    assert_close(host(td), ref, rtol=1e-5, atol=1e-6, name="rope2d")
+
+
+# ---------------------------------------------------------------- convolutions
+
+CONV_CASES = [
+    # (B, H, W, Cin, Cout, k, s, p, flags, residual)
+    (1, 12, 16, 256, 256, 3, 1, 1, 0, False),        # RCU at 1/32
+    (1, 24, 32, 768, 768, 3, 2, 1, 0, False),         # act_postprocess 3.1
+    (2, 96, 128, 96, 256, 3, 1, 1, 0, False),         # layer1_rn
+    (1, 48, 64, 256, 256, 3, 1, 1, G.CONV_RELU_IN | G.CONV_RELU_OUT, False),  # RCU conv1
+    (1, 48, 64, 256, 256, 3, 1, 1, 0, True),          # RCU conv2 + residual
+    (1, 24, 32, 1024, 96, 1, 1, 0, 0, False),         # act_postprocess 0.0 (1x1)
+    (1, 7, 9, 64, 40, 3, 2, 1, 0, False),             # ragged
+    (3, 5, 6, 32, 4, 1, 1, 0, 0, False),              # head.4-like tiny Cout
+]
+
+
+@pytest.mark.parametrize("B,H,W,Cin,Cout,k,s,pd,flags,res", CONV_CASES)
+def test_conv2d_parity(B, H, W, Cin, Cout, k, s, pd, flags, res):
+    case(f"conv2d B={B} {H}x{W} {Cin}->{Cout} k={k} s={s} p={pd} flags={flags} res={res}")
+    x, w, b = rnd(B, H, W, Cin), rnd(Cout, Cin, k, k, scale=0.05), rnd(Cout, scale=0.1)
+    Ho, Wo = (H + 2 * pd - k) // s + 1, (W + 2 * pd - k) // s + 1
+    r = rnd(B, Ho, Wo, Cout)
+    xin = np.maximum(x, 0) if flags & G.CONV_RELU_IN else x
+    ref = O.conv2d(xin, w, b, s, pd)
+    if flags & G.CONV_RELU_OUT:
+        ref = np.maximum(ref, 0)
+    if res:
+        ref = ref + r
+    y = empty(B, Ho, Wo, Cout)
+    G.check(L().gs_hip_conv2d(p(dev(x)), B, H, W, Cin, p(dev(w)), p(dev(b)), p(y), Cout, k, s, pd,
+                              0, flags, p(dev(r)) if res else None, stream()))
+    assert_close(host(y), ref, name="conv2d")
+
+
+@pytest.mark.parametrize("Cin,Cout,k,H,W", [(96, 96, 4, 24, 32), (192, 192, 2, 24, 32),
+                                            (32, 64, 2, 3, 5)])
+def test_conv_transpose_parity(Cin, Cout, k, H, W):
+    case(f"conv_transpose {Cin}->{Cout} k={k} {H}x{W}")
+    B = 2
+    x, w, b = rnd(B, H, W, Cin), rnd(Cin, Cout, k, k, scale=0.05), rnd(Cout, scale=0.1)
+    y = empty(B, H * k, W * k, Cout)
+    G.check(L().gs_hip_conv_transpose(p(dev(x)), B, H, W, Cin, p(dev(w)), p(dev(b)), p(y), Cout, k,
+                                      stream()))
+    assert_close(host(y), O.conv_transpose(x, w, b, k), name="convT")
+
+
+@pytest.mark.parametrize("B,H,W,C", [(1, 96, 128, 256), (2, 5, 7, 8)])
+def test_upsample_parity(B, H, W, C):
+    case(f"upsample2x {B}x{H}x{W}x{C}")
+    x = rnd(B, H, W, C)
+    y = empty(B, 2 * H, 2 * W, C)
+    G.check(L().gs_hip_upsample2x(p(dev(x)), B, H, W, C, p(y), stream()))
+    assert_close(host(y), O.upsample2x(x), rtol=1e-5, atol=1e-6, name="upsample")
+
+
+def test_buffer_api_roundtrip():
+    case("gs_* buffer api")
+    Lb = L()
+    assert Lb.gs_init_device() == 0
+    assert Lb.gs_has_unified_memory() == 0
+    assert Lb.gs_recommended_working_set_size() > 0
+    n = 1000
+    a = rnd(n)
+    h1 = Lb.gs_create_buffer(4 * n, 0)
+    h2 = Lb.gs_create_buffer(4 * n, 0)
+    assert h1 and h2
+    Lb.gs_buffer_write(h1, a.ctypes.data_as(C.c_void_p), 4 * n)
+    Lb.gs_buffer_copy(h1, h2, 4 * n)
+    Lb.gs_synchronize()
+    out = np.empty_like(a)
+    Lb.gs_buffer_read(h2, out.ctypes.data_as(C.c_void_p), 4 * n)
+    np.testing.assert_array_equal(out, a)
+    assert Lb.gs_buffer_contents(h1)
+    Lb.gs_release_buffer(h1)
+    Lb.gs_release_buffer(h2)
+    assert Lb.gs_create_buffer(0, 0) is None

@@ -1,0 +1,363 @@
+"""Pins the CPU oracle (oracle/) before it is trusted as the parity checker.
+
+Each check is chosen so a plausible mistake (dropped term, wrong index, wrong
+sign, transposed operand) fails it: fp64 brute force written independently of
+the oracle's loops, closed forms, invariants, torch CPU as an independent
+implementation, and bit-equality of the blocked loops with the literal
+reference loop order.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import pyoracle as O
+
+RNG = np.random.default_rng(1234)
+
+
+def rnd(*shape, scale=1.0):
+    return (RNG.standard_normal(shape) * scale).astype(np.float32)
+
+
+# ---------------------------------------------------------------- Linear
+
+
+@pytest.mark.parametrize("M,K,N", [(4, 8, 6), (37, 64, 129), (8, 257, 33)])
+def test_linear_fp64_bruteforce(M, K, N):
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.1), rnd(N)
+    ref = x.astype(np.float64) @ W.astype(np.float64).T + b
+    y = O.linear(x, W, b)
+    np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("layout", [0, 1])
+@pytest.mark.parametrize("M,K,N", [(3, 5, 7), (19, 64, 300), (9, 33, 257)])
+def test_linear_blocked_equals_reference_loop(M, K, N, layout):
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.1), rnd(N)
+    np.testing.assert_array_equal(O.linear(x, W, b, layout), O.linear(x, W, b, layout, naive=True))
+    np.testing.assert_array_equal(O.linear(x, W, None, layout),
+                                  O.linear(x, W, None, layout, naive=True))
+
+
+def test_linear_literal_layout_identity():
+    # D1: the reference CPU path reads the [out,in] buffer as [in,out]:
+    # literal(W) == standard(reshape(W, [K, N])^T), bit for bit.
+    M, K, N = 7, 12, 20
+    x, W, b = rnd(M, K), rnd(N, K), rnd(N)
+    lit = O.linear(x, W, b, layout=1)
+    std = O.linear(x, np.ascontiguousarray(W.reshape(K, N).T), b, layout=0)
+    np.testing.assert_array_equal(lit, std)
+    # and it is NOT x W^T (the quirk is real)
+    assert not np.allclose(lit, O.linear(x, W, b, layout=0), atol=1e-3)
+
+
+def test_linear_identity_and_zero_weights():
+    x = rnd(5, 16)
+    np.testing.assert_array_equal(O.linear(x, np.eye(16, dtype=np.float32)), x)
+    b = rnd(9)
+    np.testing.assert_array_equal(O.linear(x, np.zeros((9, 16), np.float32), b),
+                                  np.broadcast_to(b, (5, 9)))
+
+
+def test_linear_torch():
+    x, W, b = rnd(33, 128), rnd(96, 128, scale=0.05), rnd(96)
+    ref = F.linear(torch.from_numpy(x), torch.from_numpy(W), torch.from_numpy(b)).numpy()
+    np.testing.assert_allclose(O.linear(x, W, b), ref, rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- LayerNorm
+
+
+def test_layernorm_closed_form_two_values():
+    a, c, eps = 3.0, -1.0, 1e-6
+    x = np.array([[a, c]], np.float32)
+    y = O.layernorm(x, np.ones(2, np.float32), np.zeros(2, np.float32), eps)
+    # mean = 1, var = 4 -> (x - 1)/sqrt(4 + eps)
+    np.testing.assert_allclose(y, [[2 / np.sqrt(4 + eps), -2 / np.sqrt(4 + eps)]], rtol=1e-6)
+
+
+def test_layernorm_constant_row_gives_beta_and_affine():
+    D = 64
+    g, b = rnd(D), rnd(D)
+    y = O.layernorm(np.full((3, D), 7.25, np.float32), g, b, 1e-6)
+    np.testing.assert_array_equal(y, np.broadcast_to(b, (3, D)))
+    x = rnd(50, D, scale=3.0) + 5
+    y1 = O.layernorm(x, np.ones(D, np.float32), np.zeros(D, np.float32), 1e-6)
+    np.testing.assert_allclose(y1.mean(-1), 0, atol=1e-5)
+    np.testing.assert_allclose(y1.var(-1), 1, atol=1e-4)
+    ref = F.layer_norm(torch.from_numpy(x), (D,), torch.from_numpy(g), torch.from_numpy(b), 1e-6)
+    np.testing.assert_allclose(O.layernorm(x, g, b, 1e-6), ref.numpy(), rtol=1e-5, atol=1e-5)
+
+
+# ---------------------------------------------------------------- GELU
+
+
+def test_gelu_known_values_and_torch():
+    x = np.array([0.0, 3.0, -3.0, 1.0], np.float32)
+    y = O.gelu(x)
+    assert y[0] == 0.0
+    # gelu(x) - gelu(-x) == x for the tanh form
+    np.testing.assert_allclose(y[1] - y[2], 3.0, rtol=1e-6)
+    # tanh-form value at 1: 0.5*(1+tanh(sqrt(2/pi)*1.044715)) = 0.8411920
+    np.testing.assert_allclose(y[3], 0.8411920, rtol=2e-6)
+    z = rnd(1000, scale=3)
+    ref = F.gelu(torch.from_numpy(z), approximate="tanh").numpy()
+    np.testing.assert_allclose(O.gelu(z), ref, rtol=1e-5, atol=1e-6)
+
+
+# ---------------------------------------------------------------- attention
+
+
+def sdpa64(q, k, v, scale):
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    s = np.einsum("bhid,bhjd->bhij", q, k) * scale
+    s = np.exp(s - s.max(-1, keepdims=True))
+    s /= s.sum(-1, keepdims=True)
+    return np.einsum("bhij,bhjd->bhid", s, v)
+
+
+@pytest.mark.parametrize("Nq,Nkv,hd", [(5, 5, 8), (4, 6, 8), (33, 70, 64)])
+def test_sdpa_fp64_and_torch(Nq, Nkv, hd):
+    q, k, v = rnd(2, 3, Nq, hd), rnd(2, 3, Nkv, hd), rnd(2, 3, Nkv, hd)
+    sc = 1.0 / np.sqrt(hd)
+    o = O.sdpa(q, k, v)
+    np.testing.assert_allclose(o, sdpa64(q, k, v, sc), rtol=1e-5, atol=1e-5)
+    ref = F.scaled_dot_product_attention(torch.from_numpy(q), torch.from_numpy(k),
+                                         torch.from_numpy(v)).numpy()
+    np.testing.assert_allclose(o, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_sdpa_zero_query_is_mean_and_dominant_is_onehot():
+    k, v = rnd(1, 2, 9, 16), rnd(1, 2, 9, 16)
+    o = O.sdpa(np.zeros((1, 2, 3, 16), np.float32), k, v)
+    np.testing.assert_allclose(o, np.broadcast_to(v.mean(2, keepdims=True), o.shape), atol=1e-6)
+    kd = np.zeros((1, 1, 5, 16), np.float32)
+    kd[0, 0, 3, 0] = 1.0
+    q = np.zeros((1, 1, 1, 16), np.float32)
+    q[0, 0, 0, 0] = 400.0
+    vd = rnd(1, 1, 5, 16)
+    np.testing.assert_allclose(O.sdpa(q, kd, vd)[0, 0, 0], vd[0, 0, 3], atol=1e-6)
+
+
+# ---------------------------------------------------------------- RoPE 2D
+
+
+def test_rope_identity_at_origin_and_norm_preserving():
+    H, gw = 2, 3
+    t = rnd(1, 6, H * 64)
+    r = O.rope2d(t, H, gw, 100.0)
+    np.testing.assert_array_equal(r[0, 0], t[0, 0])  # token 0 sits at (0, 0)
+    # each rotated pair (j, j+16) of each axis-half keeps its norm
+    tt = t.reshape(1, 6, H, 2, 2, 16)
+    rr = r.reshape(1, 6, H, 2, 2, 16)
+    np.testing.assert_allclose((rr ** 2).sum(4), (tt ** 2).sum(4), rtol=1e-5)
+
+
+def test_rope_relative_position_invariance():
+    # q.k after rotation depends only on the position difference.
+    gw, gh = 5, 4
+    H = 1
+    q, k = rnd(64), rnd(64)
+
+    def rot_at(vec, y, x):
+        t = np.zeros((1, gh * gw, 64), np.float32)
+        t[0, y * gw + x] = vec
+        return O.rope2d(t, H, gw, 100.0)[0, y * gw + x].astype(np.float64)
+
+    d1 = rot_at(q, 1, 1) @ rot_at(k, 2, 3)
+    d2 = rot_at(q, 2, 2) @ rot_at(k, 3, 4)
+    d3 = rot_at(q, 0, 0) @ rot_at(k, 1, 2)
+    np.testing.assert_allclose([d1, d2], [d3, d3], rtol=1e-4, atol=1e-5)
+
+
+def test_rope_frequency_schedule_known_answer():
+    # unit vector in pair j=1 of the y half at row y=1: angle = 100^(-2/32)
+    gw = 2
+    t = np.zeros((1, 4, 64), np.float32)
+    t[0, 2, 1] = 1.0  # token 2 = (y=1, x=0), dim 1 (pair (1, 17))
+    r = O.rope2d(t, 1, gw, 100.0)[0, 2]
+    th = 100.0 ** (-2.0 / 32.0)
+    np.testing.assert_allclose([r[1], r[17]], [np.cos(th), np.sin(th)], rtol=1e-6)
+    # x half: dim 32+3 at column x=1 (token 1), angle = 100^(-6/32)
+    t = np.zeros((1, 4, 64), np.float32)
+    t[0, 1, 35] = 1.0
+    r = O.rope2d(t, 1, gw, 100.0)[0, 1]
+    th = 100.0 ** (-6.0 / 32.0)
+    np.testing.assert_allclose([r[35], r[51]], [np.cos(th), np.sin(th)], rtol=1e-6)
+
+
+def test_rope_brute_force_2x3():
+    # complex-multiplication statement of the rotation on a 2x3 grid
+    H, gh, gw = 1, 2, 3
+    t = rnd(1, gh * gw, 64)
+    r = O.rope2d(t, H, gw, 100.0)
+    for n in range(gh * gw):
+        y, x = divmod(n, gw)
+        for ax, pos in ((0, y), (1, x)):
+            u = t[0, n, ax * 32:(ax + 1) * 32].astype(np.float64)
+            z = (u[:16] + 1j * u[16:]) * np.exp(1j * pos * 100.0 ** (-np.arange(16) * 2 / 32))
+            np.testing.assert_allclose(r[0, n, ax * 32:ax * 32 + 16], z.real, atol=2e-6)
+            np.testing.assert_allclose(r[0, n, ax * 32 + 16:(ax + 1) * 32], z.imag, atol=2e-6)
+
+
+def test_rope_ref_token_known_cases():
+    # reference token RoPE (src/mastr/encoder_v2.cr:204-254): identity at (0,0)
+    x = rnd(1, 4, 128)
+    y = O.rope_ref_token(x, 2, 2, 2, 100.0)
+    np.testing.assert_array_equal(y[0, 0], x[0, 0])
+    # token (y=1, x=0), head 0, dim 0: x0*cos(f0) - x32*sin(f0), f0 = 1
+    np.testing.assert_allclose(y[0, 2, 0], x[0, 2, 0] * np.cos(1.0) - x[0, 2, 32] * np.sin(1.0),
+                               rtol=1e-5)
+    # x-half of token (0, 1), dim 32+1: x1*sin(f1) + x33*cos(f1), f1 = 100^(-2/64)
+    f1 = 100.0 ** (-2.0 / 64.0)
+    np.testing.assert_allclose(y[0, 1, 33], x[0, 1, 1] * np.sin(f1) + x[0, 1, 33] * np.cos(f1),
+                               rtol=1e-5)
+
+
+# ---------------------------------------------------------------- conv & resampling
+
+
+@pytest.mark.parametrize("k,s,p", [(3, 1, 1), (3, 2, 1), (1, 1, 0), (4, 4, 0)])
+def test_conv_blocked_equals_reference_loop_and_torch(k, s, p):
+    x, w, b = rnd(2, 9, 11, 32), rnd(40, 32, k, k, scale=0.1), rnd(40)
+    y = O.conv2d(x, w, b, s, p)
+    np.testing.assert_array_equal(y, O.conv2d(x, w, b, s, p, naive=True))
+    ref = F.conv2d(torch.from_numpy(x).permute(0, 3, 1, 2), torch.from_numpy(w),
+                   torch.from_numpy(b), stride=s, padding=p).permute(0, 2, 3, 1).numpy()
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_conv_1x1_is_linear_and_delta_kernel_is_identity():
+    x, w, b = rnd(1, 5, 7, 32), rnd(24, 32, 1, 1), rnd(24)
+    np.testing.assert_array_equal(O.conv2d(x, w, b),
+                                  O.linear(x.reshape(-1, 32), w.reshape(24, 32), b).reshape(1, 5, 7, 24))
+    d = np.zeros((32, 32, 3, 3), np.float32)
+    d[np.arange(32), np.arange(32), 1, 1] = 1.0
+    np.testing.assert_array_equal(O.conv2d(x, d, None, 1, 1), x)
+
+
+@pytest.mark.parametrize("k", [2, 4])
+def test_conv_transpose_torch_and_gemm_identity(k):
+    x, w, b = rnd(2, 3, 5, 32), rnd(32, 48, k, k, scale=0.1), rnd(48)
+    y = O.conv_transpose(x, w, b, k)
+    ref = F.conv_transpose2d(torch.from_numpy(x).permute(0, 3, 1, 2), torch.from_numpy(w),
+                             torch.from_numpy(b), stride=k).permute(0, 2, 3, 1).numpy()
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-5)
+    g = x.reshape(-1, 32).astype(np.float64) @ w.reshape(32, -1).astype(np.float64)
+    g = g.reshape(2, 3, 5, 48, k, k).transpose(0, 1, 4, 2, 5, 3).reshape(2, 3 * k, 5 * k, 48) + b
+    np.testing.assert_allclose(y, g, rtol=1e-5, atol=1e-5)
+
+
+def test_upsample_exact_fields_and_torch():
+    H, W, Cc = 5, 7, 8
+    const = np.full((1, H, W, Cc), 2.5, np.float32)
+    np.testing.assert_array_equal(O.upsample2x(const), np.full((1, 2 * H, 2 * W, Cc), 2.5))
+    yy, xx = np.meshgrid(np.arange(H), np.arange(W), indexing="ij")
+    aff = (0.5 * yy - 0.25 * xx + 1.0).astype(np.float32)[None, :, :, None].repeat(Cc, 3)
+    up = O.upsample2x(aff)
+    oy, ox = np.meshgrid(np.arange(2 * H) * (H - 1) / (2 * H - 1),
+                         np.arange(2 * W) * (W - 1) / (2 * W - 1), indexing="ij")
+    np.testing.assert_allclose(up[0, :, :, 0], 0.5 * oy - 0.25 * ox + 1.0, atol=1e-5)
+    x = rnd(2, H, W, Cc)
+    u = O.upsample2x(x)
+    for (a, b) in ((0, 0), (0, -1), (-1, 0), (-1, -1)):
+        np.testing.assert_array_equal(u[:, a, b], x[:, a, b])
+    ref = F.interpolate(torch.from_numpy(x).permute(0, 3, 1, 2), scale_factor=2, mode="bilinear",
+                        align_corners=True).permute(0, 2, 3, 1).numpy()
+    np.testing.assert_allclose(u, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_pixel_shuffle_and_unfold_torch():
+    h, w, r, Cout = 3, 4, 4, 5
+    f = rnd(2, h * w, (Cout + 1) * r * r)
+    ps = O.pixel_shuffle(f, h, w, r, Cout)
+    t = torch.from_numpy(f).reshape(2, h, w, -1).permute(0, 3, 1, 2)
+    ref = F.pixel_shuffle(t, r).permute(0, 2, 3, 1).numpy()[..., :Cout]
+    np.testing.assert_array_equal(ps, ref)
+    img = rnd(2, 3, 32, 48)
+    u = O.unfold(img, 16)
+    ref = F.unfold(torch.from_numpy(img), 16, stride=16).transpose(1, 2).numpy()
+    np.testing.assert_array_equal(u, ref)
+
+
+# ---------------------------------------------------------------- composites
+
+
+def torch_block(x, w, p, H, gw, eps):
+    """Encoder block composed from torch CPU ops (independent of the oracle)."""
+    t = torch.from_numpy
+
+    def rope(z):
+        B, N, D = z.shape
+        z = z.reshape(B, N, H, 2, 2, 16).clone()
+        n = torch.arange(N)
+        pos = torch.stack([n // gw, n % gw], 1).double()  # (y, x)
+        inv = 100.0 ** (-torch.arange(16).double() * 2 / 32)
+        ang = pos[:, :, None] * inv  # N, 2, 16
+        c, s = torch.cos(ang).float(), torch.sin(ang).float()
+        a, b = z[..., 0, :], z[..., 1, :]
+        c = c[None, :, None]
+        s = s[None, :, None]
+        out = torch.stack([a * c - b * s, b * c + a * s], -2)
+        return out.reshape(B, N, D)
+
+    D = x.shape[-1]
+    xx = t(x)
+    h = F.layer_norm(xx, (D,), t(w[p + ".norm1.weight"]), t(w[p + ".norm1.bias"]), eps)
+    qkv = F.linear(h, t(w[p + ".attn.qkv.weight"]), t(w[p + ".attn.qkv.bias"]))
+    q, k, v = qkv.split(D, -1)
+    q, k = rope(q), rope(k)
+    B, N, _ = q.shape
+    sh = lambda z: z.reshape(B, N, H, 64).transpose(1, 2)
+    a = F.scaled_dot_product_attention(sh(q), sh(k), sh(v)).transpose(1, 2).reshape(B, N, D)
+    xx = xx + F.linear(a, t(w[p + ".attn.proj.weight"]), t(w[p + ".attn.proj.bias"]))
+    h = F.layer_norm(xx, (D,), t(w[p + ".norm2.weight"]), t(w[p + ".norm2.bias"]), eps)
+    m = F.gelu(F.linear(h, t(w[p + ".mlp.fc1.weight"]), t(w[p + ".mlp.fc1.bias"])),
+               approximate="tanh")
+    return (xx + F.linear(m, t(w[p + ".mlp.fc2.weight"]), t(w[p + ".mlp.fc2.bias"]))).numpy()
+
+
+@pytest.fixture(scope="module")
+def tiny_weights(tiny_cfg):
+    import gsplat_hip as G
+    cfg = G.default_config(**tiny_cfg)
+    return G.seeded_weights(cfg, seed=0, bias_std=0.02, ln_std=0.1)
+
+
+def test_encoder_block_matches_torch_composition(tiny_cfg, tiny_weights):
+    gh, gw = 4, 6
+    x = rnd(2, gh * gw, tiny_cfg["enc_dim"])
+    y = O.encoder_block(tiny_cfg, tiny_weights, "enc_blocks.1", x, gh, gw)
+    ref = torch_block(x, tiny_weights, "enc_blocks.1", tiny_cfg["enc_heads"], gw, 1e-6)
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-5)
+
+
+def test_pair_view_swap_symmetry_and_determinism(tiny_cfg, tiny_weights):
+    w = dict(tiny_weights)
+    for k in list(w):  # share decoder chain and head weights across the views
+        if k.startswith("dec_blocks2."):
+            w[k] = w["dec_blocks." + k[len("dec_blocks2."):]]
+        if k.startswith("downstream_head2."):
+            w[k] = w["downstream_head1." + k[len("downstream_head2."):]]
+    i1 = RNG.uniform(-1, 1, (1, 3, 64, 96)).astype(np.float32)
+    i2 = RNG.uniform(-1, 1, (1, 3, 64, 96)).astype(np.float32)
+    a = O.mastr_pair(tiny_cfg, w, i1, i2)
+    b = O.mastr_pair(tiny_cfg, w, i2, i1)
+    for k in ("pts", "conf", "desc"):
+        np.testing.assert_array_equal(a[k + "1"], b[k + "2"])
+        np.testing.assert_array_equal(a[k + "2"], b[k + "1"])
+    c = O.mastr_pair(tiny_cfg, w, i1, i2)
+    for k in a:
+        np.testing.assert_array_equal(a[k], c[k])
+    assert np.all(a["conf1"] > 1.0)  # 1 + exp(.)
+
+
+def test_oracle_thread_count_does_not_change_bits(tiny_cfg, tiny_weights):
+    i1 = RNG.uniform(-1, 1, (1, 3, 64, 96)).astype(np.float32)
+    O.set_threads(1)
+    a = O.mastr_pair(tiny_cfg, tiny_weights, i1, i1[:, :, ::-1].copy())
+    O.set_threads(0)
+    b = O.mastr_pair(tiny_cfg, tiny_weights, i1, i1[:, :, ::-1].copy())
+    for k in a:
+        np.testing.assert_array_equal(a[k], b[k])
