@@ -967,7 +967,7 @@ int32_t gs_hip_mastr_encoder_block(void* ctx, int32_t layer, float* x, int32_t B
   Ctx* c = (Ctx*)ctx;
   GS_REQUIRE(layer >= 0 && layer < c->cfg.enc_depth, "encoder_block: layer out of range");
   GS_REQUIRE(B > 0 && B <= 2 * c->max_pairs, "encoder_block: B exceeds context capacity");
-  hipStream_t s = stream ? (hipStream_t)stream : default_stream();
+  hipStream_t s = (hipStream_t)stream;
   return encoder_block(*c, layer, x, (int64_t)B * c->N, s);
 }
 
@@ -975,7 +975,7 @@ int32_t gs_hip_mastr_encoder(void* ctx, const float* img, int32_t B, float* enc,
   GS_REQUIRE(ctx && img && enc, "encoder: null argument");
   Ctx* c = (Ctx*)ctx;
   GS_REQUIRE(B > 0 && B <= 2 * c->max_pairs, "encoder: B exceeds context capacity");
-  hipStream_t s = stream ? (hipStream_t)stream : default_stream();
+  hipStream_t s = (hipStream_t)stream;
   RC(launch_unfold(img, B, c->cfg.img_h, c->cfg.img_w, c->cfg.patch, c->P, s));
   return encoder_from_patches(*c, B, enc, s);
 }
@@ -988,7 +988,7 @@ int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2, int32
   GS_REQUIRE(B > 0 && B <= c->max_pairs, "pair: B exceeds context capacity");
   GS_REQUIRE(c->cfg.linear_layout == 0, "pair: the literal linear layout is encoder-only");
   GS_REQUIRE(!pts1 == !conf1 && !pts2 == !conf2, "pair: pts and conf must be given together");
-  hipStream_t s = stream ? (hipStream_t)stream : default_stream();
+  hipStream_t s = (hipStream_t)stream;
   const gs_mastr_config& f = c->cfg;
   const int64_t Mv = (int64_t)B * c->N;
   const int64_t K = 3 * f.patch * f.patch;
@@ -1016,7 +1016,7 @@ int32_t gs_hip_mastr_pair_taps(void* ctx, int32_t B, float* enc1, float* enc2, f
   GS_REQUIRE(ctx, "pair_taps: null context");
   Ctx* c = (Ctx*)ctx;
   GS_REQUIRE(B > 0 && B <= c->last_B, "pair_taps: B exceeds the last pair call");
-  hipStream_t s = stream ? (hipStream_t)stream : default_stream();
+  hipStream_t s = (hipStream_t)stream;
   const int64_t Mv = (int64_t)c->last_B * c->N;
   const int64_t ne = (int64_t)B * c->N * c->cfg.enc_dim, nd = (int64_t)B * c->N * c->cfg.dec_dim;
   if (enc1) GS_CHECK_HIP(hipMemcpyAsync(enc1, c->enc, ne * 4, hipMemcpyDeviceToDevice, s));

@@ -15,9 +15,7 @@ using namespace gs;
 
 namespace {
 
-hipStream_t pick(void* stream) {
-  return stream ? (hipStream_t)stream : default_stream();
-}
+hipStream_t pick(void* stream) { return (hipStream_t)stream; }
 
 // Library-owned scratch for weight re-layouts of the op-level entry points
 // (one per process; calls that need it are serialised by the mutex).

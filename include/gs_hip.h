@@ -27,9 +27,12 @@
  * error, with gs_hip_last_error() describing the last failure of the calling
  * thread. Pointers passed to gs_hip_* compute calls are device pointers
  * (hipMalloc'd or gs_buffer_contents) unless named host_*. `stream` is a
- * hipStream_t; NULL means the library's own stream (the one
- * gs_get_command_queue returns). All compute calls are asynchronous on that
- * stream. All tensors are fp32, row-major, contiguous unless strides are given.
+ * hipStream_t; NULL is HIP's default (null) stream, as in the HIP runtime.
+ * The library's own stream, which the kept gs_buffer_* copies use, is the
+ * one gs_get_command_queue returns; a caller mirroring the reference's single
+ * queue passes that. All compute calls are asynchronous on their stream and
+ * launch nothing before their host-side shape checks pass. All tensors are
+ * fp32, row-major, contiguous unless strides are given.
  */
 #ifndef GS_HIP_H
 #define GS_HIP_H

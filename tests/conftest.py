@@ -31,6 +31,17 @@ TINY = dict(img_h=64, img_w=96, patch=16, enc_dim=128, enc_depth=2, enc_heads=2,
             linear_layout=0, rope_mode=1)
 
 
+@pytest.fixture(autouse=True)
+def _release_device_tensors():
+    yield
+    mod = sys.modules.get("gpu_util")
+    if mod is not None:
+        import torch
+        if torch.cuda.is_available():
+            torch.cuda.synchronize()
+        mod.KEEP.clear()
+
+
 @pytest.fixture(scope="session")
 def tiny_cfg():
     return dict(TINY)

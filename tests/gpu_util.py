@@ -17,12 +17,22 @@ def case(msg):
     sys.stdout.flush()
 
 
+# Device tensors handed to the C ABI as raw pointers must outlive the kernels
+# that read them: keep every tensor made here until the test ends (cleared by
+# an autouse fixture in conftest.py).
+KEEP = []
+
+
 def dev(a):
-    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(DEV)
+    t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(DEV)
+    KEEP.append(t)
+    return t
 
 
 def empty(*shape):
-    return torch.empty(shape, device=DEV, dtype=torch.float32)
+    t = torch.empty(shape, device=DEV, dtype=torch.float32)
+    KEEP.append(t)
+    return t
 
 
 def host(t):
