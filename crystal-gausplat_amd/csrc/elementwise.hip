@@ -87,8 +87,12 @@ __global__ void unfold_kernel(const float* __restrict__ img, int32_t B, int32_t 
 }
 
 // Bilinear x2, align_corners=True (source = dst * (in-1)/(out-1)), NHWC.
+// No FMA contraction: a fused sh*oy - y0 moves the lerp weight by an ulp of
+// the source coordinate; this kernel is HBM-bound, so it keeps the plain
+// operation sequence of the CPU formula.
 __global__ void upsample2x_kernel(const float* __restrict__ x, int32_t B, int32_t H,
                                   int32_t W, int32_t C, float* __restrict__ y) {
+#pragma clang fp contract(off)
   const int Ho = 2 * H, Wo = 2 * W, C4 = C >> 2;
   const int64_t total = (int64_t)B * Ho * Wo * C4;
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -123,6 +127,7 @@ __global__ void upsample2x_kernel(const float* __restrict__ x, int32_t B, int32_
 __global__ void rope2d_kernel(float* t, int32_t B, int32_t N, int32_t H, int64_t ld,
                               int32_t grid_w, const float* __restrict__ cos_t,
                               const float* __restrict__ sin_t) {
+#pragma clang fp contract(off)
   const int64_t total = (int64_t)B * N * H * 32;
   const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (id >= total) return;
