@@ -53,7 +53,7 @@ def cpu_baseline():
     import gsplat_hip as G
     import pyoracle as O
 
-    cfg = G.default_config(enc_depth=1, dec_depth=1)
+    cfg = G.default_config(enc_depth=1, dec_depth=1, dpt_hooks=[0, 1, 1, 1])
     w = {}
     for i, (n, s, k) in enumerate(G.weight_inventory(cfg)):
         if n.startswith("enc_blocks.0."):

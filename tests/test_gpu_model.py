@@ -37,7 +37,8 @@ def test_config0_encoder_block(variant):
     so those epilogues are exercised; 'literal' uses the reference CPU
     path's linear layout (D1)."""
     case(f"config0 block {variant}")
-    cfg = G.default_config(enc_depth=1, dec_depth=1, linear_layout=1 if variant == "literal" else 0)
+    cfg = G.default_config(enc_depth=1, dec_depth=1, dpt_hooks=[0, 1, 1, 1],
+                           linear_layout=1 if variant == "literal" else 0)
     bias_std, ln_std = (0.02, 0.1) if variant == "biased" else (0.0, 0.0)
     w = weights_for(cfg, 0, bias_std, ln_std, prefix=["enc_blocks.0."])
     x = G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)
