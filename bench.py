@@ -88,6 +88,8 @@ def main():
     ap.add_argument("--config", type=int, default=3, choices=sorted(CONFIGS))
     ap.add_argument("--pairs", type=int, default=0, help="override the config's pair count")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--per-shape", action="store_true",
+                    help="also print a per-shape kernel table (stderr) from a separate step")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device-to-device copies of MIB MiB (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -191,6 +193,14 @@ def main():
         "roofline": roof,
         "kernels": kernels,
     }
+    if args.per_shape:
+        G.profile_begin(per_shape=True)
+        step()
+        torch.cuda.synchronize()
+        shp = G.profile_end()
+        for k, v in sorted(shp.items(), key=lambda kv: -kv[1]["ms"]):
+            tf = v["flops"] / (v["ms"] * 1e-3) / 1e12 if v["flops"] else 0.0
+            print(f"{v['ms']:9.3f} ms {v['launches']:4d}x {tf:7.1f} TF/s  {k}", file=sys.stderr)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     m.close()

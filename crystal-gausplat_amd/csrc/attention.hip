@@ -16,6 +16,8 @@
 // and the exponentiated scores are already the B operand of the P.V product:
 // MFMA step s takes key 8*(s/4) + 4*(lane/32) + s%4 -- exactly the key the
 // lane holds in accumulator register s. No LDS round trip for P.
+#include <string>
+
 #include "internal.h"
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -194,7 +196,11 @@ int launch_attention(const AttnBatch& bt, hipStream_t s) {
   GS_CHECK_HIP(hipGetLastError());
   if (ev) {
     const double units = (double)a0.B * a0.H * bt.ngroups;
-    prof_stop(s, ev, "attn_fwd_kernel", units * 4.0 * a0.Nq * (double)a0.Nkv * 64.0,
+    std::string nm = "attn_fwd_kernel";
+    if (prof_per_shape())
+      nm += " B=" + std::to_string(a0.B) + " H=" + std::to_string(a0.H) + " Nq=" +
+            std::to_string(a0.Nq) + " groups=" + std::to_string(bt.ngroups);
+    prof_stop(s, ev, nm.c_str(), units * 4.0 * a0.Nq * (double)a0.Nkv * 64.0,
               units * 4.0 * 64.0 * (2.0 * a0.Nq + 2.0 * a0.Nkv));
   }
   return 0;

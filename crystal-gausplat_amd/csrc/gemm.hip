@@ -15,6 +15,8 @@
 // LDS rows are padded to 36 floats so the 8 lanes of each ds_read_b128 phase
 // hit 32 distinct banks. The next K step is prefetched into registers while
 // the current one runs on the matrix cores.
+#include <string>
+
 #include "internal.h"
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -240,6 +242,17 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
+std::string gemm_prof_name(const char* base, const GemmBatch& b) {
+  std::string n = base;
+  if (prof_per_shape()) {
+    const GemmArgs& g = b.g[0];
+    n += " M=" + std::to_string(g.M) + " N=" + std::to_string(g.N) + " K=" + std::to_string(g.K) +
+         " groups=" + std::to_string(b.ngroups);
+    if (g.flags & EPI_GELU) n += " gelu";
+  }
+  return n;
+}
+
 }  // namespace
 
 int check_gemm(const GemmArgs& a, int aload, int blayout) {
@@ -305,7 +318,8 @@ int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
     hipEvent_t ev = prof_start(s);                                            \
     hipLaunchKernelGGL((gemm_f32_kernel<AL, BL, RL>), grid, block, 0, s, b);  \
     GS_CHECK_HIP(hipGetLastError());                                          \
-    prof_stop(s, ev, "gemm_f32_kernel<" #AL "," #BL "," #RL ">", flops, bytes); \
+    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_kernel<" #AL "," #BL "," #RL ">", b).c_str(), \
+                      flops, bytes);                                          \
     return 0;                                                                 \
   }
   GS_GEMM_CASE(A_PLAIN, B_NT, false)

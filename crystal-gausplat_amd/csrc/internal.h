@@ -43,6 +43,7 @@ int ensure_device();           // 0 ok; lazily runs gs_init_device
 // When enabled, launchers bracket each kernel with HIP events on its stream and
 // record (kernel name, algorithmic flops, algorithmic HBM bytes).
 bool prof_on();
+bool prof_per_shape();
 hipEvent_t prof_start(hipStream_t s);
 void prof_stop(hipStream_t s, hipEvent_t start, const char* kernel, double flops,
                double bytes);

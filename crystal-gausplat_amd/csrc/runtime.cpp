@@ -36,6 +36,7 @@ struct ProfRec {
   hipEvent_t a, b;
 };
 bool g_prof = false;
+bool g_prof_shape = false;
 std::vector<ProfRec> g_recs;
 std::vector<hipEvent_t> g_pool;
 size_t g_pool_used = 0;
@@ -58,6 +59,7 @@ hipEvent_t pool_event() {
 }  // namespace
 
 bool prof_on() { return g_prof; }
+bool prof_per_shape() { return g_prof_shape; }
 
 hipEvent_t prof_start(hipStream_t s) {
   if (!g_prof) return nullptr;
@@ -205,8 +207,9 @@ void gs_buffer_read(void* handle, void* dest, int64_t size) {
 
 void gs_buffer_sync(void* handle) { (void)handle; }
 
-int32_t gs_hip_profile_begin(void) {
+int32_t gs_hip_profile_begin(int32_t per_shape) {
   if (ensure_device()) return -2;
+  g_prof_shape = per_shape != 0;
   g_recs.clear();
   g_agg.clear();
   g_pool_used = 0;

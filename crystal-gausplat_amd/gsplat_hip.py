@@ -89,7 +89,7 @@ _SIGS = [
     ("gs_hip_mastr_encoder", C.c_int32, [vp, vp, C.c_int32, vp, vp]),
     ("gs_hip_mastr_pair", C.c_int32, [vp, vp, vp, C.c_int32, vp, vp, vp, vp, vp, vp, vp]),
     ("gs_hip_mastr_pair_taps", C.c_int32, [vp, C.c_int32, vp, vp, vp, vp, vp]),
-    ("gs_hip_profile_begin", C.c_int32, []),
+    ("gs_hip_profile_begin", C.c_int32, [C.c_int32]),
     ("gs_hip_profile_end", C.c_int32, []),
     ("gs_hip_profile_entry", C.c_int32, [C.c_int32, C.c_char_p, C.c_int32, C.POINTER(C.c_int64),
                                          C.POINTER(C.c_double), C.POINTER(C.c_double),
@@ -198,8 +198,8 @@ def seed_uniform(seed, name, n, lo=-1.0, hi=1.0):
     return a
 
 
-def profile_begin():
-    check(lib().gs_hip_profile_begin())
+def profile_begin(per_shape=False):
+    check(lib().gs_hip_profile_begin(1 if per_shape else 0))
 
 
 def profile_end():

@@ -241,9 +241,10 @@ int32_t gs_hip_mastr_pair_taps(void* ctx, int32_t B, float* enc1, float* enc2,
 /* ------------------------------------------------------------------------ */
 /* Between begin and end, every kernel launch is bracketed by HIP events on
  * its own stream. end synchronises those events and returns the number of
- * distinct kernels; entry i gives its launches, summed event time (ms),
- * summed algorithmic flops and algorithmic HBM bytes. */
-int32_t gs_hip_profile_begin(void);
+ * distinct kernels (per_shape != 0: distinct kernel + problem shape); entry i
+ * gives its launches, summed event time (ms), summed algorithmic flops and
+ * algorithmic HBM bytes. */
+int32_t gs_hip_profile_begin(int32_t per_shape);
 int32_t gs_hip_profile_end(void);
 int32_t gs_hip_profile_entry(int32_t i, char* name_out, int32_t name_cap,
                              int64_t* launches, double* ms, double* flops,
