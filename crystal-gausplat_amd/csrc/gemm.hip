@@ -79,18 +79,38 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
   // Global->LDS assignment: rows tid/8 + 32*i, fx4 column tid%8.
   const int lrow = tid >> 3, lc4 = (tid & 7) * 4;
 
-  // Implicit-conv row decode (output pixel -> image, oh, ow).
+  // Per-row load state, computed once. Loads are branch-free: every address is
+  // clamped into its buffer and out-of-range rows / taps are zeroed with a
+  // select, so the loads of the next K step issue as one straight-line block.
+  int arow[4];          // clamped A row (plain / concat), or conv output pixel
+  bool aval[4];
   int cimg[4], coh[4], cow[4];
-  if (ALOAD == A_CONV) {
+  int boff[4];          // B row offsets (N * ldb < 2^31 is checked on the host)
+  bool bval_[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = m0 + lrow + 32 * i;
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + lrow + 32 * i;
+    aval[i] = m < M;
+    arow[i] = min(m, M - 1);
+    if (ALOAD == A_CONV) {
       const int hw = p.cHo * p.cWo;
-      cimg[i] = m / hw;
-      const int rem = m - cimg[i] * hw;
+      cimg[i] = arow[i] / hw;
+      const int rem = arow[i] - cimg[i] * hw;
       coh[i] = rem / p.cWo;
       cow[i] = rem - coh[i] * p.cWo;
     }
+    if (BLAYOUT == B_NT) {
+      const int n = n0 + lrow + 32 * i;
+      bval_[i] = n < N;
+      boff[i] = min(n, N - 1) * (int)p.ldb + lc4;
+    }
+  }
+  int bncol = 0;
+  bool bnval = true;
+  if (BLAYOUT == B_NN) {
+    const int n = n0 + 4 * (tid & 31);
+    bnval = n < N;
+    bncol = min(n, N - 4);
   }
 
   fx4 ra[4], rb[4];
@@ -98,42 +118,43 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
 
 // Global loads of one K step into registers (macro rather than lambda so the
 // register arrays stay in VGPRs).
-#define GS_GEMM_LOAD(K0)                                                                \
-  {                                                                                     \
-    const int k0_ = (K0);                                                               \
-    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                     \
-      const int m = m0 + lrow + 32 * i;                                                 \
-      fx4 v = zero4;                                                                 \
-      if (ALOAD == A_PLAIN) {                                                           \
-        if (m < M) v = *(const fx4*)(p.A + (int64_t)m * p.lda + k0_ + lc4);          \
-      } else if (ALOAD == A_CONCAT) {                                                   \
-        if (m < M) {                                                                    \
-          if (k0_ < p.K1)                                                               \
-            v = *(const fx4*)(p.A + (int64_t)m * p.lda + k0_ + lc4);                 \
-          else                                                                          \
-            v = *(const fx4*)(p.A2 + (int64_t)m * p.lda2 + (k0_ - p.K1) + lc4);      \
-        }                                                                               \
-      } else {                                                                          \
-        const int kk = k0_ / p.cCin;                                                    \
-        const int ic0 = k0_ - kk * p.cCin;                                              \
-        const int kh = kk / p.ck, kw = kk - kh * p.ck;                                  \
-        const int ih = coh[i] * p.cs + kh - p.cp;                                       \
-        const int iw = cow[i] * p.cs + kw - p.cp;                                       \
-        if (m < M && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW)                      \
-          v = *(const fx4*)(p.A + (((int64_t)cimg[i] * p.cH + ih) * p.cW + iw) *     \
-                                         p.cCin + ic0 + lc4);                           \
-      }                                                                                 \
-      if (A_RELU) v = relu4(v);                                                         \
-      ra[i] = v;                                                                        \
-      if (BLAYOUT == B_NT) {                                                            \
-        const int n = n0 + lrow + 32 * i;                                               \
-        rb[i] = n < N ? *(const fx4*)(p.B + (int64_t)n * p.ldb + k0_ + lc4) : zero4; \
-      } else {                                                                          \
-        const int kb = (tid >> 5) + 8 * i;                                              \
-        const int n = n0 + 4 * (tid & 31);                                              \
-        rb[i] = n < N ? *(const fx4*)(p.B + (int64_t)(k0_ + kb) * p.ldb + n) : zero4; \
-      }                                                                                 \
-    }                                                                                   \
+#define GS_GEMM_LOAD(K0)                                                                 \
+  {                                                                                      \
+    const int k0_ = (K0);                                                                \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                      \
+      fx4 v;                                                                             \
+      bool ok = aval[i];                                                                 \
+      if (ALOAD == A_PLAIN) {                                                            \
+        v = *(const fx4*)(p.A + (int64_t)arow[i] * p.lda + k0_ + lc4);                   \
+      } else if (ALOAD == A_CONCAT) {                                                    \
+        const bool first = k0_ < p.K1;                                                   \
+        const float* base = first ? p.A : p.A2;                                          \
+        const int64_t ld = first ? p.lda : p.lda2;                                       \
+        const int kc = first ? k0_ : k0_ - p.K1;                                         \
+        v = *(const fx4*)(base + (int64_t)arow[i] * ld + kc + lc4);                      \
+      } else {                                                                           \
+        const int kk = k0_ / p.cCin;                                                     \
+        const int ic0 = k0_ - kk * p.cCin;                                               \
+        const int kh = kk / p.ck, kw = kk - kh * p.ck;                                   \
+        const int ih = coh[i] * p.cs + kh - p.cp;                                        \
+        const int iw = cow[i] * p.cs + kw - p.cp;                                        \
+        ok = ok && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW;                         \
+        const int ihc = min(max(ih, 0), p.cH - 1), iwc = min(max(iw, 0), p.cW - 1);      \
+        v = *(const fx4*)(p.A + (((int64_t)cimg[i] * p.cH + ihc) * p.cW + iwc) * p.cCin + \
+                          ic0 + lc4);                                                    \
+      }                                                                                  \
+      v = ok ? v : zero4;                                                                \
+      if (A_RELU) v = relu4(v);                                                          \
+      ra[i] = v;                                                                         \
+      if (BLAYOUT == B_NT) {                                                             \
+        const fx4 w = *(const fx4*)(p.B + boff[i] + k0_);                                \
+        rb[i] = bval_[i] ? w : zero4;                                                    \
+      } else {                                                                           \
+        const int kb = (tid >> 5) + 8 * i;                                               \
+        const fx4 w = *(const fx4*)(p.B + (int64_t)(k0_ + kb) * p.ldb + bncol);          \
+        rb[i] = bnval ? w : zero4;                                                       \
+      }                                                                                  \
+    }                                                                                    \
   }
 
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
@@ -156,7 +177,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
       }
     }
     __syncthreads();
-    if (k0 + BK < K) GS_GEMM_LOAD(k0 + BK)
+    // Prefetch the next K step (the last iteration reloads its own step:
+    // in bounds, and the values are never stored).
+    GS_GEMM_LOAD(min(k0 + BK, K - BK))
     const float* a0p = &As[wm * 64 + l32][hl * 16];
     const float* a1p = &As[wm * 64 + 32 + l32][hl * 16];
     const float* b0p = &Bs[wn * 64 + l32][hl * 16];
@@ -275,7 +298,8 @@ int check_gemm(const GemmArgs& a, int aload, int blayout) {
                "conv: output grid mismatch");
     GS_REQUIRE(a.M % (a.cHo * a.cWo) == 0, "conv: M must be images*Ho*Wo");
   }
-  if (blayout == B_NT) GS_REQUIRE(a.ldb >= a.K, "gemm: ldb < K");
+  if (blayout == B_NT)
+    GS_REQUIRE(a.ldb >= a.K && (int64_t)a.N * a.ldb < ((int64_t)1 << 31), "gemm: bad ldb");
   else GS_REQUIRE(a.N % 4 == 0 && a.ldb >= a.N, "gemm: NN layout needs N % 4 == 0");
   if (a.flags & EPI_BIAS) GS_REQUIRE(a.bias != nullptr, "gemm: null bias");
   if (a.flags & EPI_RES1) GS_REQUIRE(a.R1 != nullptr, "gemm: null residual");

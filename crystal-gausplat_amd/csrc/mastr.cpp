@@ -172,7 +172,9 @@ struct Ctx {
   size_t arena_size = 0;
   // workspaces
   float *P, *x, *h, *qkv, *att, *mlp, *enc, *d, *ym, *kv, *q, *hook1, *hook2, *dfin;
-  float *t0, *act[4], *L[4], *u, *s, *t, *up, *rA, *rB, *hd0, *hup, *hd2, *lf;
+  // DPT / descriptor workspaces, one slot per head of a grouped launch
+  float *t0[2], *act[2][4], *L[2][4], *u[2], *s[2], *t[2], *up[2], *rA[2], *rB[2], *hd0[2],
+      *hup[2], *hd2[2], *lf[2];
   float *rope_cos, *rope_sin, *ref_cos, *ref_sin;
   int ref_maxpos = 0;
   int last_B = 0;
@@ -456,127 +458,182 @@ int decoder(Ctx& c, int B, hipStream_t s) {
   return 0;
 }
 
-// Conv as implicit GEMM on an NHWC tensor [imgs, H, W, Cin] with a context
-// weight (already OHWI for k > 1).
-int conv(Ctx& c, const std::string& name, const float* x, int imgs, int H, int W_, int Cin,
-         int Cout, int k, int stride, int pad, bool bias, float* y, int flags, bool relu_in,
-         hipStream_t s, const float* r1 = nullptr, const float* r2 = nullptr) {
+// The two views' DPT heads (and descriptor heads) have identical shapes and
+// separate weights, so each of their convolutions runs as ONE grouped launch
+// (z = head): the 1/32- and 1/16-scale convolutions alone would fill a
+// fraction of the GPU.
+struct Heads {
+  int n = 0;       // 1 or 2 heads in this launch sequence
+  int id[2];       // checkpoint head number (1 or 2) of group slot v
+  std::string pre(int v) const { return "downstream_head" + std::to_string(id[v]); }
+};
+
+// Conv as implicit GEMM on NHWC tensors [imgs, H, W, Cin], one problem per
+// head; `suffix` is the weight name after the head prefix (weights of 3x3
+// convs are already OHWI).
+int conv(Ctx& c, const Heads& hs, const std::string& suffix, const float* const x[2], int imgs,
+         int H, int W_, int Cin, int Cout, int k, int stride, int pad, bool bias,
+         float* const y[2], int flags, bool relu_in, hipStream_t s,
+         const float* const r1[2] = nullptr, const float* const r2[2] = nullptr) {
   const int Ho = (H + 2 * pad - k) / stride + 1, Wo = (W_ + 2 * pad - k) / stride + 1;
-  GemmArgs a = lin(x, Cin, W(c, name + ".weight"), bias ? W(c, name + ".bias") : nullptr, y, Cout,
-                   (int64_t)imgs * Ho * Wo, Cout, k * k * Cin, flags);
-  a.cH = H;
-  a.cW = W_;
-  a.cCin = Cin;
-  a.ck = k;
-  a.cs = stride;
-  a.cp = pad;
-  a.cHo = Ho;
-  a.cWo = Wo;
-  if (r1) {
-    a.flags |= EPI_RES1;
-    a.R1 = r1;
-    a.ldr1 = Cout;
-  }
-  if (r2) {
-    a.flags |= EPI_RES2;
-    a.R2 = r2;
-    a.ldr2 = Cout;
+  GemmBatch b;
+  b.ngroups = hs.n;
+  for (int v = 0; v < hs.n; ++v) {
+    const std::string name = hs.pre(v) + suffix;
+    GemmArgs a = lin(x[v], Cin, W(c, name + ".weight"), bias ? W(c, name + ".bias") : nullptr,
+                     y[v], Cout, (int64_t)imgs * Ho * Wo, Cout, k * k * Cin, flags);
+    a.cH = H;
+    a.cW = W_;
+    a.cCin = Cin;
+    a.ck = k;
+    a.cs = stride;
+    a.cp = pad;
+    a.cHo = Ho;
+    a.cWo = Wo;
+    if (r1) {
+      a.flags |= EPI_RES1;
+      a.R1 = r1[v];
+      a.ldr1 = Cout;
+    }
+    if (r2) {
+      a.flags |= EPI_RES2;
+      a.R2 = r2[v];
+      a.ldr2 = Cout;
+    }
+    b.g[v] = a;
   }
   const bool pointwise = (k == 1 && stride == 1 && pad == 0);
-  return run1(a, pointwise ? A_PLAIN : A_CONV, s, relu_in);
+  return launch_gemm(b, pointwise ? A_PLAIN : A_CONV, B_NT, relu_in, s);
 }
 
-// ConvTranspose (k == s) from a [rows, Cin] token tensor on the gh x gw grid.
-int convt(Ctx& c, const std::string& name, const float* x, int imgs, int Cin, int Cout, int k,
-          float* y, hipStream_t s) {
-  GemmArgs a = lin(x, Cin, c.derived[name + ".weight"], c.derived[name + ".bias"], y, 0,
-                   (int64_t)imgs * c.N, k * k * Cout, Cin, EPI_SCATTER);
-  a.sc_r = k;
-  a.sc_C = Cout;
-  a.sc_Cout = Cout;
-  a.sc_gh = c.gh;
-  a.sc_gw = c.gw;
-  return run1(a, A_PLAIN, s);
-}
-
-// FeatureFusionBlock: out = out_conv(up2(RCU2(x0 (+ RCU1(x1))))).
-int fusion(Ctx& c, const std::string& name, const float* x0, const float* x1, int B, int H,
-           int W_, float* out, hipStream_t s) {
-  const int F = c.cfg.dpt_feat;
-  const float* sum = x0;
-  if (x1) {
-    RC(conv(c, name + ".resConfUnit1.conv1", x1, B, H, W_, F, F, 3, 1, 1, true, c.u, EPI_RELU, true,
-            s));
-    RC(conv(c, name + ".resConfUnit1.conv2", c.u, B, H, W_, F, F, 3, 1, 1, true, c.s, 0, false, s,
-            x1, x0));
-    sum = c.s;
+// ConvTranspose (k == s) from [rows, Cin] token tensors on the gh x gw grid.
+int convt(Ctx& c, const Heads& hs, const std::string& suffix, const float* const x[2], int imgs,
+          int Cin, int Cout, int k, float* const y[2], hipStream_t s) {
+  GemmBatch b;
+  b.ngroups = hs.n;
+  for (int v = 0; v < hs.n; ++v) {
+    const std::string name = hs.pre(v) + suffix;
+    GemmArgs a = lin(x[v], Cin, c.derived[name + ".weight"], c.derived[name + ".bias"], y[v], 0,
+                     (int64_t)imgs * c.N, k * k * Cout, Cin, EPI_SCATTER);
+    a.sc_r = k;
+    a.sc_C = Cout;
+    a.sc_Cout = Cout;
+    a.sc_gh = c.gh;
+    a.sc_gw = c.gw;
+    b.g[v] = a;
   }
-  RC(conv(c, name + ".resConfUnit2.conv1", sum, B, H, W_, F, F, 3, 1, 1, true, c.u, EPI_RELU, true,
-          s));
-  RC(conv(c, name + ".resConfUnit2.conv2", c.u, B, H, W_, F, F, 3, 1, 1, true, c.t, 0, false, s,
-          sum));
-  RC(launch_upsample2x(c.t, B, H, W_, F, c.up, s));
-  RC(conv(c, name + ".out_conv", c.up, B, 2 * H, 2 * W_, F, F, 1, 1, 0, true, out, 0, false, s));
+  return launch_gemm(b, A_PLAIN, B_NT, false, s);
+}
+
+// FeatureFusionBlock: out = out_conv(up2(RCU2(x0 (+ RCU1(x1))))). The 1x1
+// out_conv and the bilinear x2 upsample commute (both are linear and the
+// bilinear weights of each output pixel sum to one, so the bias passes
+// through), so out_conv runs at the input resolution: a quarter of its FLOPs
+// and of the upsample's input traffic. Differences are fp32 rounding only.
+int fusion(Ctx& c, const Heads& hs, const std::string& suffix, const float* const x0[2],
+           const float* const x1[2], int B, int H, int W_, float* const out[2], hipStream_t s) {
+  const int F = c.cfg.dpt_feat;
+  const float* sum[2] = {x0[0], x0[1]};
+  if (x1) {
+    RC(conv(c, hs, suffix + ".resConfUnit1.conv1", x1, B, H, W_, F, F, 3, 1, 1, true, c.u, EPI_RELU,
+            true, s));
+    const float* uin[2] = {c.u[0], c.u[1]};
+    RC(conv(c, hs, suffix + ".resConfUnit1.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.s, 0,
+            false, s, x1, x0));
+    sum[0] = c.s[0];
+    sum[1] = c.s[1];
+  }
+  RC(conv(c, hs, suffix + ".resConfUnit2.conv1", sum, B, H, W_, F, F, 3, 1, 1, true, c.u, EPI_RELU,
+          true, s));
+  const float* uin[2] = {c.u[0], c.u[1]};
+  RC(conv(c, hs, suffix + ".resConfUnit2.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.t, 0, false,
+          s, sum));
+  const float* tin[2] = {c.t[0], c.t[1]};
+  RC(conv(c, hs, suffix + ".out_conv", tin, B, H, W_, F, F, 1, 1, 0, true, c.up, 0, false, s));
+  for (int v = 0; v < hs.n; ++v) RC(launch_upsample2x(c.up[v], B, H, W_, F, out[v], s));
   return 0;
 }
 
-// DPT head of one view: hooks are row blocks of [B*N, dim] tensors.
-int dpt_head(Ctx& c, int head, const float* e, const float* h6, const float* h9,
-             const float* dfin, int B, float* pts, float* conf, hipStream_t s) {
+// DPT heads; hooks are per group slot row blocks of [B*N, dim] tensors.
+int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* const h6[2],
+              const float* const h9[2], const float* const dfin[2], int B, float* const pts[2],
+              float* const conf[2], hipStream_t s) {
   const gs_mastr_config& f = c.cfg;
   const int F = f.dpt_feat, gh = c.gh, gw = c.gw;
-  const std::string p = "downstream_head" + std::to_string(head);
-  const std::string ap = p + ".dpt.act_postprocess.";
+  const std::string ap = ".dpt.act_postprocess.";
   const int* d = f.dpt_dims;
-  // act_postprocess
-  RC(conv(c, ap + "0.0", e, B, gh, gw, f.enc_dim, d[0], 1, 1, 0, true, c.t0, 0, false, s));
-  RC(convt(c, ap + "0.1", c.t0, B, d[0], d[0], 4, c.act[0], s));
-  RC(conv(c, ap + "1.0", h6, B, gh, gw, f.dec_dim, d[1], 1, 1, 0, true, c.t0, 0, false, s));
-  RC(convt(c, ap + "1.1", c.t0, B, d[1], d[1], 2, c.act[1], s));
-  RC(conv(c, ap + "2.0", h9, B, gh, gw, f.dec_dim, d[2], 1, 1, 0, true, c.act[2], 0, false, s));
-  RC(conv(c, ap + "3.0", dfin, B, gh, gw, f.dec_dim, d[3], 1, 1, 0, true, c.t0, 0, false, s));
-  RC(conv(c, ap + "3.1", c.t0, B, gh, gw, d[3], d[3], 3, 2, 1, true, c.act[3], 0, false, s));
-  const int ah[4] = {4 * gh, 2 * gh, gh, gh / 2}, aw[4] = {4 * gw, 2 * gw, gw, gw / 2};
+  const float* t0c[2] = {c.t0[0], c.t0[1]};
+  float* act[4][2];
   for (int i = 0; i < 4; ++i)
-    RC(conv(c, p + ".dpt.scratch.layer" + std::to_string(i + 1) + "_rn", c.act[i], B, ah[i], aw[i],
-            d[i], F, 3, 1, 1, false, c.L[i], 0, false, s));
-  const std::string rp = p + ".dpt.scratch.refinenet";
-  RC(fusion(c, rp + "4", c.L[3], nullptr, B, ah[3], aw[3], c.rA, s));
-  RC(fusion(c, rp + "3", c.rA, c.L[2], B, ah[2], aw[2], c.rB, s));
-  RC(fusion(c, rp + "2", c.rB, c.L[1], B, ah[1], aw[1], c.rA, s));
-  RC(fusion(c, rp + "1", c.rA, c.L[0], B, ah[0], aw[0], c.rB, s));
+    for (int v = 0; v < 2; ++v) act[i][v] = c.act[v][i];
+  // act_postprocess
+  RC(conv(c, hs, ap + "0.0", e, B, gh, gw, f.enc_dim, d[0], 1, 1, 0, true, c.t0, 0, false, s));
+  RC(convt(c, hs, ap + "0.1", t0c, B, d[0], d[0], 4, act[0], s));
+  RC(conv(c, hs, ap + "1.0", h6, B, gh, gw, f.dec_dim, d[1], 1, 1, 0, true, c.t0, 0, false, s));
+  RC(convt(c, hs, ap + "1.1", t0c, B, d[1], d[1], 2, act[1], s));
+  RC(conv(c, hs, ap + "2.0", h9, B, gh, gw, f.dec_dim, d[2], 1, 1, 0, true, act[2], 0, false, s));
+  RC(conv(c, hs, ap + "3.0", dfin, B, gh, gw, f.dec_dim, d[3], 1, 1, 0, true, c.t0, 0, false, s));
+  RC(conv(c, hs, ap + "3.1", t0c, B, gh, gw, d[3], d[3], 3, 2, 1, true, act[3], 0, false, s));
+  const int ah[4] = {4 * gh, 2 * gh, gh, gh / 2}, aw[4] = {4 * gw, 2 * gw, gw, gw / 2};
+  float* L[4][2];
+  for (int i = 0; i < 4; ++i) {
+    for (int v = 0; v < 2; ++v) L[i][v] = c.L[v][i];
+    const float* ain[2] = {act[i][0], act[i][1]};
+    RC(conv(c, hs, ".dpt.scratch.layer" + std::to_string(i + 1) + "_rn", ain, B, ah[i], aw[i], d[i],
+            F, 3, 1, 1, false, L[i], 0, false, s));
+  }
+  const std::string rp = ".dpt.scratch.refinenet";
+  const float* Lc[4][2];
+  for (int i = 0; i < 4; ++i)
+    for (int v = 0; v < 2; ++v) Lc[i][v] = L[i][v];
+  const float* rAc[2] = {c.rA[0], c.rA[1]};
+  const float* rBc[2] = {c.rB[0], c.rB[1]};
+  RC(fusion(c, hs, rp + "4", Lc[3], nullptr, B, ah[3], aw[3], c.rA, s));
+  RC(fusion(c, hs, rp + "3", rAc, Lc[2], B, ah[2], aw[2], c.rB, s));
+  RC(fusion(c, hs, rp + "2", rBc, Lc[1], B, ah[1], aw[1], c.rA, s));
+  RC(fusion(c, hs, rp + "1", rAc, Lc[0], B, ah[0], aw[0], c.rB, s));
   const int h1 = 2 * ah[0], w1 = 2 * aw[0];
-  RC(conv(c, p + ".dpt.head.0", c.rB, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s));
-  RC(launch_upsample2x(c.hd0, B, h1, w1, F / 2, c.hup, s));
-  RC(conv(c, p + ".dpt.head.2", c.hup, B, 2 * h1, 2 * w1, F / 2, f.head_mid, 3, 1, 1, true, c.hd2,
+  RC(conv(c, hs, ".dpt.head.0", rBc, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s));
+  for (int v = 0; v < hs.n; ++v) RC(launch_upsample2x(c.hd0[v], B, h1, w1, F / 2, c.hup[v], s));
+  const float* hupc[2] = {c.hup[0], c.hup[1]};
+  RC(conv(c, hs, ".dpt.head.2", hupc, B, 2 * h1, 2 * w1, F / 2, f.head_mid, 3, 1, 1, true, c.hd2,
           EPI_RELU, false, s));
-  RC(launch_head_out(c.hd2, (int64_t)B * 4 * h1 * w1, f.head_mid, W(c, p + ".dpt.head.4.weight"),
-                     W(c, p + ".dpt.head.4.bias"), pts, conf, s));
+  for (int v = 0; v < hs.n; ++v)
+    RC(launch_head_out(c.hd2[v], (int64_t)B * 4 * h1 * w1, f.head_mid,
+                       W(c, hs.pre(v) + ".dpt.head.4.weight"), W(c, hs.pre(v) + ".dpt.head.4.bias"),
+                       pts[v], conf[v], s));
   return 0;
 }
 
-// Local-feature descriptors of one view: MLP(concat(enc, dec)) + shuffle.
-int local_features(Ctx& c, int head, const float* e, const float* dfin, int B, float* desc,
-                   hipStream_t s) {
+// Local-feature descriptors: MLP(concat(enc, dec)) + pixel shuffle, per head.
+int local_features(Ctx& c, const Heads& hs, const float* const e[2], const float* const dfin[2],
+                   int B, float* const desc[2], hipStream_t s) {
   const gs_mastr_config& f = c.cfg;
-  const std::string p = "downstream_head" + std::to_string(head) + ".head_local_features";
   const int Din = f.enc_dim + f.dec_dim;
   const int64_t Mv = (int64_t)B * c.N;
-  GemmArgs a = lin(e, f.enc_dim, W(c, p + ".fc1.weight"), W(c, p + ".fc1.bias"), c.lf, f.lf_hidden,
-                   Mv, f.lf_hidden, Din, EPI_GELU);
-  a.A2 = dfin;
-  a.lda2 = f.dec_dim;
-  a.K1 = f.enc_dim;
-  RC(run1(a, A_CONCAT, s));
   const int r = f.patch;
-  GemmArgs b = lin(c.lf, f.lf_hidden, c.derived[p + ".fc2.weight"], c.derived[p + ".fc2.bias"],
-                   desc, 0, Mv, r * r * f.desc_dim, f.lf_hidden, EPI_SCATTER);
-  b.sc_r = r;
-  b.sc_C = f.desc_dim;
-  b.sc_Cout = f.desc_dim;
-  b.sc_gh = c.gh;
-  b.sc_gw = c.gw;
-  return run1(b, A_PLAIN, s);
+  GemmBatch b1, b2;
+  b1.ngroups = b2.ngroups = hs.n;
+  for (int v = 0; v < hs.n; ++v) {
+    const std::string p = hs.pre(v) + ".head_local_features";
+    GemmArgs a = lin(e[v], f.enc_dim, W(c, p + ".fc1.weight"), W(c, p + ".fc1.bias"), c.lf[v],
+                     f.lf_hidden, Mv, f.lf_hidden, Din, EPI_GELU);
+    a.A2 = dfin[v];
+    a.lda2 = f.dec_dim;
+    a.K1 = f.enc_dim;
+    b1.g[v] = a;
+    GemmArgs g = lin(c.lf[v], f.lf_hidden, c.derived[p + ".fc2.weight"],
+                     c.derived[p + ".fc2.bias"], desc[v], 0, Mv, r * r * f.desc_dim, f.lf_hidden,
+                     EPI_SCATTER);
+    g.sc_r = r;
+    g.sc_C = f.desc_dim;
+    g.sc_Cout = f.desc_dim;
+    g.sc_gh = c.gh;
+    g.sc_gw = c.gw;
+    b2.g[v] = g;
+  }
+  RC(launch_gemm(b1, A_CONCAT, B_NT, false, s));
+  return launch_gemm(b2, A_PLAIN, B_NT, false, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -757,31 +814,35 @@ int build_workspace(Ctx& c) {
       {&c.hook1, M * Dd},
       {&c.hook2, M * Dd},
       {&c.dfin, M * Dd},
-      // DPT (one head at a time, B images)
-      {&c.t0, B * N * dmax},
-      {&c.act[0], B * 16 * N * f.dpt_dims[0]},
-      {&c.act[1], B * 4 * N * f.dpt_dims[1]},
-      {&c.act[2], B * N * f.dpt_dims[2]},
-      {&c.act[3], B * N / 4 * f.dpt_dims[3]},
-      {&c.L[0], B * 16 * N * F},
-      {&c.L[1], B * 4 * N * F},
-      {&c.L[2], B * N * F},
-      {&c.L[3], B * N / 4 * F},
-      {&c.u, B * 16 * N * F},
-      {&c.s, B * 16 * N * F},
-      {&c.t, B * 16 * N * F},
-      {&c.up, B * 64 * N * F},
-      {&c.rA, B * 64 * N * F},
-      {&c.rB, B * 64 * N * F},
-      {&c.hd0, B * 64 * N * (F / 2)},
-      {&c.hup, B * 256 * N * (F / 2)},
-      {&c.hd2, B * 256 * N * f.head_mid},
-      {&c.lf, B * N * f.lf_hidden},
       {&c.rope_cos, 512 * 16},
       {&c.rope_sin, 512 * 16},
       {&c.ref_cos, 512 * (De / f.enc_heads / 2)},
       {&c.ref_sin, 512 * (De / f.enc_heads / 2)},
   };
+  for (int v = 0; v < 2; ++v) {  // DPT / descriptor heads, B images each
+    const std::vector<std::pair<float**, int64_t>> head = {
+        {&c.t0[v], B * N * dmax},
+        {&c.act[v][0], B * 16 * N * f.dpt_dims[0]},
+        {&c.act[v][1], B * 4 * N * f.dpt_dims[1]},
+        {&c.act[v][2], B * N * f.dpt_dims[2]},
+        {&c.act[v][3], B * N / 4 * f.dpt_dims[3]},
+        {&c.L[v][0], B * 16 * N * F},
+        {&c.L[v][1], B * 4 * N * F},
+        {&c.L[v][2], B * N * F},
+        {&c.L[v][3], B * N / 4 * F},
+        {&c.u[v], B * 16 * N * F},
+        {&c.s[v], B * 16 * N * F},
+        {&c.t[v], B * 16 * N * F},
+        {&c.up[v], B * 64 * N * F},
+        {&c.rA[v], B * 64 * N * F},
+        {&c.rB[v], B * 64 * N * F},
+        {&c.hd0[v], B * 64 * N * (F / 2)},
+        {&c.hup[v], B * 256 * N * (F / 2)},
+        {&c.hd2[v], B * 256 * N * f.head_mid},
+        {&c.lf[v], B * N * f.lf_hidden},
+    };
+    req.insert(req.end(), head.begin(), head.end());
+  }
   size_t total = 0;
   for (auto& r : req) total += align256(r.second * sizeof(float));
   GS_CHECK_HIP(hipMalloc(&c.arena, total));
@@ -1004,10 +1065,31 @@ int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2, int32
   float* pts[2] = {pts1, pts2};
   float* conf[2] = {conf1, conf2};
   float* desc[2] = {desc1, desc2};
+  // group the requested heads: slot v runs view hs.id[v]
+  Heads hd, hl;
+  const float *ge[2], *gh6[2], *gh9[2], *gdf[2], *le[2], *ldf[2];
+  float *gp[2], *gc[2], *ld[2];
   for (int v = 0; v < 2; ++v) {
-    if (pts[v]) RC(dpt_head(*c, v + 1, e[v], h6[v], h9[v], df[v], B, pts[v], conf[v], s));
-    if (desc[v]) RC(local_features(*c, v + 1, e[v], df[v], B, desc[v], s));
+    if (pts[v]) {
+      const int k = hd.n++;
+      hd.id[k] = v + 1;
+      ge[k] = e[v];
+      gh6[k] = h6[v];
+      gh9[k] = h9[v];
+      gdf[k] = df[v];
+      gp[k] = pts[v];
+      gc[k] = conf[v];
+    }
+    if (desc[v]) {
+      const int k = hl.n++;
+      hl.id[k] = v + 1;
+      le[k] = e[v];
+      ldf[k] = df[v];
+      ld[k] = desc[v];
+    }
   }
+  if (hd.n) RC(dpt_heads(*c, hd, ge, gh6, gh9, gdf, B, gp, gc, s));
+  if (hl.n) RC(local_features(*c, hl, le, ldf, B, ld, s));
   return 0;
 }
 
