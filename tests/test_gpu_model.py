@@ -148,6 +148,46 @@ def test_config2_full_pair():
     check_pair(got, ref, "config2")
 
 
+def test_config4_grid_pair():
+    """Config 4 geometry: 512x512 images (32x32 grid, 1024 tokens), full model,
+    one pair against the oracle; the batched 32-pair run is covered by batch
+    invariance (bit-exact) below."""
+    case("config4 512x512 pair")
+    cfg = G.default_config(img_h=512, img_w=512)
+    w = weights_for(cfg)
+    n = 3 * 512 * 512
+    i1 = G.seed_uniform(0, "view1", n).reshape(1, 3, 512, 512)
+    i2 = G.seed_uniform(0, "view2", n).reshape(1, 3, 512, 512)
+    m = G.Mastr(cfg, 1)
+    m.init_seeded(0)
+    got = run_pair(m, cfg, i1, i2, 1)
+    m.close()
+    del m
+    torch.cuda.empty_cache()
+    O.set_threads(0)
+    ref = O.mastr_pair(cfg.as_dict(), w, i1, i2)
+    check_pair(got, ref, "config4")
+
+
+def test_config4_batch_invariance_32_pairs():
+    """32 pairs at 512x512 in one launch sequence: pairs 0 and 31 equal the
+    same pairs run alone, bit for bit."""
+    case("config4 32-pair batch invariance")
+    cfg = G.default_config(img_h=512, img_w=512)
+    B = 32
+    n = B * 3 * 512 * 512
+    i1 = G.seed_uniform(0, "view1", n).reshape(B, 3, 512, 512)
+    i2 = G.seed_uniform(0, "view2", n).reshape(B, 3, 512, 512)
+    m = G.Mastr(cfg, B)
+    m.init_seeded(0)
+    full = run_pair(m, cfg, i1, i2, B)
+    for b in (0, B - 1):
+        one = run_pair(m, cfg, i1[b:b + 1], i2[b:b + 1], 1)
+        for k in full:
+            np.testing.assert_array_equal(one[k][0], full[k][b], err_msg=f"{k} pair {b}")
+    m.close()
+
+
 def test_view_swap_symmetry_full_size():
     """With the second decoder chain and head sharing the first's weights,
     swapping the views swaps the outputs (bit for bit) at the config-2 size."""
