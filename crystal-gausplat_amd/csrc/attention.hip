@@ -169,11 +169,172 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
   }
 }
 
+
+// bf16-input / fp32-accumulate variant (v_mfma_f32_32x32x16_bf16), softmax in
+// fp32. Q, K and V are read in fp32 and rounded to bf16 (nearest even).
+//   S^T = K . Q^T: MFMA slice t (hd 16t .. 16t+15) takes, for lane half h,
+//     hd 16t + 8h .. +7 of the lane's key row (A) and query (B).
+//   O^T += V^T . P^T: slice s of a 32-key block takes, for lane half h, keys
+//     {16s + 4h + 0..3, 16s + 8 + 4h + 0..3} -- exactly the keys the lane
+//     holds in S^T accumulator registers 8s .. 8s+7 -- so P is converted in
+//     registers; V is staged transposed in LDS (Vt[hd][key]) so a lane reads
+//     its 2 x 4 keys with two 8-byte loads.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, int32_t Bcount) {
+  const int grp = blockIdx.z / Bcount;
+  const int b = blockIdx.z - grp * Bcount;
+  const AttnArgs& p = batch.g[grp];
+  const int head = blockIdx.y;
+  const int Nq = p.Nq, Nkv = p.Nkv;
+
+  __shared__ __attribute__((aligned(16))) __bf16 Ks[KT][HD + 8];
+  __shared__ __attribute__((aligned(16))) __bf16 Vt[HD][KT + 8];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  const float* qb = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh;
+  const float* kb = p.k + (int64_t)b * p.k_sb + (int64_t)head * p.k_sh;
+  const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)head * p.v_sh;
+  float* ob = p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh;
+
+  const int q0 = blockIdx.x * QT + wave * 32;
+  const float qscale = p.scale * 1.4426950408889634f;
+  bf16x8 qf[4];
+  {
+    const int qrow = min(q0 + l32, Nq - 1);
+    const float* qr = qb + (int64_t)qrow * p.q_sn + hl * 8;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const fx4 v0 = *(const fx4*)(qr + 16 * t);
+      const fx4 v1 = *(const fx4*)(qr + 16 * t + 4);
+      bf16x8 h;
+      h[0] = (__bf16)(v0.x * qscale);
+      h[1] = (__bf16)(v0.y * qscale);
+      h[2] = (__bf16)(v0.z * qscale);
+      h[3] = (__bf16)(v0.w * qscale);
+      h[4] = (__bf16)(v1.x * qscale);
+      h[5] = (__bf16)(v1.y * qscale);
+      h[6] = (__bf16)(v1.z * qscale);
+      h[7] = (__bf16)(v1.w * qscale);
+      qf[t] = h;
+    }
+  }
+
+  floatx16 o0 = {}, o1 = {};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
+  fx4 rk[4], rv[4];
+  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+#define GS_ATT_LOAD(KB)                                                         \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i) {                               \
+    const int key = (KB) + lrow + 16 * i;                                       \
+    const int kc = min(key, Nkv - 1);                                           \
+    const fx4 kk = *(const fx4*)(kb + (int64_t)kc * p.k_sn + lc4);              \
+    const fx4 vv = *(const fx4*)(vb + (int64_t)kc * p.v_sn + lc4);              \
+    rk[i] = key < Nkv ? kk : zero4;                                             \
+    rv[i] = key < Nkv ? vv : zero4;                                             \
+  }
+
+  GS_ATT_LOAD(0)
+  for (int kbase = 0; kbase < Nkv; kbase += KT) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bf16x4 h;
+      h.x = (__bf16)rk[i].x;
+      h.y = (__bf16)rk[i].y;
+      h.z = (__bf16)rk[i].z;
+      h.w = (__bf16)rk[i].w;
+      *(bf16x4*)&Ks[lrow + 16 * i][lc4] = h;
+      const int key = lrow + 16 * i;
+      Vt[lc4 + 0][key] = (__bf16)rv[i].x;
+      Vt[lc4 + 1][key] = (__bf16)rv[i].y;
+      Vt[lc4 + 2][key] = (__bf16)rv[i].z;
+      Vt[lc4 + 3][key] = (__bf16)rv[i].w;
+    }
+    __syncthreads();
+    GS_ATT_LOAD(min(kbase + KT, ((Nkv - 1) / KT) * KT))
+
+#pragma unroll
+    for (int sub = 0; sub < KT / 32; ++sub) {
+      const int sb = kbase + sub * 32;
+      if (sb >= Nkv) break;
+      floatx16 s = {};
+      const __bf16* kr = &Ks[sub * 32 + l32][hl * 8];
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)(kr + 16 * t), qf[t], s, 0, 0,
+                                                    0);
+      if (sb + 32 > Nkv) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = sb + 8 * (r >> 2) + 4 * hl + (r & 3);
+          if (key >= Nkv) s[r] = -INFINITY;
+        }
+      }
+      float mb = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
+      mb = fmaxf(mb, __shfl_xor(mb, 32));
+      const float m_new = fmaxf(m_run, mb);
+      const float alpha = exp2f(m_run - m_new);
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = exp2f(s[r] - m_new);
+        ps += s[r];
+      }
+      l_run = l_run * alpha + ps;
+      m_run = m_new;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        o0[r] *= alpha;
+        o1[r] *= alpha;
+      }
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+        bf16x8 pb;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pb[i] = (__bf16)s[8 * sl + i];
+        const int k0 = sub * 32 + 16 * sl + 4 * hl;
+        const bf16x4 va0 = *(const bf16x4*)&Vt[l32][k0];
+        const bf16x4 va1 = *(const bf16x4*)&Vt[l32][k0 + 8];
+        const bf16x4 vb0 = *(const bf16x4*)&Vt[32 + l32][k0];
+        const bf16x4 vb1 = *(const bf16x4*)&Vt[32 + l32][k0 + 8];
+        const bf16x8 v0 = {va0.x, va0.y, va0.z, va0.w, va1.x, va1.y, va1.z, va1.w};
+        const bf16x8 v1 = {vb0.x, vb0.y, vb0.z, vb0.w, vb1.x, vb1.y, vb1.z, vb1.w};
+        o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, pb, o0, 0, 0, 0);
+        o1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v1, pb, o1, 0, 0, 0);
+      }
+    }
+  }
+#undef GS_ATT_LOAD
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / l_tot;
+  const int q = q0 + l32;
+  if (q < Nq) {
+    float* orow = ob + (int64_t)q * p.o_sn;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      *(fx4*)(orow + 8 * g + 4 * hl) =
+          mk4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv);
+      *(fx4*)(orow + 32 + 8 * g + 4 * hl) =
+          mk4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv);
+    }
+  }
+}
+
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 }  // namespace
 
-int launch_attention(const AttnBatch& bt, hipStream_t s) {
+int launch_attention(const AttnBatch& bt, hipStream_t s, bool bf16) {
   GS_REQUIRE(bt.ngroups >= 1 && bt.ngroups <= kMaxGroups, "attention: bad group count");
   const AttnArgs& a0 = bt.g[0];
   for (int i = 0; i < bt.ngroups; ++i) {
@@ -192,11 +353,14 @@ int launch_attention(const AttnBatch& bt, hipStream_t s) {
   GS_REQUIRE((int64_t)a0.B * bt.ngroups <= 65535 && a0.H <= 65535, "attention: grid too large");
   dim3 grid((a0.Nq + QT - 1) / QT, a0.H, a0.B * bt.ngroups), block(256);
   hipEvent_t ev = prof_start(s);
-  hipLaunchKernelGGL(attn_fwd_kernel, grid, block, 0, s, bt, a0.B);
+  if (bf16)
+    hipLaunchKernelGGL(attn_fwd_bf16_kernel, grid, block, 0, s, bt, a0.B);
+  else
+    hipLaunchKernelGGL(attn_fwd_kernel, grid, block, 0, s, bt, a0.B);
   GS_CHECK_HIP(hipGetLastError());
   if (ev) {
     const double units = (double)a0.B * a0.H * bt.ngroups;
-    std::string nm = "attn_fwd_kernel";
+    std::string nm = bf16 ? "attn_fwd_bf16_kernel" : "attn_fwd_kernel";
     if (prof_per_shape())
       nm += " B=" + std::to_string(a0.B) + " H=" + std::to_string(a0.H) + " Nq=" +
             std::to_string(a0.Nq) + " groups=" + std::to_string(bt.ngroups);

@@ -384,3 +384,35 @@ int launch_convt_relayout(const float* w, const float* b, int32_t Cin, int32_t C
 }
 
 }  // namespace gs
+
+namespace gs {
+namespace {
+
+// fp32 -> bf16, round to nearest even (the weight copies of the bf16 path).
+__global__ void f32_to_bf16_kernel(const float* __restrict__ in, __bf16* __restrict__ out,
+                                   int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    const fx4 v = *(const fx4*)(in + i);
+    out[i] = (__bf16)v.x;
+    out[i + 1] = (__bf16)v.y;
+    out[i + 2] = (__bf16)v.z;
+    out[i + 3] = (__bf16)v.w;
+  } else {
+    for (int64_t j = i; j < n; ++j) out[j] = (__bf16)in[j];
+  }
+}
+
+}  // namespace
+
+int launch_f32_to_bf16(const float* in, void* out, int64_t n, hipStream_t s) {
+  if (n <= 0) return 0;
+  GS_REQUIRE(((uintptr_t)in & 15) == 0, "f32_to_bf16: input must be 16-byte aligned");
+  const int64_t threads = (n + 3) / 4;
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s,
+                     in, (__bf16*)out, n);
+  GS_CHECK_HIP(hipGetLastError());
+  return 0;
+}
+
+}  // namespace gs

@@ -45,168 +45,14 @@ __device__ __forceinline__ fx4 relu4(fx4 v) {
                      fmaxf(v.w, 0.f));
 }
 
-template <int ALOAD, int BLAYOUT, bool A_RELU>
-__global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
-  const GemmArgs& p = batch.g[blockIdx.z];
-  const int M = p.M, N = p.N, K = p.K;
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  const int ntiles = tiles_m * tiles_n;
-
-  // XCD-aware remap: workgroups are dealt round-robin to the 8 XCDs; give
-  // each XCD a contiguous range of logical tiles so neighbouring tiles (which
-  // share A rows / B columns) meet in the same L2.
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-  if (bid >= ntiles) return;
-  // Grouped ordering: GROUP_M row tiles sweep the column tiles together.
-  const int per_group = GROUP_M * tiles_n;
-  const int gid = bid / per_group;
-  const int first_m = gid * GROUP_M;
-  const int gsz = min(tiles_m - first_m, GROUP_M);
-  const int tm = first_m + (bid % per_group) % gsz;
-  const int tn = (bid % per_group) / gsz;
-  const int m0 = tm * BM, n0 = tn * BN;
-
-  __shared__ __attribute__((aligned(16))) float As[BM][LDS];
-  __shared__ __attribute__((aligned(16))) float Bs[BN][LDS];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, hl = lane >> 5;
-
-  // Global->LDS assignment: rows tid/8 + 32*i, fx4 column tid%8.
-  const int lrow = tid >> 3, lc4 = (tid & 7) * 4;
-
-  // Per-row load state, computed once. Loads are branch-free: every address is
-  // clamped into its buffer and out-of-range rows / taps are zeroed with a
-  // select, so the loads of the next K step issue as one straight-line block.
-  int arow[4];          // clamped A row (plain / concat), or conv output pixel
-  bool aval[4];
-  int cimg[4], coh[4], cow[4];
-  int boff[4];          // B row offsets (N * ldb < 2^31 is checked on the host)
-  bool bval_[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int m = m0 + lrow + 32 * i;
-    aval[i] = m < M;
-    arow[i] = min(m, M - 1);
-    if (ALOAD == A_CONV) {
-      const int hw = p.cHo * p.cWo;
-      cimg[i] = arow[i] / hw;
-      const int rem = arow[i] - cimg[i] * hw;
-      coh[i] = rem / p.cWo;
-      cow[i] = rem - coh[i] * p.cWo;
-    }
-    if (BLAYOUT == B_NT) {
-      const int n = n0 + lrow + 32 * i;
-      bval_[i] = n < N;
-      boff[i] = min(n, N - 1) * (int)p.ldb + lc4;
-    }
-  }
-  int bncol = 0;
-  bool bnval = true;
-  if (BLAYOUT == B_NN) {
-    const int n = n0 + 4 * (tid & 31);
-    bnval = n < N;
-    bncol = min(n, N - 4);
-  }
-
-  fx4 ra[4], rb[4];
-  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
-
-// Global loads of one K step into registers (macro rather than lambda so the
-// register arrays stay in VGPRs).
-#define GS_GEMM_LOAD(K0)                                                                 \
-  {                                                                                      \
-    const int k0_ = (K0);                                                                \
-    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                      \
-      fx4 v;                                                                             \
-      bool ok = aval[i];                                                                 \
-      if (ALOAD == A_PLAIN) {                                                            \
-        v = *(const fx4*)(p.A + (int64_t)arow[i] * p.lda + k0_ + lc4);                   \
-      } else if (ALOAD == A_CONCAT) {                                                    \
-        const bool first = k0_ < p.K1;                                                   \
-        const float* base = first ? p.A : p.A2;                                          \
-        const int64_t ld = first ? p.lda : p.lda2;                                       \
-        const int kc = first ? k0_ : k0_ - p.K1;                                         \
-        v = *(const fx4*)(base + (int64_t)arow[i] * ld + kc + lc4);                      \
-      } else {                                                                           \
-        const int kk = k0_ / p.cCin;                                                     \
-        const int ic0 = k0_ - kk * p.cCin;                                               \
-        const int kh = kk / p.ck, kw = kk - kh * p.ck;                                   \
-        const int ih = coh[i] * p.cs + kh - p.cp;                                        \
-        const int iw = cow[i] * p.cs + kw - p.cp;                                        \
-        ok = ok && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW;                         \
-        const int ihc = min(max(ih, 0), p.cH - 1), iwc = min(max(iw, 0), p.cW - 1);      \
-        v = *(const fx4*)(p.A + (((int64_t)cimg[i] * p.cH + ihc) * p.cW + iwc) * p.cCin + \
-                          ic0 + lc4);                                                    \
-      }                                                                                  \
-      v = ok ? v : zero4;                                                                \
-      if (A_RELU) v = relu4(v);                                                          \
-      ra[i] = v;                                                                         \
-      if (BLAYOUT == B_NT) {                                                             \
-        const fx4 w = *(const fx4*)(p.B + boff[i] + k0_);                                \
-        rb[i] = bval_[i] ? w : zero4;                                                    \
-      } else {                                                                           \
-        const int kb = (tid >> 5) + 8 * i;                                               \
-        const fx4 w = *(const fx4*)(p.B + (int64_t)(k0_ + kb) * p.ldb + bncol);          \
-        rb[i] = bnval ? w : zero4;                                                       \
-      }                                                                                  \
-    }                                                                                    \
-  }
-
-  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
-
-  GS_GEMM_LOAD(0)
-  for (int k0 = 0; k0 < K; k0 += BK) {
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *(fx4*)&As[lrow + 32 * i][lc4] = ra[i];
-      if (BLAYOUT == B_NT) {
-        *(fx4*)&Bs[lrow + 32 * i][lc4] = rb[i];
-      } else {
-        const int kb = (tid >> 5) + 8 * i;
-        const int n = 4 * (tid & 31);
-        Bs[n + 0][kb] = rb[i].x;
-        Bs[n + 1][kb] = rb[i].y;
-        Bs[n + 2][kb] = rb[i].z;
-        Bs[n + 3][kb] = rb[i].w;
-      }
-    }
-    __syncthreads();
-    // Prefetch the next K step (the last iteration reloads its own step:
-    // in bounds, and the values are never stored).
-    GS_GEMM_LOAD(min(k0 + BK, K - BK))
-    const float* a0p = &As[wm * 64 + l32][hl * 16];
-    const float* a1p = &As[wm * 64 + 32 + l32][hl * 16];
-    const float* b0p = &Bs[wn * 64 + l32][hl * 16];
-    const float* b1p = &Bs[wn * 64 + 32 + l32][hl * 16];
-#pragma unroll
-    for (int t4 = 0; t4 < 4; ++t4) {
-      const fx4 a0 = *(const fx4*)(a0p + t4 * 4);
-      const fx4 a1 = *(const fx4*)(a1p + t4 * 4);
-      const fx4 b0 = *(const fx4*)(b0p + t4 * 4);
-      const fx4 b1 = *(const fx4*)(b1p + t4 * 4);
-#define GS_MFMA4(AX, BX)                                                           \
-  acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.AX, b0.BX, acc00, 0, 0, 0);     \
-  acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.AX, b1.BX, acc01, 0, 0, 0);     \
-  acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.AX, b0.BX, acc10, 0, 0, 0);     \
-  acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.AX, b1.BX, acc11, 0, 0, 0);
-      GS_MFMA4(x, x)
-      GS_MFMA4(y, y)
-      GS_MFMA4(z, z)
-      GS_MFMA4(w, w)
-#undef GS_MFMA4
-    }
-  }
-#undef GS_GEMM_LOAD
-
-  // ---- epilogue ----
-  // Accumulator layout of a 32x32 block: lane l, register r holds
-  // row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
+// Bias, RoPE, GELU / ReLU, residuals and the (scatter) store of a wave's
+// 64x64 sub-tile. Accumulator layout of a 32x32 block: lane l, register r
+// holds row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16& acc00,
+                                              const floatx16& acc01, const floatx16& acc10,
+                                              const floatx16& acc11, int m0, int n0, int wm,
+                                              int wn, int l32, int hl) {
+  const int M = p.M, N = p.N;
   const int flags = p.flags;
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi) {
@@ -261,6 +107,277 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
       }
     }
   }
+}
+
+// Global loads of one K step into registers (macros rather than lambdas so the
+// register arrays stay in VGPRs). They use the kernel's per-row state
+// (arow, aval, cimg/coh/cow, boff/bval_, bncol/bnval).
+#define GS_LOAD_A(K0)                                                                    \
+  {                                                                                      \
+    const int k0_ = (K0);                                                                \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                      \
+      fx4 v;                                                                             \
+      bool ok = aval[i];                                                                 \
+      if (ALOAD == A_PLAIN) {                                                            \
+        v = *(const fx4*)(p.A + (int64_t)arow[i] * p.lda + k0_ + lc4);                   \
+      } else if (ALOAD == A_CONCAT) {                                                    \
+        const bool first = k0_ < p.K1;                                                   \
+        const float* base = first ? p.A : p.A2;                                          \
+        const int64_t ld = first ? p.lda : p.lda2;                                       \
+        const int kc = first ? k0_ : k0_ - p.K1;                                         \
+        v = *(const fx4*)(base + (int64_t)arow[i] * ld + kc + lc4);                      \
+      } else {                                                                           \
+        const int kk = k0_ / p.cCin;                                                     \
+        const int ic0 = k0_ - kk * p.cCin;                                               \
+        const int kh = kk / p.ck, kw = kk - kh * p.ck;                                   \
+        const int ih = coh[i] * p.cs + kh - p.cp;                                        \
+        const int iw = cow[i] * p.cs + kw - p.cp;                                        \
+        ok = ok && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW;                         \
+        const int ihc = min(max(ih, 0), p.cH - 1), iwc = min(max(iw, 0), p.cW - 1);      \
+        v = *(const fx4*)(p.A + (((int64_t)cimg[i] * p.cH + ihc) * p.cW + iwc) * p.cCin + \
+                          ic0 + lc4);                                                    \
+      }                                                                                  \
+      v = ok ? v : zero4;                                                                \
+      if (A_RELU) v = relu4(v);                                                          \
+      ra[i] = v;                                                                         \
+    }                                                                                    \
+  }
+
+#define GS_LOAD_B_F32(K0)                                                                \
+  {                                                                                      \
+    const int k0_ = (K0);                                                                \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                      \
+      if (BLAYOUT == B_NT) {                                                             \
+        const fx4 w = *(const fx4*)(p.B + boff[i] + k0_);                                \
+        rb[i] = bval_[i] ? w : zero4;                                                    \
+      } else {                                                                           \
+        const int kb = (tid >> 5) + 8 * i;                                               \
+        const fx4 w = *(const fx4*)(p.B + (int64_t)(k0_ + kb) * p.ldb + bncol);          \
+        rb[i] = bnval ? w : zero4;                                                       \
+      }                                                                                  \
+    }                                                                                    \
+  }
+
+// Per-row load state shared by the fp32 and bf16 kernels: every address is
+// clamped into its buffer and out-of-range rows / taps are zeroed with a
+// select, so the loads of the next K step issue as one straight-line block.
+#define GS_ROW_STATE()                                                                   \
+  int arow[4];                                                                           \
+  bool aval[4];                                                                          \
+  int cimg[4], coh[4], cow[4];                                                           \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                        \
+    const int m = m0 + lrow + 32 * i;                                                    \
+    aval[i] = m < M;                                                                     \
+    arow[i] = min(m, M - 1);                                                             \
+    if (ALOAD == A_CONV) {                                                               \
+      const int hw = p.cHo * p.cWo;                                                      \
+      cimg[i] = arow[i] / hw;                                                            \
+      const int rem = arow[i] - cimg[i] * hw;                                            \
+      coh[i] = rem / p.cWo;                                                              \
+      cow[i] = rem - coh[i] * p.cWo;                                                     \
+    }                                                                                    \
+  }
+
+// Tile coordinates of this workgroup (XCD-aware remap + grouped ordering);
+// false when the workgroup has no tile in this group's problem.
+__device__ __forceinline__ bool gemm_tile(const GemmArgs& p, int& m0, int& n0) {
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+  const int ntiles = tiles_m * tiles_n;
+  // Workgroups are dealt round-robin to the 8 XCDs; give each XCD a
+  // contiguous range of logical tiles so neighbouring tiles (which share A
+  // rows / B columns) meet in the same L2.
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  if (bid >= ntiles) return false;
+  // Grouped ordering: GROUP_M row tiles sweep the column tiles together.
+  const int per_group = GROUP_M * tiles_n;
+  const int gid = bid / per_group;
+  const int first_m = gid * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  m0 = (first_m + (bid % per_group) % gsz) * BM;
+  n0 = ((bid % per_group) / gsz) * BN;
+  return true;
+}
+
+template <int ALOAD, int BLAYOUT, bool A_RELU>
+__global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int M = p.M, N = p.N, K = p.K;
+  int m0, n0;
+  if (!gemm_tile(p, m0, n0)) return;
+
+  __shared__ __attribute__((aligned(16))) float As[BM][LDS];
+  __shared__ __attribute__((aligned(16))) float Bs[BN][LDS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  // Global->LDS assignment: rows tid/8 + 32*i, fx4 column tid%8.
+  const int lrow = tid >> 3, lc4 = (tid & 7) * 4;
+
+  GS_ROW_STATE()
+  int boff[4];          // B row offsets (N * ldb < 2^31 is checked on the host)
+  bool bval_[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (BLAYOUT == B_NT) {
+      const int n = n0 + lrow + 32 * i;
+      bval_[i] = n < N;
+      boff[i] = min(n, N - 1) * (int)p.ldb + lc4;
+    }
+  }
+  int bncol = 0;
+  bool bnval = true;
+  if (BLAYOUT == B_NN) {
+    const int n = n0 + 4 * (tid & 31);
+    bnval = n < N;
+    bncol = min(n, N - 4);
+  }
+
+  fx4 ra[4], rb[4];
+  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+
+  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+
+  GS_LOAD_A(0)
+  GS_LOAD_B_F32(0)
+  for (int k0 = 0; k0 < K; k0 += BK) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      *(fx4*)&As[lrow + 32 * i][lc4] = ra[i];
+      if (BLAYOUT == B_NT) {
+        *(fx4*)&Bs[lrow + 32 * i][lc4] = rb[i];
+      } else {
+        const int kb = (tid >> 5) + 8 * i;
+        const int n = 4 * (tid & 31);
+        Bs[n + 0][kb] = rb[i].x;
+        Bs[n + 1][kb] = rb[i].y;
+        Bs[n + 2][kb] = rb[i].z;
+        Bs[n + 3][kb] = rb[i].w;
+      }
+    }
+    __syncthreads();
+    // Prefetch the next K step (the last iteration reloads its own step:
+    // in bounds, and the values are never stored).
+    GS_LOAD_A(min(k0 + BK, K - BK))
+    GS_LOAD_B_F32(min(k0 + BK, K - BK))
+    const float* a0p = &As[wm * 64 + l32][hl * 16];
+    const float* a1p = &As[wm * 64 + 32 + l32][hl * 16];
+    const float* b0p = &Bs[wn * 64 + l32][hl * 16];
+    const float* b1p = &Bs[wn * 64 + 32 + l32][hl * 16];
+#pragma unroll
+    for (int t4 = 0; t4 < 4; ++t4) {
+      const fx4 a0 = *(const fx4*)(a0p + t4 * 4);
+      const fx4 a1 = *(const fx4*)(a1p + t4 * 4);
+      const fx4 b0 = *(const fx4*)(b0p + t4 * 4);
+      const fx4 b1 = *(const fx4*)(b1p + t4 * 4);
+#define GS_MFMA4(AX, BX)                                                           \
+  acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.AX, b0.BX, acc00, 0, 0, 0);     \
+  acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.AX, b1.BX, acc01, 0, 0, 0);     \
+  acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.AX, b0.BX, acc10, 0, 0, 0);     \
+  acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.AX, b1.BX, acc11, 0, 0, 0);
+      GS_MFMA4(x, x)
+      GS_MFMA4(y, y)
+      GS_MFMA4(z, z)
+      GS_MFMA4(w, w)
+#undef GS_MFMA4
+    }
+  }
+
+  gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+}
+
+
+// bf16-input / fp32-accumulate variant (v_mfma_f32_32x32x16_bf16): same tile,
+// loaders and epilogue as the fp32 kernel; A is read in fp32 and rounded to
+// bf16 (round-to-nearest-even) on its way into LDS, B is a bf16 copy of the
+// weights ([N, K], NT layout). Within one K step of 32, MFMA slice s (0..1)
+// feeds lane l (half h = l/32) with k = 16s + 8h .. 16s + 8h + 7, one
+// ds_read_b128 per operand block. LDS rows are 40 bf16 (80 B).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+constexpr int LDSH = BK + 8;
+
+template <int ALOAD, bool A_RELU>
+__global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
+  constexpr int BLAYOUT = B_NT;
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int M = p.M, N = p.N, K = p.K;
+  int m0, n0;
+  if (!gemm_tile(p, m0, n0)) return;
+
+  __shared__ __attribute__((aligned(16))) __bf16 As[BM][LDSH];
+  __shared__ __attribute__((aligned(16))) __bf16 Bs[BN][LDSH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int lrow = tid >> 3, lc4 = (tid & 7) * 4;
+
+  GS_ROW_STATE()
+  // B (bf16): rows tid/4 + 64*j (j < 2), 8 bf16 at column 8*(tid%4)
+  const __bf16* Bh = (const __bf16*)p.Bh;
+  const int brow = tid >> 2, bc8 = (tid & 3) * 8;
+  int bo[2];
+  bool bok[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + brow + 64 * j;
+    bok[j] = n < N;
+    bo[j] = min(n, N - 1) * (int)p.ldb + bc8;
+  }
+
+  fx4 ra[4];
+  bf16x8 rbh[2];
+  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+  const bf16x8 zero8 = {};
+
+  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+
+#define GS_LOAD_B_BF16(K0)                                                       \
+  _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                \
+    const bf16x8 w = *(const bf16x8*)(Bh + bo[j] + (K0));                        \
+    rbh[j] = bok[j] ? w : zero8;                                                 \
+  }
+
+  GS_LOAD_A(0)
+  GS_LOAD_B_BF16(0)
+  for (int k0 = 0; k0 < K; k0 += BK) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      bf16x4 h;
+      h.x = (__bf16)ra[i].x;
+      h.y = (__bf16)ra[i].y;
+      h.z = (__bf16)ra[i].z;
+      h.w = (__bf16)ra[i].w;
+      *(bf16x4*)&As[lrow + 32 * i][lc4] = h;
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) *(bf16x8*)&Bs[brow + 64 * j][bc8] = rbh[j];
+    __syncthreads();
+    GS_LOAD_A(min(k0 + BK, K - BK))
+    GS_LOAD_B_BF16(min(k0 + BK, K - BK))
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      const int kc = sl * 16 + hl * 8;
+      const bf16x8 a0 = *(const bf16x8*)&As[wm * 64 + l32][kc];
+      const bf16x8 a1 = *(const bf16x8*)&As[wm * 64 + 32 + l32][kc];
+      const bf16x8 b0 = *(const bf16x8*)&Bs[wn * 64 + l32][kc];
+      const bf16x8 b1 = *(const bf16x8*)&Bs[wn * 64 + 32 + l32][kc];
+      acc00 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc00, 0, 0, 0);
+      acc01 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc01, 0, 0, 0);
+      acc10 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc10, 0, 0, 0);
+      acc11 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, acc11, 0, 0, 0);
+    }
+  }
+#undef GS_LOAD_B_BF16
+  gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -319,12 +436,15 @@ int check_gemm(const GemmArgs& a, int aload, int blayout) {
 }
 
 int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
-                hipStream_t s) {
+                hipStream_t s, bool bf16) {
   GS_REQUIRE(b.ngroups >= 1 && b.ngroups <= kMaxGroups, "gemm: bad group count");
   int max_tiles = 0;
   for (int i = 0; i < b.ngroups; ++i) {
     int rc = check_gemm(b.g[i], aload, blayout);
     if (rc) return rc;
+    if (bf16)
+      GS_REQUIRE(blayout == B_NT && b.g[i].Bh && aligned16(b.g[i].Bh) && b.g[i].ldb % 8 == 0,
+                 "gemm: bf16 needs a 16-byte aligned bf16 weight copy in the NT layout");
     const int t = ((b.g[i].M + BM - 1) / BM) * ((b.g[i].N + BN - 1) / BN);
     max_tiles = t > max_tiles ? t : max_tiles;
   }
@@ -337,8 +457,22 @@ int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
       flops += 2.0 * g.M * (double)g.N * g.K;
       bytes += 4.0 * ((double)g.M * g.K + (double)g.N * g.K + (double)g.M * g.N);
     }
+#define GS_GEMM_BF16_CASE(AL, RL)                                             \
+  if (bf16 && aload == AL && a_relu == RL) {                                  \
+    hipEvent_t ev = prof_start(s);                                            \
+    hipLaunchKernelGGL((gemm_bf16_kernel<AL, RL>), grid, block, 0, s, b);     \
+    GS_CHECK_HIP(hipGetLastError());                                          \
+    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_bf16_kernel<" #AL "," #RL ">", b).c_str(), \
+                      flops, bytes);                                          \
+    return 0;                                                                 \
+  }
+  GS_GEMM_BF16_CASE(A_PLAIN, false)
+  GS_GEMM_BF16_CASE(A_CONCAT, false)
+  GS_GEMM_BF16_CASE(A_CONV, false)
+  GS_GEMM_BF16_CASE(A_CONV, true)
+#undef GS_GEMM_BF16_CASE
 #define GS_GEMM_CASE(AL, BL, RL)                                              \
-  if (aload == AL && blayout == BL && a_relu == RL) {                         \
+  if (!bf16 && aload == AL && blayout == BL && a_relu == RL) {                \
     hipEvent_t ev = prof_start(s);                                            \
     hipLaunchKernelGGL((gemm_f32_kernel<AL, BL, RL>), grid, block, 0, s, b);  \
     GS_CHECK_HIP(hipGetLastError());                                          \

@@ -75,6 +75,7 @@ struct GemmArgs {
   // (kh*ck + kw)*cCin + ic
   int32_t cH, cW, cCin, ck, cs, cp, cHo, cWo;
   const float* B;   // NT: B[n*ldb + k]; NN: B[k*ldb + n]
+  const void* Bh;   // bf16 copy of B (NT layout, same ldb) for the bf16 kernels
   int64_t ldb;
   float* C;
   int64_t ldc;
@@ -103,8 +104,9 @@ struct GemmBatch {
 };
 
 // Launch a grouped GEMM (all groups must share the loader / layout kinds).
+// bf16: bf16-input / fp32-accumulate MFMA on the groups' Bh weight copies.
 int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
-                hipStream_t s);
+                hipStream_t s, bool bf16 = false);
 int check_gemm(const GemmArgs& a, int aload, int blayout);
 
 // ---- attention -----------------------------------------------------------------
@@ -121,7 +123,7 @@ struct AttnBatch {
   AttnArgs g[kMaxGroups];
   int32_t ngroups;
 };
-int launch_attention(const AttnBatch& b, hipStream_t s);
+int launch_attention(const AttnBatch& b, hipStream_t s, bool bf16 = false);
 
 // ---- LayerNorm -----------------------------------------------------------------
 struct LnArgs {
@@ -162,6 +164,9 @@ int launch_oihw_to_ohwi(const float* w, int32_t Cout, int32_t Cin, int32_t k,
 int launch_convt_relayout(const float* w, const float* b, int32_t Cin,
                           int32_t Cout, int32_t k, float* wout, float* bout,
                           hipStream_t s);
+
+// fp32 -> bf16 (round to nearest even), n elements.
+int launch_f32_to_bf16(const float* in, void* out, int64_t n, hipStream_t s);
 
 // RoPE tables for 64-wide heads: cos/sin [max_pos][16], host computed.
 void rope_table_host(int32_t max_pos, float base, float* cos_t, float* sin_t);

@@ -168,6 +168,8 @@ struct Ctx {
   std::map<std::string, float*> derived;  // kv weights etc. by name
   char* warena = nullptr;
   size_t warena_size = 0;
+  char* wbf16 = nullptr;     // bf16 mirror of warena (precision 1)
+  bool bf16_dirty = true;
   char* arena = nullptr;
   size_t arena_size = 0;
   // workspaces
@@ -214,19 +216,32 @@ void with_rope(GemmArgs& a, const Ctx& c, int ncols) {
   a.grid_w = c.gw;
 }
 
-int run1(const GemmArgs& a, int aload, hipStream_t s, bool relu_in = false) {
+// All context GEMMs go through here: in the bf16 precision mode each group's
+// weight operand is redirected to its bf16 mirror.
+int gemm(const Ctx& c, GemmBatch& b, int aload, bool relu_in, hipStream_t s) {
+  const bool bf = c.cfg.precision == 1;
+  if (bf)
+    for (int i = 0; i < b.ngroups; ++i) {
+      const char* w = (const char*)b.g[i].B;
+      GS_REQUIRE(w >= c.warena && w < c.warena + c.warena_size, "gemm: weight outside the arena");
+      b.g[i].Bh = c.wbf16 + (w - c.warena) / 2;
+    }
+  return launch_gemm(b, aload, B_NT, relu_in, s, bf);
+}
+
+int run1(const Ctx& c, const GemmArgs& a, int aload, hipStream_t s, bool relu_in = false) {
   GemmBatch b;
   b.g[0] = a;
   b.ngroups = 1;
-  return launch_gemm(b, aload, B_NT, relu_in, s);
+  return gemm(c, b, aload, relu_in, s);
 }
 
-int run2(const GemmArgs& a0, const GemmArgs& a1, int aload, hipStream_t s) {
+int run2(const Ctx& c, const GemmArgs& a0, const GemmArgs& a1, int aload, hipStream_t s) {
   GemmBatch b;
   b.g[0] = a0;
   b.g[1] = a1;
   b.ngroups = 2;
-  return launch_gemm(b, aload, B_NT, false, s);
+  return gemm(c, b, aload, false, s);
 }
 
 #define RC(expr)              \
@@ -254,7 +269,7 @@ int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, fl
       a.R1 = C;
       a.ldr1 = ldc;
     }
-    return run1(a, A_PLAIN, s);
+    return run1(c, a, A_PLAIN, s);
   }
   const int Ng = N / groups;
   for (int g = 0; g < groups; ++g) {
@@ -322,7 +337,7 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   ab.g[0] = attn_args(c.qkv, 3 * D, c.qkv + D, 3 * D, c.qkv + 2 * D, 3 * D, c.att, D,
                       (int)(M / c.N), H, c.N);
   ab.ngroups = 1;
-  RC(launch_attention(ab, s));
+  RC(launch_attention(ab, s, c.cfg.precision == 1));
   RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s));
   RC(layernorm1(x, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias"), c.h, M, D, f.ln_eps, s));
   RC(linear_mode(c, p + ".mlp.fc1", c.h, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D, EPI_GELU, s));
@@ -353,8 +368,8 @@ int decoder(Ctx& c, int B, hipStream_t s) {
   const int64_t Mv = (int64_t)B * c.N, M = 2 * Mv;
   const float eps = f.ln_eps;
   const bool rope = f.rope_mode == 1;
-  RC(run1(lin(c.enc, De, W(c, "decoder_embed.weight"), W(c, "decoder_embed.bias"), c.d, D, M, D,
-              De, 0),
+  RC(run1(c, lin(c.enc, De, W(c, "decoder_embed.weight"), W(c, "decoder_embed.bias"), c.d, D, M, D,
+                 De, 0),
           A_PLAIN, s));
   for (int l = 0; l < f.dec_depth; ++l) {
     std::string p[2] = {"dec_blocks." + std::to_string(l), "dec_blocks2." + std::to_string(l)};
@@ -384,7 +399,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
                    2 * D, Mv, 2 * D, D, 0);
         if (rope) with_rope(a[k], c, D);
       }
-      RC(run2(a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], A_PLAIN, s));
     }
     // self-attention
     RC(ln2(".norm1", dc, hc));
@@ -395,20 +410,20 @@ int decoder(Ctx& c, int B, hipStream_t s) {
                    qkvc[k], 3 * D, Mv, 3 * D, D, 0);
         if (rope) with_rope(a[k], c, 2 * D);
       }
-      RC(run2(a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], A_PLAIN, s));
       AttnBatch ab;
       for (int k = 0; k < 2; ++k)
         ab.g[k] = attn_args(qkvc[k], 3 * D, qkvc[k] + D, 3 * D, qkvc[k] + 2 * D, 3 * D, ac[k], D, B,
                             H, c.N);
       ab.ngroups = 2;
-      RC(launch_attention(ab, s));
+      RC(launch_attention(ab, s, c.cfg.precision == 1));
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(ac[k], D, W(c, p[k] + ".attn.proj.weight"), W(c, p[k] + ".attn.proj.bias"),
                    dc[k], D, Mv, D, D, EPI_RES1);
         a[k].R1 = dc[k];
         a[k].ldr1 = D;
       }
-      RC(run2(a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], A_PLAIN, s));
     }
     // cross-attention (query norm3, reference role naming)
     RC(ln2(".norm3", dc, hc));
@@ -419,19 +434,19 @@ int decoder(Ctx& c, int B, hipStream_t s) {
                    W(c, p[k] + ".cross_attn.projq.bias"), qc[k], D, Mv, D, D, 0);
         if (rope) with_rope(a[k], c, D);
       }
-      RC(run2(a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], A_PLAIN, s));
       AttnBatch ab;
       for (int k = 0; k < 2; ++k)
         ab.g[k] = attn_args(qc[k], D, kvc[k], 2 * D, kvc[k] + D, 2 * D, ac[k], D, B, H, c.N);
       ab.ngroups = 2;
-      RC(launch_attention(ab, s));
+      RC(launch_attention(ab, s, c.cfg.precision == 1));
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(ac[k], D, W(c, p[k] + ".cross_attn.proj.weight"),
                    W(c, p[k] + ".cross_attn.proj.bias"), dc[k], D, Mv, D, D, EPI_RES1);
         a[k].R1 = dc[k];
         a[k].ldr1 = D;
       }
-      RC(run2(a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], A_PLAIN, s));
     }
     // MLP (norm2, reference role naming)
     RC(ln2(".norm2", dc, hc));
@@ -440,14 +455,14 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       for (int k = 0; k < 2; ++k)
         a[k] = lin(hc[k], D, W(c, p[k] + ".mlp.fc1.weight"), W(c, p[k] + ".mlp.fc1.bias"), mc[k],
                    f.dec_mlp, Mv, f.dec_mlp, D, EPI_GELU);
-      RC(run2(a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], A_PLAIN, s));
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(mc[k], f.dec_mlp, W(c, p[k] + ".mlp.fc2.weight"), W(c, p[k] + ".mlp.fc2.bias"),
                    dc[k], D, Mv, D, f.dec_mlp, EPI_RES1);
         a[k].R1 = dc[k];
         a[k].ldr1 = D;
       }
-      RC(run2(a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], A_PLAIN, s));
     }
     if (f.dpt_hooks[1] == l + 1)
       GS_CHECK_HIP(hipMemcpyAsync(c.hook1, c.d, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
@@ -503,7 +518,7 @@ int conv(Ctx& c, const Heads& hs, const std::string& suffix, const float* const 
     b.g[v] = a;
   }
   const bool pointwise = (k == 1 && stride == 1 && pad == 0);
-  return launch_gemm(b, pointwise ? A_PLAIN : A_CONV, B_NT, relu_in, s);
+  return gemm(c, b, pointwise ? A_PLAIN : A_CONV, relu_in, s);
 }
 
 // ConvTranspose (k == s) from [rows, Cin] token tensors on the gh x gw grid.
@@ -522,7 +537,7 @@ int convt(Ctx& c, const Heads& hs, const std::string& suffix, const float* const
     a.sc_gw = c.gw;
     b.g[v] = a;
   }
-  return launch_gemm(b, A_PLAIN, B_NT, false, s);
+  return gemm(c, b, A_PLAIN, false, s);
 }
 
 // FeatureFusionBlock: out = out_conv(up2(RCU2(x0 (+ RCU1(x1))))). The 1x1
@@ -632,8 +647,8 @@ int local_features(Ctx& c, const Heads& hs, const float* const e[2], const float
     g.sc_gw = c.gw;
     b2.g[v] = g;
   }
-  RC(launch_gemm(b1, A_CONCAT, B_NT, false, s));
-  return launch_gemm(b2, A_PLAIN, B_NT, false, s);
+  RC(gemm(c, b1, A_CONCAT, false, s));
+  return gemm(c, b2, A_PLAIN, false, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -698,6 +713,15 @@ int place_weight(Ctx& c, const std::string& name, const float* host, int64_t n) 
     }
   }
   GS_CHECK_HIP(hipMemcpy(dst, src, count * sizeof(float), hipMemcpyHostToDevice));
+  c.bf16_dirty = true;
+  return 0;
+}
+
+// Refresh the bf16 weight mirror after weight updates (precision 1).
+int sync_bf16(Ctx& c, hipStream_t s) {
+  if (c.cfg.precision != 1 || !c.bf16_dirty) return 0;
+  RC(launch_f32_to_bf16((const float*)c.warena, c.wbf16, (int64_t)(c.warena_size / 4), s));
+  c.bf16_dirty = false;
   return 0;
 }
 
@@ -728,6 +752,7 @@ int build_weights(Ctx& c) {
   for (auto& ds : derived_sizes) total += align256(ds.second * sizeof(float));
   GS_CHECK_HIP(hipMalloc(&c.warena, total));
   c.warena_size = total;
+  if (f.precision == 1) GS_CHECK_HIP(hipMalloc(&c.wbf16, total / 2));
   char* cur = c.warena;
   auto take = [&](int64_t nfl) {
     float* p = (float*)cur;
@@ -882,6 +907,8 @@ int validate_config(const gs_mastr_config& f) {
   GS_REQUIRE(f.desc_dim > 0 && (f.patch * f.patch * f.desc_dim) % 32 == 0, "config: bad desc_dim");
   GS_REQUIRE(f.linear_layout == 0 || f.linear_layout == 1, "config: linear_layout must be 0 or 1");
   GS_REQUIRE(f.rope_mode >= 0 && f.rope_mode <= 2, "config: rope_mode must be 0, 1 or 2");
+  GS_REQUIRE(f.precision == 0 || (f.precision == 1 && f.linear_layout == 0),
+             "config: precision must be 0 (fp32) or 1 (bf16 MFMA, linear_layout 0)");
   GS_REQUIRE(f.enc_dim % 32 == 0 && f.dec_dim % 32 == 0, "config: dims must be multiples of 32");
   return 0;
 }
@@ -922,6 +949,7 @@ void gs_mastr_default_config(gs_mastr_config* c) {
   c->rope_base = 100.0f;
   c->linear_layout = 0;
   c->rope_mode = 1;
+  c->precision = 0;
 }
 
 int32_t gs_mastr_weight_count(const gs_mastr_config* cfg) {
@@ -1000,6 +1028,7 @@ void gs_hip_mastr_destroy(void* ctx) {
   Ctx* c = (Ctx*)ctx;
   hipDeviceSynchronize();
   if (c->warena) hipFree(c->warena);
+  if (c->wbf16) hipFree(c->wbf16);
   if (c->arena) hipFree(c->arena);
   delete c;
 }
@@ -1029,6 +1058,7 @@ int32_t gs_hip_mastr_encoder_block(void* ctx, int32_t layer, float* x, int32_t B
   GS_REQUIRE(layer >= 0 && layer < c->cfg.enc_depth, "encoder_block: layer out of range");
   GS_REQUIRE(B > 0 && B <= 2 * c->max_pairs, "encoder_block: B exceeds context capacity");
   hipStream_t s = (hipStream_t)stream;
+  RC(sync_bf16(*c, s));
   return encoder_block(*c, layer, x, (int64_t)B * c->N, s);
 }
 
@@ -1037,6 +1067,7 @@ int32_t gs_hip_mastr_encoder(void* ctx, const float* img, int32_t B, float* enc,
   Ctx* c = (Ctx*)ctx;
   GS_REQUIRE(B > 0 && B <= 2 * c->max_pairs, "encoder: B exceeds context capacity");
   hipStream_t s = (hipStream_t)stream;
+  RC(sync_bf16(*c, s));
   RC(launch_unfold(img, B, c->cfg.img_h, c->cfg.img_w, c->cfg.patch, c->P, s));
   return encoder_from_patches(*c, B, enc, s);
 }
@@ -1053,6 +1084,7 @@ int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2, int32
   const gs_mastr_config& f = c->cfg;
   const int64_t Mv = (int64_t)B * c->N;
   const int64_t K = 3 * f.patch * f.patch;
+  RC(sync_bf16(*c, s));
   RC(launch_unfold(img1, B, f.img_h, f.img_w, f.patch, c->P, s));
   RC(launch_unfold(img2, B, f.img_h, f.img_w, f.patch, c->P + Mv * K, s));
   RC(encoder_from_patches(*c, 2 * B, c->enc, s));

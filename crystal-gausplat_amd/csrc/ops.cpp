@@ -78,8 +78,10 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   if (ensure_device()) return -2;
   GS_REQUIRE(w_layout == 0 || w_layout == 1, "linear: w_layout must be 0 or 1");
   GS_REQUIRE(M >= 0 && M <= INT32_MAX, "linear: M out of range");
-  GS_REQUIRE((epilogue & ~(GS_EPI_GELU | GS_EPI_RESIDUAL | GS_EPI_RELU)) == 0,
+  GS_REQUIRE((epilogue & ~(GS_EPI_GELU | GS_EPI_RESIDUAL | GS_EPI_RELU | GS_EPI_BF16)) == 0,
              "linear: unknown epilogue flag");
+  const bool bf16 = (epilogue & GS_EPI_BF16) != 0;
+  GS_REQUIRE(!bf16 || w_layout == 0, "linear: the bf16 variant needs w_layout 0");
   GS_REQUIRE(!(epilogue & GS_EPI_RESIDUAL) || residual, "linear: residual flag without residual");
   GemmArgs a = blank_args();
   a.A = x;
@@ -97,10 +99,23 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
             ((epilogue & GS_EPI_RESIDUAL) ? EPI_RES1 : 0);
   a.R1 = residual;
   a.ldr1 = N;
+  hipStream_t s = pick(stream);
+  std::unique_lock<std::mutex> lk(g_ws_mu, std::defer_lock);
+  if (bf16) {
+    lk.lock();
+    void* ws = nullptr;
+    int rc = workspace((size_t)N * K * 2, &ws);
+    if (rc) return rc;
+    rc = launch_f32_to_bf16(w, ws, (int64_t)N * K, s);
+    if (rc) return rc;
+    a.Bh = ws;
+  }
   GemmBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
-  return launch_gemm(bt, A_PLAIN, w_layout == 0 ? B_NT : B_NN, false, pick(stream));
+  int rc = launch_gemm(bt, A_PLAIN, w_layout == 0 ? B_NT : B_NN, false, s, bf16);
+  if (rc == 0 && bf16) GS_CHECK_HIP(hipStreamSynchronize(s));  // workspace reuse
+  return rc;
 }
 
 int32_t gs_hip_layernorm(const float* x, const float* gamma, const float* beta, float* y,

@@ -32,6 +32,7 @@ class MastrConfig(C.Structure):
         ("rope_base", C.c_float),
         ("linear_layout", C.c_int32),
         ("rope_mode", C.c_int32),
+        ("precision", C.c_int32),
     ]
 
     def as_dict(self):
@@ -96,7 +97,7 @@ _SIGS = [
                                          C.POINTER(C.c_double)]),
 ]
 
-EPI_GELU, EPI_RESIDUAL, EPI_RELU = 1, 2, 4
+EPI_GELU, EPI_RESIDUAL, EPI_RELU, EPI_BF16 = 1, 2, 4, 8
 CONV_RELU_IN, CONV_RELU_OUT = 1, 2
 
 _lib = None

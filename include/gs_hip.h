@@ -97,6 +97,7 @@ void gs_seed_uniform(uint64_t seed, const char* name, float lo, float hi,
 #define GS_EPI_GELU 1     /* y = gelu_tanh(x.W + b)                          */
 #define GS_EPI_RESIDUAL 2 /* y = residual + (x.W + b)                        */
 #define GS_EPI_RELU 4     /* y = max(x.W + b, 0)                             */
+#define GS_EPI_BF16 8     /* bf16-input / fp32-accumulate MFMA (w_layout 0)  */
 
 /* NN::GPUOps.linear_forward (src/nn/gpu_ops.cr:39-78) plus the bias add the
  * reference does on the CPU (src/nn/linear.cr:206-230).
@@ -180,6 +181,8 @@ typedef struct gs_mastr_config {
   float rope_base;
   int32_t linear_layout; /* 0 = x W^T; 1 = reference CPU literal layout */
   int32_t rope_mode;     /* 0 none, 1 per-attention q/k 2D, 2 ref-token */
+  int32_t precision;     /* 0 = fp32 MFMA; 1 = bf16-input / fp32-accumulate
+                            MFMA GEMMs and attention (linear_layout 0 only) */
 } gs_mastr_config;
 
 /* MASt3R ViT-L/ViT-B at 384x512 (24x32 patch grid), eps 1e-6, RoPE base 100,

@@ -58,3 +58,20 @@ def assert_close(got, ref, rtol=RTOL, atol=ATOL, name=""):
             f"{name}: {int(bad.sum())}/{bad.size} elements outside rtol={rtol} atol={atol}; "
             f"worst at {i}: got {got[i]!r} ref {ref[i]!r}; max abs err {err.max():.3e}")
     return float(err.max())
+
+
+# bf16-input / fp32-accumulate variant: 2e-2 relative (north star), stated
+# norm-wise over the tensor, with the worst element bounded by 2e-2 of the
+# tensor's largest magnitude.
+BF16_RTOL = 2e-2
+
+
+def assert_close_bf16(got, ref, rtol=BF16_RTOL, name=""):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert got.shape == ref.shape, (name, got.shape, ref.shape)
+    assert np.isfinite(got).all(), f"{name}: non-finite output"
+    rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+    worst = np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30)
+    assert rel <= rtol and worst <= rtol, f"{name}: norm-wise rel err {rel:.3e}, worst/max {worst:.3e}"
+    return rel, worst

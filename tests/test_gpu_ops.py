@@ -8,7 +8,7 @@ import torch
 
 import gsplat_hip as G
 import pyoracle as O
-from gpu_util import assert_close, case, dev, empty, host, stream
+from gpu_util import assert_close, assert_close_bf16, case, dev, empty, host, stream
 
 pytestmark = pytest.mark.gpu
 
@@ -66,6 +66,18 @@ def test_linear_epilogues(epi):
     G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), None if epi == "nobias" else p(dev(b)), p(y),
                               M, K, N, 0, flags, p(y) if epi == "residual" else None, stream()))
     assert_close(host(y), ref, name=epi)
+
+
+@pytest.mark.parametrize("M,K,N", [(768, 1024, 3072), (768, 4096, 1024), (37, 64, 100)])
+def test_linear_bf16_variant(M, K, N):
+    case(f"linear bf16 M={M} K={K} N={N}")
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.02), rnd(N, scale=0.1)
+    y = empty(M, N)
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, 0, G.EPI_BF16, None,
+                              stream()))
+    rel, worst = assert_close_bf16(host(y), O.linear(x, W, b), name="linear bf16")
+    print(f"bf16 linear: rel {rel:.2e} worst {worst:.2e}")
+    assert rel > 1e-5  # it really ran in bf16
 
 
 @pytest.mark.parametrize("M,K,N", [(768, 1024, 1024), (50, 64, 96)])
