@@ -102,6 +102,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16&
             }
           } else {
             p.C[(int64_t)row * p.ldc + col] = v;
+            if (flags & EPI_DUAL) p.C2[(int64_t)row * p.ldc + col] = v;
           }
         }
       }
@@ -425,6 +426,8 @@ int check_gemm(const GemmArgs& a, int aload, int blayout) {
     GS_REQUIRE(a.rope_cos && a.rope_sin && a.rope_ncols % 64 == 0 &&
                    a.rope_ncols <= a.N && a.tok_per_img > 0 && a.grid_w > 0,
                "gemm: bad rope epilogue");
+  if (a.flags & EPI_DUAL)
+    GS_REQUIRE(a.C2 != nullptr && !(a.flags & EPI_SCATTER), "gemm: bad dual store");
   if (a.flags & EPI_SCATTER)
     GS_REQUIRE(a.sc_r > 0 && a.sc_C > 0 && a.N == a.sc_r * a.sc_r * a.sc_C &&
                    a.sc_Cout <= a.sc_C && a.sc_gh > 0 && a.sc_gw > 0 &&

@@ -62,6 +62,7 @@ enum EpiFlags : int {
   EPI_RES2 = 16,     // v = R2 + v (applied after RES1)
   EPI_ROPE = 32,     // RoPE on columns [0, rope_ncols)
   EPI_SCATTER = 64,  // sub-pixel scatter store (ConvT / pixel shuffle)
+  EPI_DUAL = 128,    // also store the result to C2 (same ldc)
 };
 
 struct GemmArgs {
@@ -79,6 +80,7 @@ struct GemmArgs {
   int64_t ldb;
   float* C;
   int64_t ldc;
+  float* C2;        // second destination of EPI_DUAL
   const float* bias;
   const float* R1;
   int64_t ldr1;

@@ -180,6 +180,11 @@ struct Ctx {
   float *rope_cos, *rope_sin, *ref_cos, *ref_sin;
   int ref_maxpos = 0;
   int last_B = 0;
+  // hipGraph replay of the pair launch sequence (gs_hip_mastr_set_graph)
+  bool graph_on = false;
+  hipGraphExec_t gexec = nullptr;
+  const void* gkey[9] = {};
+  int gkey_B = 0;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -350,11 +355,12 @@ int encoder_from_patches(Ctx& c, int64_t nimg, float* out, hipStream_t s) {
   const gs_mastr_config& f = c.cfg;
   const int D = f.enc_dim, K = 3 * f.patch * f.patch;
   const int64_t M = nimg * c.N;
-  RC(linear_mode(c, "patch_embed.proj", c.P, K, c.x, D, M, D, K, 0, s));
-  if (f.rope_mode == 2) {
-    RC(launch_rope_ref_token(c.x, c.h, (int)nimg, c.gh, c.gw, D, f.enc_heads, c.ref_cos,
+  if (f.rope_mode == 2) {  // token-level RoPE between the patch embedding and block 0
+    RC(linear_mode(c, "patch_embed.proj", c.P, K, c.h, D, M, D, K, 0, s));
+    RC(launch_rope_ref_token(c.h, c.x, (int)nimg, c.gh, c.gw, D, f.enc_heads, c.ref_cos,
                              c.ref_sin, c.ref_maxpos, s));
-    GS_CHECK_HIP(hipMemcpyAsync(c.x, c.h, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
+  } else {
+    RC(linear_mode(c, "patch_embed.proj", c.P, K, c.x, D, M, D, K, 0, s));
   }
   for (int l = 0; l < f.enc_depth; ++l) RC(encoder_block(c, l, c.x, M, s));
   RC(layernorm1(c.x, W(c, "enc_norm.weight"), W(c, "enc_norm.bias"), out, M, D, f.ln_eps, s));
@@ -456,18 +462,21 @@ int decoder(Ctx& c, int B, hipStream_t s) {
         a[k] = lin(hc[k], D, W(c, p[k] + ".mlp.fc1.weight"), W(c, p[k] + ".mlp.fc1.bias"), mc[k],
                    f.dec_mlp, Mv, f.dec_mlp, D, EPI_GELU);
       RC(run2(c, a[0], a[1], A_PLAIN, s));
+      // the DPT hooks snapshot the state after blocks hooks[1] and hooks[2]:
+      // the fc2 epilogue stores that block's output a second time
+      float* hook = f.dpt_hooks[1] == l + 1 ? c.hook1 : (f.dpt_hooks[2] == l + 1 ? c.hook2 : nullptr);
+      float* hook2 = (f.dpt_hooks[1] == l + 1 && f.dpt_hooks[2] == l + 1) ? c.hook2 : nullptr;
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(mc[k], f.dec_mlp, W(c, p[k] + ".mlp.fc2.weight"), W(c, p[k] + ".mlp.fc2.bias"),
-                   dc[k], D, Mv, D, f.dec_mlp, EPI_RES1);
+                   dc[k], D, Mv, D, f.dec_mlp, EPI_RES1 | (hook ? EPI_DUAL : 0));
         a[k].R1 = dc[k];
         a[k].ldr1 = D;
+        if (hook) a[k].C2 = hook + (int64_t)k * Mv * D;
       }
       RC(run2(c, a[0], a[1], A_PLAIN, s));
+      if (hook2)  // both hooks on the same block
+        GS_CHECK_HIP(hipMemcpyAsync(hook2, hook, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
     }
-    if (f.dpt_hooks[1] == l + 1)
-      GS_CHECK_HIP(hipMemcpyAsync(c.hook1, c.d, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
-    if (f.dpt_hooks[2] == l + 1)
-      GS_CHECK_HIP(hipMemcpyAsync(c.hook2, c.d, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
   }
   RC(layernorm1(c.d, W(c, "dec_norm.weight"), W(c, "dec_norm.bias"), c.dfin, M, D, eps, s));
   return 0;
@@ -1027,6 +1036,7 @@ void gs_hip_mastr_destroy(void* ctx) {
   if (!ctx) return;
   Ctx* c = (Ctx*)ctx;
   hipDeviceSynchronize();
+  if (c->gexec) hipGraphExecDestroy(c->gexec);
   if (c->warena) hipFree(c->warena);
   if (c->wbf16) hipFree(c->wbf16);
   if (c->arena) hipFree(c->arena);
@@ -1072,19 +1082,16 @@ int32_t gs_hip_mastr_encoder(void* ctx, const float* img, int32_t B, float* enc,
   return encoder_from_patches(*c, B, enc, s);
 }
 
-int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2, int32_t B, float* pts1,
-                          float* conf1, float* desc1, float* pts2, float* conf2, float* desc2,
-                          void* stream) {
-  GS_REQUIRE(ctx && img1 && img2, "pair: null image");
-  Ctx* c = (Ctx*)ctx;
-  GS_REQUIRE(B > 0 && B <= c->max_pairs, "pair: B exceeds context capacity");
-  GS_REQUIRE(c->cfg.linear_layout == 0, "pair: the literal linear layout is encoder-only");
-  GS_REQUIRE(!pts1 == !conf1 && !pts2 == !conf2, "pair: pts and conf must be given together");
-  hipStream_t s = (hipStream_t)stream;
+}  // extern "C"
+
+namespace {
+
+// The pair launch sequence (encoder on both views, decoder, heads).
+int pair_body(Ctx* c, const float* img1, const float* img2, int32_t B, float* pts1, float* conf1,
+              float* desc1, float* pts2, float* conf2, float* desc2, hipStream_t s) {
   const gs_mastr_config& f = c->cfg;
   const int64_t Mv = (int64_t)B * c->N;
   const int64_t K = 3 * f.patch * f.patch;
-  RC(sync_bf16(*c, s));
   RC(launch_unfold(img1, B, f.img_h, f.img_w, f.patch, c->P, s));
   RC(launch_unfold(img2, B, f.img_h, f.img_w, f.patch, c->P + Mv * K, s));
   RC(encoder_from_patches(*c, 2 * B, c->enc, s));
@@ -1122,6 +1129,62 @@ int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2, int32
   }
   if (hd.n) RC(dpt_heads(*c, hd, ge, gh6, gh9, gdf, B, gp, gc, s));
   if (hl.n) RC(local_features(*c, hl, le, ldf, B, ld, s));
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2, int32_t B, float* pts1,
+                          float* conf1, float* desc1, float* pts2, float* conf2, float* desc2,
+                          void* stream) {
+  GS_REQUIRE(ctx && img1 && img2, "pair: null image");
+  Ctx* c = (Ctx*)ctx;
+  GS_REQUIRE(B > 0 && B <= c->max_pairs, "pair: B exceeds context capacity");
+  GS_REQUIRE(c->cfg.linear_layout == 0, "pair: the literal linear layout is encoder-only");
+  GS_REQUIRE(!pts1 == !conf1 && !pts2 == !conf2, "pair: pts and conf must be given together");
+  hipStream_t s = (hipStream_t)stream;
+  RC(sync_bf16(*c, s));
+  if (!c->graph_on || prof_on())
+    return pair_body(c, img1, img2, B, pts1, conf1, desc1, pts2, conf2, desc2, s);
+  GS_REQUIRE(s != nullptr, "pair: graph replay needs a non-null stream");
+  const void* key[9] = {img1, img2, pts1, conf1, desc1, pts2, conf2, desc2, (const void*)s};
+  bool hit = c->gexec != nullptr && c->gkey_B == B;
+  for (int i = 0; hit && i < 9; ++i) hit = key[i] == c->gkey[i];
+  if (!hit) {
+    if (c->gexec) {
+      GS_CHECK_HIP(hipGraphExecDestroy(c->gexec));
+      c->gexec = nullptr;
+    }
+    GS_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    const int rc = pair_body(c, img1, img2, B, pts1, conf1, desc1, pts2, conf2, desc2, s);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(s, &g);
+    if (rc) {
+      if (g) hipGraphDestroy(g);
+      return rc;
+    }
+    GS_CHECK_HIP(e);
+    const hipError_t ei = hipGraphInstantiate(&c->gexec, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    GS_CHECK_HIP(ei);
+    for (int i = 0; i < 9; ++i) c->gkey[i] = key[i];
+    c->gkey_B = B;
+  }
+  c->last_B = B;
+  GS_CHECK_HIP(hipGraphLaunch(c->gexec, s));
+  return 0;
+}
+
+int32_t gs_hip_mastr_set_graph(void* ctx, int32_t enable) {
+  GS_REQUIRE(ctx, "set_graph: null context");
+  Ctx* c = (Ctx*)ctx;
+  c->graph_on = enable != 0;
+  if (!c->graph_on && c->gexec) {
+    GS_CHECK_HIP(hipGraphExecDestroy(c->gexec));
+    c->gexec = nullptr;
+  }
   return 0;
 }
 

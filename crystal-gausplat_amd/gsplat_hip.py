@@ -90,6 +90,7 @@ _SIGS = [
     ("gs_hip_mastr_encoder", C.c_int32, [vp, vp, C.c_int32, vp, vp]),
     ("gs_hip_mastr_pair", C.c_int32, [vp, vp, vp, C.c_int32, vp, vp, vp, vp, vp, vp, vp]),
     ("gs_hip_mastr_pair_taps", C.c_int32, [vp, C.c_int32, vp, vp, vp, vp, vp]),
+    ("gs_hip_mastr_set_graph", C.c_int32, [vp, C.c_int32]),
     ("gs_hip_profile_begin", C.c_int32, [C.c_int32]),
     ("gs_hip_profile_end", C.c_int32, []),
     ("gs_hip_profile_entry", C.c_int32, [C.c_int32, C.c_char_p, C.c_int32, C.POINTER(C.c_int64),
@@ -248,6 +249,9 @@ class Mastr:
              desc2=None, stream=None):
         check(lib().gs_hip_mastr_pair(self.h, ptr(img1), ptr(img2), B, ptr(pts1), ptr(conf1),
                                       ptr(desc1), ptr(pts2), ptr(conf2), ptr(desc2), stream))
+
+    def set_graph(self, enable=True):
+        check(lib().gs_hip_mastr_set_graph(self.h, 1 if enable else 0))
 
     def pair_taps(self, B, enc1=None, enc2=None, dec1=None, dec2=None, stream=None):
         check(lib().gs_hip_mastr_pair_taps(self.h, B, ptr(enc1), ptr(enc2), ptr(dec1), ptr(dec2),

@@ -232,6 +232,12 @@ int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2,
                           int32_t B, float* pts1, float* conf1, float* desc1,
                           float* pts2, float* conf2, float* desc2,
                           void* stream);
+/* enable != 0: gs_hip_mastr_pair captures its launch sequence into a hipGraph
+ * on the first call with a given (B, image / output pointers, stream) and
+ * replays it while those repeat (re-capturing when they change). Needs a
+ * non-null stream; calls made while gs_hip_profile_* is active run eagerly.
+ * The weights may change between replays (the graph reads them in place). */
+int32_t gs_hip_mastr_set_graph(void* ctx, int32_t enable);
 /* Intermediate taps of the last gs_hip_mastr_pair call, copied to device
  * buffers: enc1/enc2 [B,N,enc_dim], dec1/dec2 = dec_norm output
  * [B,N,dec_dim]. Any pointer may be NULL. */

@@ -228,6 +228,45 @@ def test_config4_bf16_vs_fp32():
         print(f"config4 bf16 {k}: rel {rel:.2e} worst {worst:.2e}")
 
 
+def test_graph_replay_matches_eager(tiny_cfg):
+    """hipGraph replay of the pair sequence: several replays, with eager work,
+    synchronisation and in-place input changes between them; every replay is
+    bit-identical to the eager run on the same inputs."""
+    case("graph replay")
+    cfg = G.default_config(**tiny_cfg)
+    B = 2
+    n = B * 3 * cfg.img_h * cfg.img_w
+    shape = (B, 3, cfg.img_h, cfg.img_w)
+    imgs = [(G.seed_uniform(s, "view1", n).reshape(shape), G.seed_uniform(s, "view2", n).reshape(shape))
+            for s in range(3)]
+    m = G.Mastr(cfg, B)
+    m.init_seeded(0, 0.02, 0.1)
+    st = torch.cuda.Stream()
+    H, W = cfg.img_h, cfg.img_w
+    with torch.cuda.stream(st):
+        i1, i2 = dev(imgs[0][0]), dev(imgs[0][1])
+        outs = [empty(B, H, W, c) for c in (3, 1, cfg.desc_dim, 3, 1, cfg.desc_dim)]
+        eager = []
+        for a, b in imgs:
+            i1.copy_(torch.from_numpy(a).to("cuda", non_blocking=False))
+            i2.copy_(torch.from_numpy(b).to("cuda", non_blocking=False))
+            m.pair(i1, i2, B, *outs, stream=st.cuda_stream)
+            eager.append([host(o).copy() for o in outs])
+        m.set_graph(True)
+        for rep in range(2):
+            for j, (a, b) in enumerate(imgs):
+                i1.copy_(torch.from_numpy(a).to("cuda"))
+                i2.copy_(torch.from_numpy(b).to("cuda"))
+                junk = torch.randn(1 << 20, device="cuda") * 2  # eager work between replays
+                m.pair(i1, i2, B, *outs, stream=st.cuda_stream)
+                torch.cuda.synchronize()
+                del junk
+                for o, e in zip(outs, eager[j]):
+                    np.testing.assert_array_equal(host(o), e, err_msg=f"replay {rep} input {j}")
+        m.set_graph(False)
+    m.close()
+
+
 def test_view_swap_symmetry_full_size():
     """With the second decoder chain and head sharing the first's weights,
     swapping the views swaps the outputs (bit for bit) at the config-2 size."""
