@@ -6,6 +6,8 @@
 
 #include <string>
 
+struct gs_mastr_config;
+
 namespace gs {
 
 // Native 4-wide float vector for kernels (HIP's float4 struct is copied via
@@ -176,5 +178,22 @@ void rope_table_host(int32_t max_pos, float base, float* cos_t, float* sin_t);
 // pos * 1/base^(2i/hd) (src/mastr/encoder_v2.cr:165-176).
 void rope_ref_table_host(int32_t max_pos, int32_t hd, float base, float* cos_t,
                          float* sin_t);
+
+// Caller-side passes (pointcloud.hip). image_prep: F frames [sh,sw,C] ->
+// [F,th,tw,C] (resize only) or [F,3,th,tw] (normalize, with or without
+// resize). collect_points: appends the points with conf > thr at *counter
+// (device int64, advanced by the selected count; positions >= cap are not
+// written); scratch holds collect_points_scratch(n) int64.
+int launch_image_prep(const float* src, int32_t F, int32_t sh, int32_t sw, int32_t C,
+                      int32_t th, int32_t tw, bool resize, bool normalize, bool nchw,
+                      float* dst, hipStream_t s);
+int64_t collect_points_scratch(int64_t n);
+int launch_collect_points(const float* pts, const float* conf, int64_t n, float thr,
+                          float* out_pts, float* out_conf, int64_t cap, int64_t* counter,
+                          int64_t* scratch, hipStream_t s);
+int launch_fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t s);
+
+// Configuration of a MASt3R context created by gs_hip_mastr_create.
+const ::gs_mastr_config* mastr_ctx_config(void* ctx);
 
 }  // namespace gs

@@ -185,6 +185,10 @@ struct Ctx {
   hipGraphExec_t gexec = nullptr;
   const void* gkey[9] = {};
   int gkey_B = 0;
+  // frames_to_pointcloud buffers (prepared frames, per-chunk point maps,
+  // compaction counter and scratch), grown on demand
+  char* pcbuf = nullptr;
+  size_t pcbuf_size = 0;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -1040,6 +1044,7 @@ void gs_hip_mastr_destroy(void* ctx) {
   if (c->warena) hipFree(c->warena);
   if (c->wbf16) hipFree(c->wbf16);
   if (c->arena) hipFree(c->arena);
+  if (c->pcbuf) hipFree(c->pcbuf);
   delete c;
 }
 
@@ -1083,6 +1088,8 @@ int32_t gs_hip_mastr_encoder(void* ctx, const float* img, int32_t B, float* enc,
 }
 
 }  // extern "C"
+
+const gs_mastr_config* gs::mastr_ctx_config(void* ctx) { return &((Ctx*)ctx)->cfg; }
 
 namespace {
 
@@ -1202,6 +1209,74 @@ int32_t gs_hip_mastr_pair_taps(void* ctx, int32_t B, float* enc1, float* enc2, f
   if (dec1) GS_CHECK_HIP(hipMemcpyAsync(dec1, c->dfin, nd * 4, hipMemcpyDeviceToDevice, s));
   if (dec2)
     GS_CHECK_HIP(hipMemcpyAsync(dec2, c->dfin + Mv * c->cfg.dec_dim, nd * 4, hipMemcpyDeviceToDevice, s));
+  return 0;
+}
+
+int32_t gs_hip_mastr_frames_to_pointcloud(void* ctx, const float* frames, int32_t F,
+                                          int32_t src_h, int32_t src_w, float threshold,
+                                          float* out_pts, float* out_conf, int64_t capacity,
+                                          int64_t* n_points, void* stream) {
+  GS_REQUIRE(ctx && n_points, "frames_to_pointcloud: null argument");
+  Ctx* c = (Ctx*)ctx;
+  *n_points = 0;
+  if (F < 2) return 0;
+  GS_REQUIRE(frames, "frames_to_pointcloud: null frames");
+  GS_REQUIRE(c->cfg.linear_layout == 0, "frames_to_pointcloud: needs linear_layout 0");
+  GS_REQUIRE(capacity >= 0 && (capacity == 0 || (out_pts && out_conf)),
+             "frames_to_pointcloud: bad output buffers");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t H = c->cfg.img_h, W = c->cfg.img_w, HW = H * W;
+  const int32_t P = F - 1;
+  const int32_t Bmax = std::min(c->max_pairs, P);
+  // carve the buffer
+  const size_t sz_prep = align256((size_t)F * 3 * HW * 4), sz_pts = align256((size_t)Bmax * HW * 12),
+               sz_conf = align256((size_t)Bmax * HW * 4), sz_cnt = 256,
+               sz_scr = align256((size_t)collect_points_scratch(Bmax * HW) * 8);
+  const size_t need = sz_prep + 2 * sz_pts + 2 * sz_conf + sz_cnt + sz_scr;
+  if (need > c->pcbuf_size) {
+    if (c->pcbuf) {
+      GS_CHECK_HIP(hipDeviceSynchronize());
+      GS_CHECK_HIP(hipFree(c->pcbuf));
+      c->pcbuf = nullptr;
+      c->pcbuf_size = 0;
+    }
+    GS_CHECK_HIP(hipMalloc(&c->pcbuf, need));
+    c->pcbuf_size = need;
+  }
+  char* cur = c->pcbuf;
+  float* prep = (float*)cur;
+  cur += sz_prep;
+  float* pts1 = (float*)cur;
+  cur += sz_pts;
+  float* pts2 = (float*)cur;
+  cur += sz_pts;
+  float* conf1 = (float*)cur;
+  cur += sz_conf;
+  float* conf2 = (float*)cur;
+  cur += sz_conf;
+  int64_t* counter = (int64_t*)cur;
+  cur += sz_cnt;
+  int64_t* scratch = (int64_t*)cur;
+
+  RC(launch_fill_i64(counter, 1, 0, s));
+  RC(launch_image_prep(frames, F, src_h, src_w, 3, (int32_t)H, (int32_t)W, true, true, true, prep,
+                       s));
+  RC(sync_bf16(*c, s));
+  for (int32_t p0 = 0; p0 < P; p0 += Bmax) {
+    const int32_t Bc = std::min(Bmax, P - p0);
+    const bool last = p0 + Bc == P;
+    RC(pair_body(c, prep + (int64_t)p0 * 3 * HW, prep + (int64_t)(p0 + 1) * 3 * HW, Bc, pts1,
+                 conf1, nullptr, last ? pts2 : nullptr, last ? conf2 : nullptr, nullptr, s));
+    RC(launch_collect_points(pts1, conf1, (int64_t)Bc * HW, threshold, out_pts, out_conf,
+                             capacity, counter, scratch, s));
+    if (last)
+      RC(launch_collect_points(pts2 + (int64_t)(Bc - 1) * HW * 3, conf2 + (int64_t)(Bc - 1) * HW,
+                               HW, threshold, out_pts, out_conf, capacity, counter, scratch, s));
+  }
+  int64_t n = 0;
+  GS_CHECK_HIP(hipMemcpyAsync(&n, counter, sizeof(n), hipMemcpyDeviceToHost, s));
+  GS_CHECK_HIP(hipStreamSynchronize(s));
+  *n_points = n;
   return 0;
 }
 

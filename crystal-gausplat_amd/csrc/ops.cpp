@@ -62,6 +62,11 @@ int rope_tables(float base, const float** c, const float** s) {
   return 0;
 }
 
+// Block-count scratch of gs_hip_collect_points (grown on demand).
+std::mutex g_cp_mu;
+int64_t* g_cp = nullptr;
+int64_t g_cp_n = 0;
+
 GemmArgs blank_args() {
   GemmArgs a;
   memset(&a, 0, sizeof(a));
@@ -253,6 +258,45 @@ int32_t gs_hip_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32
                           void* stream) {
   if (ensure_device()) return -2;
   return launch_upsample2x(x, B, H, W, C, y, pick(stream));
+}
+
+int32_t gs_hip_resize_image(const float* src, int32_t F, int32_t sh, int32_t sw, int32_t C,
+                            int32_t th, int32_t tw, float* dst, void* stream) {
+  if (ensure_device()) return -2;
+  return launch_image_prep(src, F, sh, sw, C, th, tw, true, false, false, dst, pick(stream));
+}
+
+int32_t gs_hip_preprocess_image(const float* src, int32_t B, int32_t H, int32_t W, float* dst,
+                                void* stream) {
+  if (ensure_device()) return -2;
+  return launch_image_prep(src, B, H, W, 3, H, W, false, true, true, dst, pick(stream));
+}
+
+int32_t gs_hip_prepare_frames(const float* src, int32_t F, int32_t sh, int32_t sw, int32_t th,
+                              int32_t tw, float* dst, void* stream) {
+  if (ensure_device()) return -2;
+  return launch_image_prep(src, F, sh, sw, 3, th, tw, true, true, true, dst, pick(stream));
+}
+
+int32_t gs_hip_collect_points(const float* pts, const float* conf, int64_t n, float threshold,
+                              float* out_pts, float* out_conf, int64_t capacity, int64_t* count,
+                              void* stream) {
+  if (ensure_device()) return -2;
+  GS_REQUIRE(n >= 0, "collect_points: n < 0");
+  std::lock_guard<std::mutex> lk(g_cp_mu);
+  const int64_t need = collect_points_scratch(n);
+  if (need > g_cp_n) {
+    if (g_cp) {
+      GS_CHECK_HIP(hipDeviceSynchronize());
+      GS_CHECK_HIP(hipFree(g_cp));
+      g_cp = nullptr;
+      g_cp_n = 0;
+    }
+    GS_CHECK_HIP(hipMalloc(&g_cp, need * sizeof(int64_t)));
+    g_cp_n = need;
+  }
+  return launch_collect_points(pts, conf, n, threshold, out_pts, out_conf, capacity, count, g_cp,
+                               pick(stream));
 }
 
 }  // extern "C"

@@ -76,6 +76,13 @@ _SIGS = [
     ("gs_hip_conv_transpose", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp,
                                           vp, C.c_int32, C.c_int32, vp]),
     ("gs_hip_upsample2x", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp]),
+    ("gs_hip_resize_image", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                        C.c_int32, vp, vp]),
+    ("gs_hip_preprocess_image", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, vp, vp]),
+    ("gs_hip_prepare_frames", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                          C.c_int32, vp, vp]),
+    ("gs_hip_collect_points", C.c_int32, [vp, vp, C.c_int64, C.c_float, vp, vp, C.c_int64, vp,
+                                          vp]),
     ("gs_mastr_default_config", None, [C.POINTER(MastrConfig)]),
     ("gs_mastr_weight_count", C.c_int32, [C.POINTER(MastrConfig)]),
     ("gs_mastr_weight_info", C.c_int32, [C.POINTER(MastrConfig), C.c_int32, C.c_char_p, C.c_int32,
@@ -91,6 +98,15 @@ _SIGS = [
     ("gs_hip_mastr_pair", C.c_int32, [vp, vp, vp, C.c_int32, vp, vp, vp, vp, vp, vp, vp]),
     ("gs_hip_mastr_pair_taps", C.c_int32, [vp, C.c_int32, vp, vp, vp, vp, vp]),
     ("gs_hip_mastr_set_graph", C.c_int32, [vp, C.c_int32]),
+    ("gs_hip_mastr_frames_to_pointcloud", C.c_int32, [vp, vp, C.c_int32, C.c_int32, C.c_int32,
+                                                      C.c_float, vp, vp, C.c_int64,
+                                                      C.POINTER(C.c_int64), vp]),
+    ("gs_safetensors_count", C.c_int32, [C.c_char_p]),
+    ("gs_safetensors_info", C.c_int32, [C.c_char_p, C.c_int32, C.c_char_p, C.c_int32, C.c_char_p,
+                                        C.POINTER(C.c_int64), C.POINTER(C.c_int32)]),
+    ("gs_safetensors_read_f32", C.c_int32, [C.c_char_p, C.c_char_p, vp, C.c_int64]),
+    ("gs_hip_mastr_load_safetensors", C.c_int32, [vp, C.c_char_p, C.POINTER(C.c_int32),
+                                                  C.POINTER(C.c_int32), C.POINTER(C.c_int32)]),
     ("gs_hip_profile_begin", C.c_int32, [C.c_int32]),
     ("gs_hip_profile_end", C.c_int32, []),
     ("gs_hip_profile_entry", C.c_int32, [C.c_int32, C.c_char_p, C.c_int32, C.POINTER(C.c_int64),
@@ -200,6 +216,31 @@ def seed_uniform(seed, name, n, lo=-1.0, hi=1.0):
     return a
 
 
+def safetensors_index(path):
+    """[(name, dtype, shape tuple)] of a safetensors file, in header order."""
+    L = lib()
+    p = os.fsencode(path)
+    n = L.gs_safetensors_count(p)
+    if n < 0:
+        check(n)
+    name, dt = C.create_string_buffer(512), C.create_string_buffer(8)
+    shp, nd = (C.c_int64 * 8)(), C.c_int32()
+    out = []
+    for i in range(n):
+        check(L.gs_safetensors_info(p, i, name, 512, dt, shp, C.byref(nd)))
+        out.append((name.value.decode(), dt.value.decode(), tuple(shp[:nd.value])))
+    return out
+
+
+def safetensors_read(path, name, shape):
+    """Tensor `name` of a safetensors file as float32 numpy (F32/F16/BF16)."""
+    import numpy as np
+    a = np.empty(shape, dtype=np.float32)
+    check(lib().gs_safetensors_read_f32(os.fsencode(path), name.encode(),
+                                        a.ctypes.data_as(C.c_void_p), a.size))
+    return a
+
+
 def profile_begin(per_shape=False):
     check(lib().gs_hip_profile_begin(1 if per_shape else 0))
 
@@ -238,6 +279,25 @@ class Mastr:
         a = np.ascontiguousarray(arr, dtype=np.float32)
         check(lib().gs_hip_mastr_set_weight(self.h, name.encode(), a.ctypes.data_as(C.c_void_p),
                                             a.size))
+
+    def load_safetensors(self, path):
+        """Place every inventory weight found in a checkpoint file; returns
+        dict(loaded, unexpected, missing) counts."""
+        a, b, c = C.c_int32(), C.c_int32(), C.c_int32()
+        check(lib().gs_hip_mastr_load_safetensors(self.h, os.fsencode(path), C.byref(a),
+                                                  C.byref(b), C.byref(c)))
+        return dict(loaded=a.value, unexpected=b.value, missing=c.value)
+
+    def frames_to_pointcloud(self, frames, threshold, out_pts, out_conf, stream=None):
+        """frames: device tensor [F, h, w, 3]; out_pts [cap, 3], out_conf [cap]
+        device tensors. Returns the total point count (may exceed cap)."""
+        F, h, w, c = frames.shape
+        assert c == 3 and out_pts.shape[0] == out_conf.shape[0]
+        n = C.c_int64()
+        check(lib().gs_hip_mastr_frames_to_pointcloud(self.h, ptr(frames), F, h, w, threshold,
+                                                      ptr(out_pts), ptr(out_conf),
+                                                      out_pts.shape[0], C.byref(n), stream))
+        return n.value
 
     def encoder_block(self, layer, x, B, stream=None):
         check(lib().gs_hip_mastr_encoder_block(self.h, layer, ptr(x), B, stream))

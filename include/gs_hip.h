@@ -163,6 +163,38 @@ int32_t gs_hip_conv_transpose(const float* x, int32_t B, int32_t H, int32_t W,
 int32_t gs_hip_upsample2x(const float* x, int32_t B, int32_t H, int32_t W,
                           int32_t C, float* y, void* stream);
 
+/* Caller-side passes of MASt3RInference, on the device (fp32, HBM-bound). */
+/* resize_image (src/mastr/inference.cr:330-374) on F frames:
+ * src [F, sh, sw, C] -> dst [F, th, tw, C]; bilinear with source coordinate
+ * (t * (s-1)) / (t_n-1) in fp32, truncated and clamped to [0, s-2], and the
+ * reference's four-term sum. sh, sw, th, tw >= 2. Bit-exact to the reference
+ * arithmetic. */
+int32_t gs_hip_resize_image(const float* src, int32_t F, int32_t sh,
+                            int32_t sw, int32_t C, int32_t th, int32_t tw,
+                            float* dst, void* stream);
+/* preprocess_image (src/mastr/inference.cr:193-229): [B,H,W,3] in [0,1] ->
+ * [B,3,H,W], (v - mean[c]) / std[c], ImageNet mean / std. */
+int32_t gs_hip_preprocess_image(const float* src, int32_t B, int32_t H,
+                                int32_t W, float* dst, void* stream);
+/* resize_image then preprocess_image in one pass (the per-frame work of
+ * frames_to_pointcloud, src/mastr/inference.cr:152-153 + 95-96):
+ * [F, sh, sw, 3] -> [F, 3, th, tw]. Bit-identical to the two calls. */
+int32_t gs_hip_prepare_frames(const float* src, int32_t F, int32_t sh,
+                              int32_t sw, int32_t th, int32_t tw, float* dst,
+                              void* stream);
+/* collect_points (src/mastr/inference.cr:296-328) as an order-preserving
+ * compaction: the points of pts [n,3] whose conf [n] is > threshold (strict;
+ * NaN never selected) are appended, in element order, at out_pts[*count],
+ * out_conf[*count]; *count (DEVICE int64, caller-zeroed before the first
+ * call) advances by the selected number, also past capacity (positions >=
+ * capacity are not written), so the caller can detect overflow. Uses a
+ * library-owned scratch buffer: concurrent calls on different streams must
+ * not overlap. */
+int32_t gs_hip_collect_points(const float* pts, const float* conf, int64_t n,
+                              float threshold, float* out_pts,
+                              float* out_conf, int64_t capacity,
+                              int64_t* count, void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* 3. Graph-level entry points (MASt3R)                                      */
 /* ------------------------------------------------------------------------ */
@@ -243,6 +275,48 @@ int32_t gs_hip_mastr_set_graph(void* ctx, int32_t enable);
  * [B,N,dec_dim]. Any pointer may be NULL. */
 int32_t gs_hip_mastr_pair_taps(void* ctx, int32_t B, float* enc1, float* enc2,
                                float* dec1, float* dec2, void* stream);
+
+/* MASt3RInference#frames_to_pointcloud (src/mastr/inference.cr:135-191):
+ * F frames [F, src_h, src_w, 3] in [0,1] (device) are resized to the
+ * context's image size and normalised once each; the F-1 consecutive pairs
+ * run as batched pair calls of up to max_pairs pairs (no descriptor heads);
+ * the view-1 points of every pair, then the view-2 points of the last pair,
+ * with conf > threshold are compacted in order into out_pts [capacity, 3],
+ * out_conf [capacity] (device). *n_points (host) receives the total count,
+ * which may exceed capacity (then only the first capacity are written).
+ * F < 2 gives 0 points. Synchronises the stream before returning; runs
+ * eagerly even when graph replay is enabled. */
+int32_t gs_hip_mastr_frames_to_pointcloud(void* ctx, const float* frames,
+                                          int32_t F, int32_t src_h,
+                                          int32_t src_w, float threshold,
+                                          float* out_pts, float* out_conf,
+                                          int64_t capacity, int64_t* n_points,
+                                          void* stream);
+
+/* Checkpoint ingestion. SafetensorsLoader (src/mastr/weights.cr:30-290):
+ * u64-LE header length + JSON header {name: {dtype, shape, data_offsets}}
+ * ("__metadata__" skipped) + raw data, mmapped; F32 / F16 / BF16 tensors read
+ * as fp32 (F16 exactly, subnormals included; BF16 by a 16-bit shift). The
+ * host-only calls need no GPU. A malformed file (offsets outside the data,
+ * size not matching shape x dtype, bad JSON) is an error, not a partial read. */
+int32_t gs_safetensors_count(const char* path);
+/* Tensor i in header order: name (NUL-terminated, truncated to name_cap),
+ * dtype string (up to 7 chars + NUL into dtype_out[8]), shape (up to 8 dims,
+ * unused 0), ndim. */
+int32_t gs_safetensors_info(const char* path, int32_t i, char* name_out,
+                            int32_t name_cap, char* dtype_out,
+                            int64_t shape_out[8], int32_t* ndim_out);
+/* Tensor `name` converted to fp32 into host memory (numel must match). */
+int32_t gs_safetensors_read_f32(const char* path, const char* name,
+                                float* host_out, int64_t numel);
+/* WeightLoader#load_* (src/mastr/weight_loader.cr:43-123): every tensor of the
+ * file whose name is in the context's inventory is placed (its shape must
+ * equal the inventory shape, else error); n_unexpected counts file tensors not in the inventory,
+ * n_missing inventory weights absent from the file (left as they were). The
+ * fused attn.qkv tensors are placed fused. Any count pointer may be NULL. */
+int32_t gs_hip_mastr_load_safetensors(void* ctx, const char* path,
+                                      int32_t* n_loaded, int32_t* n_unexpected,
+                                      int32_t* n_missing);
 
 /* ------------------------------------------------------------------------ */
 /* 4. Measurement (no reference counterpart: the reference only wall-clocks  */

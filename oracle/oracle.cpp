@@ -51,6 +51,17 @@
  *                       Pinned: exact on constant and affine fields, corners
  *                       preserved, torch interpolate(align_corners=True).
  *   orc_pixel_shuffle   no reference kernel. Pinned: torch pixel_shuffle.
+ *   orc_resize_image    src/mastr/inference.cr:330-374 (fp32 source
+ *                       coordinate, truncation, clamp to s-2, four-term sum in
+ *                       that order). Pinned: identity at equal size, corners
+ *                       preserved, exact on an affine ramp with exact grid
+ *                       steps, torch interpolate(bilinear, align_corners=True).
+ *   orc_preprocess_image src/mastr/inference.cr:193-229. Pinned: numpy
+ *                       float32 (v - mean) / std per channel and a transpose
+ *                       check on a coded pattern.
+ *   orc_collect_points  src/mastr/inference.cr:296-328. Pinned: numpy boolean
+ *                       mask compaction (C order), empty / all-selected / NaN
+ *                       confidence cases.
  *   composites          src/mastr/encoder_v2.cr:38-48 (pre-norm block),
  *                       135-154 (encoder), src/mastr/decoder_v2.cr:47-63
  *                       (decoder block), 170-191 (pair decoder),
@@ -959,4 +970,61 @@ extern "C" int32_t orc_mastr_pair_taps(const orc_config* cfg, orc_weight_fn wf,
   pair(c, img1, img2, B, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, enc1,
        enc2, dec1, dec2);
   return 0;
+}
+
+// ---- caller-side image and point-cloud passes ----------------------------
+
+extern "C" void orc_resize_image(const float* src, int32_t sh, int32_t sw, int32_t C, int32_t th,
+                                 int32_t tw, float* dst) {
+  for (int32_t ty = 0; ty < th; ++ty) {
+    for (int32_t tx = 0; tx < tw; ++tx) {
+      // fp32 products and quotients, as the reference evaluates them
+      const float sy = (float)ty * (float)(sh - 1) / (float)(th - 1);
+      const float sx = (float)tx * (float)(sw - 1) / (float)(tw - 1);
+      const int32_t y0 = std::min(std::max((int32_t)sy, 0), sh - 2);
+      const int32_t x0 = std::min(std::max((int32_t)sx, 0), sw - 2);
+      const int32_t y1 = y0 + 1, x1 = x0 + 1;
+      const float fy = sy - (float)y0;
+      const float fx = sx - (float)x0;
+      for (int32_t c = 0; c < C; ++c) {
+        const float v00 = src[((int64_t)y0 * sw + x0) * C + c];
+        const float v01 = src[((int64_t)y0 * sw + x1) * C + c];
+        const float v10 = src[((int64_t)y1 * sw + x0) * C + c];
+        const float v11 = src[((int64_t)y1 * sw + x1) * C + c];
+        const float v = v00 * (1 - fx) * (1 - fy) + v01 * fx * (1 - fy) + v10 * (1 - fx) * fy +
+                        v11 * fx * fy;
+        dst[((int64_t)ty * tw + tx) * C + c] = v;
+      }
+    }
+  }
+}
+
+extern "C" void orc_preprocess_image(const float* src, int32_t B, int32_t H, int32_t W,
+                                     float* dst) {
+  const float mean[3] = {0.485f, 0.456f, 0.406f};
+  const float stdv[3] = {0.229f, 0.224f, 0.225f};
+  for (int32_t b = 0; b < B; ++b)
+    for (int32_t y = 0; y < H; ++y)
+      for (int32_t x = 0; x < W; ++x)
+        for (int32_t c = 0; c < 3; ++c) {
+          const int64_t si = (((int64_t)b * H + y) * W + x) * 3 + c;
+          const int64_t di = (((int64_t)b * 3 + c) * H + y) * W + x;
+          dst[di] = (src[si] - mean[c]) / stdv[c];
+        }
+}
+
+extern "C" int64_t orc_collect_points(const float* pts, const float* conf, int64_t n,
+                                      float threshold, float* out_pts, float* out_conf) {
+  int64_t k = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const float c = conf[i];
+    if (c > threshold) {
+      out_pts[3 * k] = pts[3 * i];
+      out_pts[3 * k + 1] = pts[3 * i + 1];
+      out_pts[3 * k + 2] = pts[3 * i + 2];
+      out_conf[k] = c;
+      ++k;
+    }
+  }
+  return k;
 }

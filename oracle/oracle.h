@@ -93,6 +93,22 @@ void orc_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C,
 void orc_pixel_shuffle(const float* f, int32_t B, int32_t h, int32_t w,
                        int32_t Cf, int32_t r, int32_t C, float* desc);
 
+/* ---- caller-side image and point-cloud passes --------------------------- */
+/* resize_image (src/mastr/inference.cr:330-374): bilinear, align-corners
+ * mapping sy = ty*(sh-1)/(th-1) in fp32, x0/y0 clamped to [0, s-2].
+ * src [sh, sw, C] -> dst [th, tw, C]; needs sh, sw, th, tw >= 2. */
+void orc_resize_image(const float* src, int32_t sh, int32_t sw, int32_t C,
+                      int32_t th, int32_t tw, float* dst);
+/* preprocess_image (src/mastr/inference.cr:193-229): [B,H,W,3] in [0,1] ->
+ * [B,3,H,W], (v - mean[c]) / std[c] with the ImageNet mean / std. */
+void orc_preprocess_image(const float* src, int32_t B, int32_t H, int32_t W,
+                          float* dst);
+/* collect_points (src/mastr/inference.cr:296-328): the points whose
+ * confidence is > threshold, in element order. pts [n,3], conf [n] ->
+ * out_pts [k,3], out_conf [k]; returns k. */
+int64_t orc_collect_points(const float* pts, const float* conf, int64_t n,
+                           float threshold, float* out_pts, float* out_conf);
+
 /* ---- composites --------------------------------------------------------- */
 typedef struct orc_config {
   int32_t img_h, img_w, patch;

@@ -65,6 +65,9 @@ _SIGS = [
     ("orc_upsample2x", None, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]),
     ("orc_pixel_shuffle", None, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                  C.c_int32, vp]),
+    ("orc_resize_image", None, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]),
+    ("orc_preprocess_image", None, [vp, C.c_int32, C.c_int32, C.c_int32, vp]),
+    ("orc_collect_points", C.c_int64, [vp, vp, C.c_int64, C.c_float, vp, vp]),
     ("orc_encoder_block", C.c_int32, [C.POINTER(OrcConfig), C.c_char_p, WEIGHT_FN, vp, vp,
                                       C.c_int32, C.c_int32, C.c_int32]),
     ("orc_encoder", C.c_int32, [C.POINTER(OrcConfig), WEIGHT_FN, vp, vp, C.c_int32, vp]),
@@ -224,6 +227,57 @@ def pixel_shuffle(f, h, w, r, Cout):
     out = np.empty((B, h * r, w * r, Cout), np.float32)
     lib().orc_pixel_shuffle(_p(f), B, h, w, Cf, r, Cout, _p(out))
     return out
+
+
+def resize_image(img, th, tw):
+    """[sh, sw, C] -> [th, tw, C] (src/mastr/inference.cr:330-374)."""
+    img = f32(img)
+    sh, sw, Cc = img.shape
+    out = np.empty((th, tw, Cc), np.float32)
+    lib().orc_resize_image(_p(img), sh, sw, Cc, th, tw, _p(out))
+    return out
+
+
+def preprocess_image(img):
+    """[B, H, W, 3] -> [B, 3, H, W] (src/mastr/inference.cr:193-229)."""
+    img = f32(img)
+    B, H, W, _ = img.shape
+    out = np.empty((B, 3, H, W), np.float32)
+    lib().orc_preprocess_image(_p(img), B, H, W, _p(out))
+    return out
+
+
+def collect_points(pts, conf, threshold):
+    """pts [..., 3], conf [...] -> (points [k, 3], confs [k])."""
+    pts = f32(pts).reshape(-1, 3)
+    conf = f32(conf).reshape(-1)
+    assert pts.shape[0] == conf.shape[0]
+    op = np.empty_like(pts)
+    oc = np.empty_like(conf)
+    k = lib().orc_collect_points(_p(pts), _p(conf), conf.shape[0], threshold, _p(op), _p(oc))
+    return op[:k].copy(), oc[:k].copy()
+
+
+def frames_to_pointcloud(cfgd, weights, frames, threshold):
+    """frames_to_pointcloud (src/mastr/inference.cr:135-191) composed from the
+    oracle's passes: each frame resized to the model size, consecutive pairs
+    through the pair path, view-1 points of every pair and view-2 points of
+    the last pair collected in that order. frames: list of [h, w, 3]."""
+    if len(frames) < 2:
+        return np.zeros((0, 3), np.float32), np.zeros((0,), np.float32)
+    H, W = cfgd["img_h"], cfgd["img_w"]
+    prep = [preprocess_image(resize_image(f, H, W)[None]) for f in frames]
+    pts, confs = [], []
+    for i in range(len(frames) - 1):
+        o = mastr_pair(cfgd, weights, prep[i], prep[i + 1], desc=False)
+        p, c = collect_points(o["pts1"], o["conf1"], threshold)
+        pts.append(p)
+        confs.append(c)
+        if i == len(frames) - 2:
+            p, c = collect_points(o["pts2"], o["conf2"], threshold)
+            pts.append(p)
+            confs.append(c)
+    return np.concatenate(pts), np.concatenate(confs)
 
 
 def config_from(d):

@@ -361,3 +361,66 @@ def test_oracle_thread_count_does_not_change_bits(tiny_cfg, tiny_weights):
     b = O.mastr_pair(tiny_cfg, tiny_weights, i1, i1[:, :, ::-1].copy())
     for k in a:
         np.testing.assert_array_equal(a[k], b[k])
+
+
+# ---- caller-side passes (src/mastr/inference.cr:193-374) -------------------
+
+def test_resize_identity_corners_and_affine_ramp():
+    rng = np.random.default_rng(3)
+    img = rng.random((7, 11, 3), dtype=np.float32)
+    assert np.array_equal(O.resize_image(img, 7, 11), img)  # equal size: identity
+    up = O.resize_image(img, 20, 31)
+    for (ty, tx), (sy, sx) in {(0, 0): (0, 0), (0, 30): (0, 10), (19, 0): (6, 0),
+                               (19, 30): (6, 10)}.items():
+        assert np.array_equal(up[ty, tx], img[sy, sx])
+    # affine ramp f = 3y + 2x + c on a grid whose steps are exact halves:
+    # bilinear reproduces it exactly; a transposed axis or scale would not
+    yy, xx = np.meshgrid(np.arange(5), np.arange(9), indexing="ij")
+    ramp = np.stack([3 * yy + 2 * xx, yy - xx, 0 * yy + 1], -1).astype(np.float32)
+    out = O.resize_image(ramp, 9, 17)
+    ty, tx = np.meshgrid(np.arange(9) / 2, np.arange(17) / 2, indexing="ij")
+    want = np.stack([3 * ty + 2 * tx, ty - tx, 0 * ty + 1], -1).astype(np.float32)
+    assert np.array_equal(out, want)
+
+
+@pytest.mark.parametrize("sh,sw,th,tw", [(37, 53, 64, 96), (120, 90, 48, 64), (2, 2, 5, 3)])
+def test_resize_matches_torch_align_corners(sh, sw, th, tw):
+    rng = np.random.default_rng(sh)
+    img = rng.random((sh, sw, 3), dtype=np.float32)
+    got = O.resize_image(img, th, tw)
+    ref = F.interpolate(torch.from_numpy(img).permute(2, 0, 1)[None], size=(th, tw),
+                        mode="bilinear", align_corners=True)[0].permute(1, 2, 0).numpy()
+    # torch forms the source coordinate as ty * ((sh-1)/(th-1)), the reference
+    # as (ty*(sh-1))/(th-1): the fp32 coordinates differ by an ulp or so
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-5)
+
+
+def test_preprocess_numpy_and_layout():
+    rng = np.random.default_rng(4)
+    img = rng.random((2, 5, 7, 3), dtype=np.float32)
+    got = O.preprocess_image(img)
+    mean = np.array([0.485, 0.456, 0.406], np.float32)
+    std = np.array([0.229, 0.224, 0.225], np.float32)
+    want = ((img - mean) / std).transpose(0, 3, 1, 2)
+    assert got.dtype == np.float32 and np.array_equal(got, want)
+    # coded pattern: value encodes (b, y, x, c); the output plane c holds it
+    b, y, x, c = np.meshgrid(np.arange(2), np.arange(5), np.arange(7), np.arange(3),
+                             indexing="ij")
+    code = (1000 * b + 100 * y + 10 * x + c).astype(np.float32)
+    back = O.preprocess_image(code) * std[None, :, None, None] + mean[None, :, None, None]
+    np.testing.assert_allclose(back, code.transpose(0, 3, 1, 2), rtol=1e-6)
+
+
+def test_collect_points_mask_order_and_edges():
+    rng = np.random.default_rng(5)
+    pts = rng.standard_normal((3, 4, 5, 3)).astype(np.float32)
+    conf = rng.random((3, 4, 5, 1)).astype(np.float32)
+    conf[0, 0, 0, 0] = np.nan
+    conf[1, 2, 3, 0] = 0.5  # equal to the threshold: not selected (strict >)
+    p, c = O.collect_points(pts, conf, 0.5)
+    m = conf.reshape(-1) > 0.5
+    assert np.array_equal(p, pts.reshape(-1, 3)[m]) and np.array_equal(c, conf.reshape(-1)[m])
+    p, c = O.collect_points(pts, conf, 2.0)
+    assert p.shape == (0, 3) and c.shape == (0,)
+    p, c = O.collect_points(pts, np.nan_to_num(conf), -1.0)
+    assert np.array_equal(p, pts.reshape(-1, 3))
