@@ -171,7 +171,8 @@ __global__ void rope_ref_token_kernel(const float* __restrict__ x, float* __rest
 
 // DPT head tail: 1x1 conv Cin -> 4 (+bias), pts = ch 0..2, conf = 1 + exp(ch 3)
 // (the reference's split_output, src/mastr/decoder_v2.cr:619-655, with the
-// MASt3R confidence mapping).
+// MASt3R confidence mapping) or, SIGMOID, the reference's own 1 / (1 + exp(-x)).
+template <bool SIGMOID>
 __global__ __launch_bounds__(256) void head_out_kernel(const float* __restrict__ x, int64_t P,
                                                        int32_t Cin, const float* __restrict__ w,
                                                        const float* __restrict__ b,
@@ -199,7 +200,8 @@ __global__ __launch_bounds__(256) void head_out_kernel(const float* __restrict__
   pts[px * 3 + 0] = a0 + b[0];
   pts[px * 3 + 1] = a1 + b[1];
   pts[px * 3 + 2] = a2 + b[2];
-  conf[px] = 1.0f + expf(a3 + b[3]);
+  const float raw = a3 + b[3];
+  conf[px] = SIGMOID ? 1.0f / (1.0f + expf(-raw)) : 1.0f + expf(raw);
 }
 
 inline unsigned nblocks(int64_t total, int per) { return (unsigned)((total + per - 1) / per); }
@@ -289,13 +291,17 @@ int launch_rope_ref_token(const float* x, float* y, int32_t B, int32_t gh, int32
 }
 
 int launch_head_out(const float* x, int64_t P, int32_t Cin, const float* w, const float* b,
-                    float* pts, float* conf, hipStream_t s) {
+                    float* pts, float* conf, bool sigmoid, hipStream_t s) {
   GS_REQUIRE(Cin % 4 == 0 && Cin <= 4096, "head_out: need Cin % 4 == 0");
   GS_REQUIRE(aligned16(x), "head_out: input must be 16-byte aligned");
   if (P == 0) return 0;
   hipEvent_t ev = prof_start(s);
-  hipLaunchKernelGGL(head_out_kernel, dim3(nblocks(P, 256)), dim3(256),
-                     4 * Cin * sizeof(float), s, x, P, Cin, w, b, pts, conf);
+  if (sigmoid)
+    hipLaunchKernelGGL(head_out_kernel<true>, dim3(nblocks(P, 256)), dim3(256),
+                       4 * Cin * sizeof(float), s, x, P, Cin, w, b, pts, conf);
+  else
+    hipLaunchKernelGGL(head_out_kernel<false>, dim3(nblocks(P, 256)), dim3(256),
+                       4 * Cin * sizeof(float), s, x, P, Cin, w, b, pts, conf);
   GS_CHECK_HIP(hipGetLastError());
   prof_stop(s, ev, "head_out_kernel", 8.0 * (double)P * Cin, 4.0 * (double)P * (Cin + 4));
   return 0;

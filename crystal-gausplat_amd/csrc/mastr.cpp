@@ -127,7 +127,9 @@ Inventory make_inventory(const gs_mastr_config& c) {
       v.conv(p + ".dpt.scratch.layer" + std::to_string(i + 1) + "_rn", F, d[i], 3, false);
     for (int r = 1; r <= 4; ++r) {
       const std::string rp = p + ".dpt.scratch.refinenet" + std::to_string(r);
-      for (int u = (r == 4 ? 2 : 1); u <= 2; ++u) {
+      // refinenet4's first unit has no input in the full DPT (no skip at the
+      // deepest level) but is in the checkpoint and in the reference's stub
+      for (int u = 1; u <= 2; ++u) {
         v.conv(rp + ".resConfUnit" + std::to_string(u) + ".conv1", F, F, 3);
         v.conv(rp + ".resConfUnit" + std::to_string(u) + ".conv2", F, F, 3);
       }
@@ -174,6 +176,7 @@ struct Ctx {
   size_t arena_size = 0;
   // workspaces
   float *P, *x, *h, *qkv, *att, *mlp, *enc, *d, *ym, *kv, *q, *hook1, *hook2, *dfin;
+  float* dmem;  // composite 1: decoder_embed output, the fixed cross-attention memory
   // DPT / descriptor workspaces, one slot per head of a grouped launch
   float *t0[2], *act[2][4], *L[2][4], *u[2], *s[2], *t[2], *up[2], *rA[2], *rB[2], *hd0[2],
       *hup[2], *hd2[2], *lf[2];
@@ -378,9 +381,13 @@ int decoder(Ctx& c, int B, hipStream_t s) {
   const int64_t Mv = (int64_t)B * c.N, M = 2 * Mv;
   const float eps = f.ln_eps;
   const bool rope = f.rope_mode == 1;
-  RC(run1(c, lin(c.enc, De, W(c, "decoder_embed.weight"), W(c, "decoder_embed.bias"), c.d, D, M, D,
-                 De, 0),
-          A_PLAIN, s));
+  const bool own_memory = f.composite == 1;
+  {
+    GemmArgs a = lin(c.enc, De, W(c, "decoder_embed.weight"), W(c, "decoder_embed.bias"), c.d, D, M,
+                     D, De, own_memory ? EPI_DUAL : 0);
+    a.C2 = own_memory ? c.dmem : nullptr;
+    RC(run1(c, a, A_PLAIN, s));
+  }
   for (int l = 0; l < f.dec_depth; ++l) {
     std::string p[2] = {"dec_blocks." + std::to_string(l), "dec_blocks2." + std::to_string(l)};
     float* dc[2] = {c.d, c.d + Mv * D};
@@ -399,8 +406,13 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       bt.ngroups = 2;
       return launch_layernorm(bt, s);
     };
-    // Cross-attention memory = the other view's state before this block.
+    // Cross-attention memory: the other view's state before this block, or
+    // (composite 1) this view's decoder_embed output.
     float* other[2] = {dc[1], dc[0]};
+    if (own_memory) {
+      other[0] = c.dmem;
+      other[1] = c.dmem + Mv * D;
+    }
     RC(ln2(".norm_y", other, yc));
     {
       GemmArgs a[2];
@@ -629,7 +641,45 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
   for (int v = 0; v < hs.n; ++v)
     RC(launch_head_out(c.hd2[v], (int64_t)B * 4 * h1 * w1, f.head_mid,
                        W(c, hs.pre(v) + ".dpt.head.4.weight"), W(c, hs.pre(v) + ".dpt.head.4.bias"),
-                       pts[v], conf[v], s));
+                       pts[v], conf[v], false, s));
+  return 0;
+}
+
+// The reference's stub DPTHead#forward (src/mastr/decoder_v2.cr:502-530) on
+// the patch grid: layer4_rn (3x3, no bias) -> refinenet4 without skip (two
+// conv-ReLU-conv+x units, src/mastr/decoder_v2.cr:365-370, then the 1x1
+// out_conv) -> ReLU -> head.0 -> ReLU -> head.2 -> head.4 -> pts, sigmoid conf.
+// The ReLUs before head.0 / head.2 run as the convolutions' input prologue.
+int dpt_ref_heads(Ctx& c, const Heads& hs, const float* const dfin[2], int B,
+                  float* const pts[2], float* const conf[2], hipStream_t s) {
+  const gs_mastr_config& f = c.cfg;
+  const int F = f.dpt_feat, gh = c.gh, gw = c.gw;
+  float* L[2] = {c.L[0][2], c.L[1][2]};
+  RC(conv(c, hs, ".dpt.scratch.layer4_rn", dfin, B, gh, gw, f.dec_dim, F, 3, 1, 1, false, L, 0,
+          false, s));
+  const std::string rp = ".dpt.scratch.refinenet4";
+  const float* Lc[2] = {L[0], L[1]};
+  const float* uc[2] = {c.u[0], c.u[1]};
+  RC(conv(c, hs, rp + ".resConfUnit1.conv1", Lc, B, gh, gw, F, F, 3, 1, 1, true, c.u, EPI_RELU,
+          false, s));
+  RC(conv(c, hs, rp + ".resConfUnit1.conv2", uc, B, gh, gw, F, F, 3, 1, 1, true, c.s, 0, false, s,
+          Lc));
+  const float* sc[2] = {c.s[0], c.s[1]};
+  RC(conv(c, hs, rp + ".resConfUnit2.conv1", sc, B, gh, gw, F, F, 3, 1, 1, true, c.u, EPI_RELU,
+          false, s));
+  RC(conv(c, hs, rp + ".resConfUnit2.conv2", uc, B, gh, gw, F, F, 3, 1, 1, true, c.t, 0, false, s,
+          sc));
+  const float* tc[2] = {c.t[0], c.t[1]};
+  RC(conv(c, hs, rp + ".out_conv", tc, B, gh, gw, F, F, 1, 1, 0, true, c.up, 0, false, s));
+  const float* upc[2] = {c.up[0], c.up[1]};
+  RC(conv(c, hs, ".dpt.head.0", upc, B, gh, gw, F, F / 2, 3, 1, 1, true, c.hd0, 0, true, s));
+  const float* h0c[2] = {c.hd0[0], c.hd0[1]};
+  RC(conv(c, hs, ".dpt.head.2", h0c, B, gh, gw, F / 2, f.head_mid, 3, 1, 1, true, c.hd2, 0, true,
+          s));
+  for (int v = 0; v < hs.n; ++v)
+    RC(launch_head_out(c.hd2[v], (int64_t)B * c.N, f.head_mid,
+                       W(c, hs.pre(v) + ".dpt.head.4.weight"), W(c, hs.pre(v) + ".dpt.head.4.bias"),
+                       pts[v], conf[v], true, s));
   return 0;
 }
 
@@ -852,6 +902,7 @@ int build_workspace(Ctx& c) {
       {&c.hook1, M * Dd},
       {&c.hook2, M * Dd},
       {&c.dfin, M * Dd},
+      {&c.dmem, f.composite == 1 ? M * Dd : 0},
       {&c.rope_cos, 512 * 16},
       {&c.rope_sin, 512 * 16},
       {&c.ref_cos, 512 * (De / f.enc_heads / 2)},
@@ -923,6 +974,9 @@ int validate_config(const gs_mastr_config& f) {
   GS_REQUIRE(f.precision == 0 || (f.precision == 1 && f.linear_layout == 0),
              "config: precision must be 0 (fp32) or 1 (bf16 MFMA, linear_layout 0)");
   GS_REQUIRE(f.enc_dim % 32 == 0 && f.dec_dim % 32 == 0, "config: dims must be multiples of 32");
+  GS_REQUIRE(f.composite == 0 || f.composite == 1, "config: composite must be 0 or 1");
+  GS_REQUIRE(f.composite == 0 || f.dpt_dims[3] == f.dec_dim,
+             "config: composite 1 applies layer4_rn to the decoder output (dpt_dims[3] == dec_dim)");
   return 0;
 }
 
@@ -1134,7 +1188,8 @@ int pair_body(Ctx* c, const float* img1, const float* img2, int32_t B, float* pt
       ld[k] = desc[v];
     }
   }
-  if (hd.n) RC(dpt_heads(*c, hd, ge, gh6, gh9, gdf, B, gp, gc, s));
+  if (hd.n && f.composite == 1) RC(dpt_ref_heads(*c, hd, gdf, B, gp, gc, s));
+  if (hd.n && f.composite == 0) RC(dpt_heads(*c, hd, ge, gh6, gh9, gdf, B, gp, gc, s));
   if (hl.n) RC(local_features(*c, hl, le, ldf, B, ld, s));
   return 0;
 }
@@ -1151,6 +1206,8 @@ int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2, int32
   GS_REQUIRE(B > 0 && B <= c->max_pairs, "pair: B exceeds context capacity");
   GS_REQUIRE(c->cfg.linear_layout == 0, "pair: the literal linear layout is encoder-only");
   GS_REQUIRE(!pts1 == !conf1 && !pts2 == !conf2, "pair: pts and conf must be given together");
+  GS_REQUIRE(c->cfg.composite == 0 || (!desc1 && !desc2),
+             "pair: composite 1 (reference stub heads) has no descriptor head");
   hipStream_t s = (hipStream_t)stream;
   RC(sync_bf16(*c, s));
   if (!c->graph_on || prof_on())
@@ -1225,13 +1282,15 @@ int32_t gs_hip_mastr_frames_to_pointcloud(void* ctx, const float* frames, int32_
   GS_REQUIRE(capacity >= 0 && (capacity == 0 || (out_pts && out_conf)),
              "frames_to_pointcloud: bad output buffers");
   hipStream_t s = (hipStream_t)stream;
-  const int64_t H = c->cfg.img_h, W = c->cfg.img_w, HW = H * W;
+  const int64_t H = c->cfg.img_h, W = c->cfg.img_w;
+  // point maps are at image resolution, or on the patch grid for composite 1
+  const int64_t HWo = c->cfg.composite == 1 ? c->N : H * W;
   const int32_t P = F - 1;
   const int32_t Bmax = std::min(c->max_pairs, P);
   // carve the buffer
-  const size_t sz_prep = align256((size_t)F * 3 * HW * 4), sz_pts = align256((size_t)Bmax * HW * 12),
-               sz_conf = align256((size_t)Bmax * HW * 4), sz_cnt = 256,
-               sz_scr = align256((size_t)collect_points_scratch(Bmax * HW) * 8);
+  const size_t sz_prep = align256((size_t)F * 3 * H * W * 4),
+               sz_pts = align256((size_t)Bmax * HWo * 12), sz_conf = align256((size_t)Bmax * HWo * 4),
+               sz_cnt = 256, sz_scr = align256((size_t)collect_points_scratch(Bmax * HWo) * 8);
   const size_t need = sz_prep + 2 * sz_pts + 2 * sz_conf + sz_cnt + sz_scr;
   if (need > c->pcbuf_size) {
     if (c->pcbuf) {
@@ -1265,13 +1324,14 @@ int32_t gs_hip_mastr_frames_to_pointcloud(void* ctx, const float* frames, int32_
   for (int32_t p0 = 0; p0 < P; p0 += Bmax) {
     const int32_t Bc = std::min(Bmax, P - p0);
     const bool last = p0 + Bc == P;
-    RC(pair_body(c, prep + (int64_t)p0 * 3 * HW, prep + (int64_t)(p0 + 1) * 3 * HW, Bc, pts1,
-                 conf1, nullptr, last ? pts2 : nullptr, last ? conf2 : nullptr, nullptr, s));
-    RC(launch_collect_points(pts1, conf1, (int64_t)Bc * HW, threshold, out_pts, out_conf,
+    RC(pair_body(c, prep + (int64_t)p0 * 3 * H * W, prep + (int64_t)(p0 + 1) * 3 * H * W, Bc,
+                 pts1, conf1, nullptr, last ? pts2 : nullptr, last ? conf2 : nullptr, nullptr, s));
+    RC(launch_collect_points(pts1, conf1, (int64_t)Bc * HWo, threshold, out_pts, out_conf,
                              capacity, counter, scratch, s));
     if (last)
-      RC(launch_collect_points(pts2 + (int64_t)(Bc - 1) * HW * 3, conf2 + (int64_t)(Bc - 1) * HW,
-                               HW, threshold, out_pts, out_conf, capacity, counter, scratch, s));
+      RC(launch_collect_points(pts2 + (int64_t)(Bc - 1) * HWo * 3,
+                               conf2 + (int64_t)(Bc - 1) * HWo, HWo, threshold, out_pts, out_conf,
+                               capacity, counter, scratch, s));
   }
   int64_t n = 0;
   GS_CHECK_HIP(hipMemcpyAsync(&n, counter, sizeof(n), hipMemcpyDeviceToHost, s));

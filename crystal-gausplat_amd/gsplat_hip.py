@@ -33,6 +33,7 @@ class MastrConfig(C.Structure):
         ("linear_layout", C.c_int32),
         ("rope_mode", C.c_int32),
         ("precision", C.c_int32),
+        ("composite", C.c_int32),
     ]
 
     def as_dict(self):
@@ -167,6 +168,16 @@ def default_config(**over):
         else:
             setattr(cfg, k, v)
     return cfg
+
+
+def ref512_config(**over):
+    """The reference's literal MASt3RInference#forward_pair at 512x512
+    (src/mastr/inference.cr:25-57, 92-115): token-level RoPE, LayerNorm eps
+    1e-5, own-view decoder memory, stub DPT heads on the 32x32 patch grid,
+    sigmoid confidence."""
+    kw = dict(img_h=512, img_w=512, rope_mode=2, ln_eps=1e-5, composite=1)
+    kw.update(over)
+    return default_config(**kw)
 
 
 def weight_inventory(cfg):

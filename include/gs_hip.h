@@ -215,6 +215,19 @@ typedef struct gs_mastr_config {
   int32_t rope_mode;     /* 0 none, 1 per-attention q/k 2D, 2 ref-token */
   int32_t precision;     /* 0 = fp32 MFMA; 1 = bf16-input / fp32-accumulate
                             MFMA GEMMs and attention (linear_layout 0 only) */
+  int32_t composite;     /* 0 = MASt3R composition (full DPT at image
+                            resolution, 1+exp confidence, descriptors, each
+                            decoder chain attending to the other view's
+                            previous state);
+                            1 = the reference's literal forward_pair: each
+                            chain attends to its own view's decoder_embed
+                            output (src/mastr/decoder_v2.cr:170-191), stub DPT
+                            at patch resolution (layer4_rn -> refinenet4 with
+                            conv-ReLU-conv+x units -> ReLU, head.0, ReLU,
+                            head.2, head.4), sigmoid confidence
+                            (src/mastr/decoder_v2.cr:502-530, 619-655), no
+                            descriptors. "ref512" = composite 1 at 512x512,
+                            rope_mode 2, ln_eps 1e-5. */
 } gs_mastr_config;
 
 /* MASt3R ViT-L/ViT-B at 384x512 (24x32 patch grid), eps 1e-6, RoPE base 100,
@@ -259,7 +272,9 @@ int32_t gs_hip_mastr_encoder(void* ctx, const float* img, int32_t B,
                              float* enc, void* stream);
 /* MASt3RInference#forward_pair (src/mastr/inference.cr:92-115) for B pairs:
  * img1, img2 [B,3,H,W] -> per view pts [B,H,W,3], conf [B,H,W,1] (1+exp),
- * desc [B,H,W,desc_dim]. Any output pointer may be NULL to skip that head. */
+ * desc [B,H,W,desc_dim]. Any output pointer may be NULL to skip that head.
+ * composite 1: pts [B,gh,gw,3], conf [B,gh,gw,1] (sigmoid) on the patch grid
+ * gh = H/patch, gw = W/patch; desc must be NULL. */
 int32_t gs_hip_mastr_pair(void* ctx, const float* img1, const float* img2,
                           int32_t B, float* pts1, float* conf1, float* desc1,
                           float* pts2, float* conf2, float* desc2,

@@ -68,7 +68,11 @@
  *                       356-437 (RCU / RefineNet), 502-530 + 619-655 (head).
  *                       Composition follows the MASt3R configuration (other
  *                       view as cross-attention memory, full DPT, 1+exp
- *                       confidence, local-feature descriptors). Pinned: every
+ *                       confidence, local-feature descriptors); composite 1
+ *                       follows the reference's own forward_pair instead
+ *                       (decoder_v2.cr:176-184 own-view memory, 502-530 stub
+ *                       DPT with the 365-370 residual unit, 619-655 sigmoid
+ *                       confidence). Pinned: every
  *                       primitive above, view-swap symmetry with shared
  *                       decoder weights, determinism, and hand-composed
  *                       torch CPU reference of an encoder block.
@@ -843,6 +847,48 @@ void dpt_head(const Ctx& c, const std::string& pre, const float* const hooks[4],
   }
 }
 
+/* The reference's ResidualConvUnit (src/mastr/decoder_v2.cr:365-370):
+ * y = x + conv2(ReLU(conv1(x))). */
+void rcu_ref(const Ctx& c, const std::string& name, const float* x, int32_t B,
+             int32_t H, int32_t W, int32_t F, float* y) {
+  const int64_t n = (int64_t)B * H * W * F;
+  Buf t(n), u(n);
+  conv_mod(c, name + ".conv1", x, B, H, W, F, F, 3, 1, 1, true, t.data());
+  orc_relu(t.data(), n, t.data());
+  conv_mod(c, name + ".conv2", t.data(), B, H, W, F, F, 3, 1, 1, true, u.data());
+  orc_add(x, u.data(), n, y);
+}
+
+/* The reference's stub DPTHead#forward (src/mastr/decoder_v2.cr:502-530) and
+ * split_output (619-655): layer4_rn on the patch grid, refinenet4 without
+ * skip (RefineNetBlock#forward, 408-417), ReLU, head.0, ReLU, head.2,
+ * head.4, sigmoid confidence. */
+void dpt_ref_head(const Ctx& c, const std::string& pre, const float* dec,
+                  int32_t B, int32_t gh, int32_t gw, float* pts, float* conf) {
+  const orc_config* cf = c.cfg;
+  const int32_t F = cf->dpt_feat, Fh = F / 2, Hm = cf->head_mid;
+  const int64_t P = (int64_t)B * gh * gw, n = P * F;
+  Buf x(n), y(n), z(n);
+  conv_mod(c, pre + ".dpt.scratch.layer4_rn", dec, B, gh, gw, cf->dec_dim, F, 3, 1, 1,
+           false, x.data());
+  const std::string rp = pre + ".dpt.scratch.refinenet4";
+  rcu_ref(c, rp + ".resConfUnit1", x.data(), B, gh, gw, F, y.data());
+  rcu_ref(c, rp + ".resConfUnit2", y.data(), B, gh, gw, F, z.data());
+  conv_mod(c, rp + ".out_conv", z.data(), B, gh, gw, F, F, 1, 1, 0, true, x.data());
+  orc_relu(x.data(), n, x.data());
+  Buf h0((size_t)P * Fh), h1((size_t)P * Hm), h2((size_t)P * 4);
+  conv_mod(c, pre + ".dpt.head.0", x.data(), B, gh, gw, F, Fh, 3, 1, 1, true, h0.data());
+  orc_relu(h0.data(), (int64_t)h0.size(), h0.data());
+  conv_mod(c, pre + ".dpt.head.2", h0.data(), B, gh, gw, Fh, Hm, 3, 1, 1, true, h1.data());
+  conv_mod(c, pre + ".dpt.head.4", h1.data(), B, gh, gw, Hm, 4, 1, 1, 0, true, h2.data());
+  for (int64_t i = 0; i < P; ++i) {
+    pts[i * 3 + 0] = h2[i * 4 + 0];
+    pts[i * 3 + 1] = h2[i * 4 + 1];
+    pts[i * 3 + 2] = h2[i * 4 + 2];
+    conf[i] = 1.0f / (1.0f + expf(-h2[i * 4 + 3]));
+  }
+}
+
 /* Local features: MLP(concat(enc, dec_final)) -> pixel shuffle -> desc. */
 void local_features(const Ctx& c, const std::string& pre, const float* enc,
                     const float* dec, int32_t B, int32_t gh, int32_t gw,
@@ -898,9 +944,15 @@ void pair(const Ctx& c, const float* img1, const float* img2, int32_t B,
   linear_mod(c, "decoder_embed", e2.data(), M, De, Dd, d2.data());
   /* hooks: index 0 = encoder output, l = state after decoder block l */
   Buf hook1[4], hook2[4];
+  if (cf->composite == 1) { /* src/mastr/decoder_v2.cr:176-184: own view, fixed */
+    m1 = d1;
+    m2 = d2;
+  }
   for (int32_t l = 0; l < cf->dec_depth; ++l) {
-    m1 = d2; /* each chain attends to the other view's previous state */
-    m2 = d1;
+    if (cf->composite == 0) {
+      m1 = d2; /* each chain attends to the other view's previous state */
+      m2 = d1;
+    }
     decoder_block(c, "dec_blocks." + std::to_string(l), d1.data(), m1.data(), B, N, gw);
     decoder_block(c, "dec_blocks2." + std::to_string(l), d2.data(), m2.data(), B, N, gw);
     for (int i = 1; i < 3; ++i)
@@ -917,6 +969,11 @@ void pair(const Ctx& c, const float* img1, const float* img2, int32_t B,
   if (!pts1 && !pts2 && !desc1 && !desc2) return;
   const float* h1[4] = {e1.data(), hook1[1].data(), hook1[2].data(), f1.data()};
   const float* h2[4] = {e2.data(), hook2[1].data(), hook2[2].data(), f2.data()};
+  if (cf->composite == 1) {
+    if (pts1) dpt_ref_head(c, "downstream_head1", f1.data(), B, gh, gw, pts1, conf1);
+    if (pts2) dpt_ref_head(c, "downstream_head2", f2.data(), B, gh, gw, pts2, conf2);
+    return;
+  }
   if (pts1) dpt_head(c, "downstream_head1", h1, B, gh, gw, pts1, conf1);
   if (pts2) dpt_head(c, "downstream_head2", h2, B, gh, gw, pts2, conf2);
   if (desc1) local_features(c, "downstream_head1", e1.data(), f1.data(), B, gh, gw, desc1);
@@ -955,6 +1012,7 @@ extern "C" int32_t orc_mastr_pair(const orc_config* cfg, orc_weight_fn wf,
                                   float* conf1, float* desc1, float* pts2,
                                   float* conf2, float* desc2) {
   if (check_pair_cfg(cfg)) return -1;
+  if (cfg->composite == 1 && (desc1 || desc2)) return -1;
   Ctx c{cfg, wf, user};
   pair(c, img1, img2, B, pts1, conf1, desc1, pts2, conf2, desc2, nullptr, nullptr,
        nullptr, nullptr);

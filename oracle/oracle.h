@@ -124,6 +124,10 @@ typedef struct orc_config {
   float rope_base;           /* 100 */
   int32_t linear_layout;     /* 0 = x W^T, 1 = reference CPU literal */
   int32_t rope_mode;         /* 0 none, 1 per-attention q/k 2D, 2 ref-token */
+  int32_t composite;         /* 0 MASt3R composition; 1 the reference's
+                                literal forward_pair (own-view decoder
+                                memory, stub DPT on the patch grid, sigmoid
+                                confidence, no descriptors) */
 } orc_config;
 
 /* Weights are fetched by name through a callback (arrays owned by caller). */
@@ -136,7 +140,8 @@ int32_t orc_encoder_block(const orc_config* cfg, const char* prefix,
 /* Full encoder: img [B,3,H,W] -> enc [B, N, enc_dim] (after enc_norm). */
 int32_t orc_encoder(const orc_config* cfg, orc_weight_fn wf, void* user,
                     const float* img, int32_t B, float* enc);
-/* Full two-view pair: outputs NHWC per view. */
+/* Full two-view pair: outputs NHWC per view (composite 1: pts / conf on the
+ * patch grid, desc must be NULL; returns -1 otherwise). */
 int32_t orc_mastr_pair(const orc_config* cfg, orc_weight_fn wf, void* user,
                        const float* img1, const float* img2, int32_t B,
                        float* pts1, float* conf1, float* desc1, float* pts2,

@@ -32,6 +32,7 @@ class OrcConfig(C.Structure):
         ("rope_base", C.c_float),
         ("linear_layout", C.c_int32),
         ("rope_mode", C.c_int32),
+        ("composite", C.c_int32),
     ]
 
 
@@ -284,7 +285,7 @@ def config_from(d):
     """OrcConfig from a dict with the gs_mastr_config field names."""
     c = OrcConfig()
     for name, _ in OrcConfig._fields_:
-        v = d[name]
+        v = d.get(name, 0) if name == "composite" else d[name]
         if isinstance(v, (list, tuple)):
             arr = getattr(c, name)
             for i, x in enumerate(v):
@@ -336,12 +337,16 @@ def encoder(cfgd, weights, img):
 
 
 def mastr_pair(cfgd, weights, img1, img2, heads=True, desc=True):
-    """Returns dict pts1, conf1, desc1, pts2, conf2, desc2 (NHWC)."""
+    """Returns dict pts1, conf1, desc1, pts2, conf2, desc2 (NHWC); with
+    composite 1 pts / conf are on the patch grid and desc is None."""
     cfg = config_from(cfgd)
     W = _Weights(weights)
     img1, img2 = f32(img1), f32(img2)
     B = img1.shape[0]
     H, Wd = cfgd["img_h"], cfgd["img_w"]
+    if cfgd.get("composite", 0) == 1:  # stub heads on the patch grid, no descriptors
+        H, Wd = H // cfgd["patch"], Wd // cfgd["patch"]
+        desc = False
     out = {}
     for v in (1, 2):
         out[f"pts{v}"] = np.empty((B, H, Wd, 3), np.float32) if heads else None

@@ -363,6 +363,64 @@ def test_oracle_thread_count_does_not_change_bits(tiny_cfg, tiny_weights):
         np.testing.assert_array_equal(a[k], b[k])
 
 
+def torch_ref_stub_head(dec, w, pre, gh, gw):
+    """The reference's stub DPTHead#forward + split_output
+    (src/mastr/decoder_v2.cr:502-530, 619-655) from torch CPU ops."""
+    t = torch.from_numpy
+    B, _, D = dec.shape
+
+    def conv(z, n, pad, bias=True):
+        return F.conv2d(z, t(w[n + ".weight"]), t(w[n + ".bias"]) if bias else None, padding=pad)
+
+    x = conv(t(dec).reshape(B, gh, gw, D).permute(0, 3, 1, 2), pre + ".dpt.scratch.layer4_rn", 1,
+             bias=False)
+    rp = pre + ".dpt.scratch.refinenet4"
+    for u in (1, 2):  # ResidualConvUnit: x + conv2(relu(conv1(x)))
+        x = x + conv(F.relu(conv(x, f"{rp}.resConfUnit{u}.conv1", 1)),
+                     f"{rp}.resConfUnit{u}.conv2", 1)
+    x = conv(x, rp + ".out_conv", 0)
+    x = conv(F.relu(x), pre + ".dpt.head.0", 1)
+    x = conv(F.relu(x), pre + ".dpt.head.2", 1)
+    x = conv(x, pre + ".dpt.head.4", 0).permute(0, 2, 3, 1)
+    return x[..., :3].numpy(), torch.sigmoid(x[..., 3:]).numpy()
+
+
+def _ref_cfg(tiny_cfg):
+    return dict(tiny_cfg, composite=1, rope_mode=2, ln_eps=1e-5)
+
+
+def test_ref_composite_stub_head_matches_torch(tiny_cfg, tiny_weights):
+    d = _ref_cfg(tiny_cfg)
+    i1 = RNG.uniform(-1, 1, (2, 3, 64, 96)).astype(np.float32)
+    i2 = RNG.uniform(-1, 1, (2, 3, 64, 96)).astype(np.float32)
+    out = O.mastr_pair(d, tiny_weights, i1, i2)
+    assert out["pts1"].shape == (2, 4, 6, 3) and out["desc1"] is None
+    _, _, d1, d2 = O.mastr_pair_taps(d, tiny_weights, i1, i2)
+    for v, dec in ((1, d1), (2, d2)):
+        p, c = torch_ref_stub_head(dec, tiny_weights, f"downstream_head{v}", 4, 6)
+        np.testing.assert_allclose(out[f"pts{v}"], p, rtol=1e-4, atol=1e-5)
+        np.testing.assert_allclose(out[f"conf{v}"], c, rtol=1e-4, atol=1e-6)
+    assert np.all((out["conf1"] > 0) & (out["conf1"] < 1))  # sigmoid
+
+
+def test_ref_composite_views_are_independent(tiny_cfg, tiny_weights):
+    """Reference decoder memory = the view's own decoder_embed output
+    (src/mastr/decoder_v2.cr:176-184): view 1 ignores image 2 entirely; the
+    MASt3R composition (other view's state) does not."""
+    i1 = RNG.uniform(-1, 1, (1, 3, 64, 96)).astype(np.float32)
+    i2 = RNG.uniform(-1, 1, (1, 3, 64, 96)).astype(np.float32)
+    i3 = RNG.uniform(-1, 1, (1, 3, 64, 96)).astype(np.float32)
+    d = _ref_cfg(tiny_cfg)
+    a = O.mastr_pair(d, tiny_weights, i1, i2)
+    b = O.mastr_pair(d, tiny_weights, i1, i3)
+    np.testing.assert_array_equal(a["pts1"], b["pts1"])
+    np.testing.assert_array_equal(a["conf1"], b["conf1"])
+    assert not np.array_equal(a["pts2"], b["pts2"])
+    a = O.mastr_pair(tiny_cfg, tiny_weights, i1, i2, desc=False)
+    b = O.mastr_pair(tiny_cfg, tiny_weights, i1, i3, desc=False)
+    assert not np.array_equal(a["pts1"], b["pts1"])
+
+
 # ---- caller-side passes (src/mastr/inference.cr:193-374) -------------------
 
 def test_resize_identity_corners_and_affine_ramp():
