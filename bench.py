@@ -1,12 +1,23 @@
 """MASt3R two-view inference throughput on one MI355X (pairs/s, fp32).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 3|2|4]
+    python bench.py --workload frames|ref512|checkpoint   (secondary lines)
 
 A step is one full forward (ViT-L encoder on both views, ViT-B cross-attention
 decoder, two DPT heads, two local-feature heads) over one batch of synthetic
 image pairs already resident in HBM. Default workload: config 3 of the
 baseline (16 pairs at 3x384x512, U(-1,1) images, seed-0 N(0,0.02) weights).
 Prints one JSON line.
+
+Secondary workloads (each its own JSON line, not the headline metric):
+  frames      frames_to_pointcloud: 33 synthetic 720x1280 frames resized and
+              normalised on the device, 32 consecutive pairs at 512x512 in one
+              batched call, confidence compaction; pairs/s end to end, with
+              the HBM roofline of the resize / compaction passes.
+  ref512      the reference-literal composition at 512x512 (stub DPT heads),
+              32 pairs per step; pairs/s.
+  checkpoint  gs_hip_mastr_load_safetensors of an fp32 checkpoint of the
+              default configuration written to a temporary file; GB/s.
 """
 import argparse
 import json
@@ -81,6 +92,107 @@ def cpu_baseline():
     }
 
 
+def _timed(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def _kernel_rates(prof, steps):
+    return {k: {"launches": v["launches"] // steps, "ms_per_step": round(v["ms"] / steps, 3),
+                "gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1) if v["bytes"] else None,
+                "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2) if v["flops"] else None}
+            for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
+
+
+def secondary(args):
+    import torch
+
+    import gsplat_hip as G
+    out = {"n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "higher_is_better": True,
+           "vs_baseline": None, "dtype": "f32", "data": "synthetic"}
+    stream = torch.cuda.current_stream().cuda_stream
+    if args.workload == "checkpoint":
+        import tempfile
+
+        from safetensors.numpy import save_file
+        cfg = G.default_config()
+        w = G.seeded_weights(cfg, 0, 0.02, 0.1)
+        nbytes = sum(a.nbytes for a in w.values())
+        m = G.Mastr(cfg, 1)
+        with tempfile.TemporaryDirectory() as td:
+            path = os.path.join(td, "mastr.safetensors")
+            save_file(w, path)
+            del w
+            counts = m.load_safetensors(path)  # warm the page cache
+            sec = _timed(lambda: m.load_safetensors(path), args.steps, 0)
+        m.close()
+        out.update(metric="MASt3R fp32 checkpoint ingestion (mmap, convert, re-layout, upload)",
+                   value=round(nbytes / sec / 1e9, 3), unit="GB/s", ms_per_step=round(sec * 1e3, 1),
+                   config={"workload": f"{counts['loaded']} tensors, {nbytes / 1e9:.2f} GB F32, "
+                                       "page-cached file"})
+        return out
+    if args.workload == "ref512":
+        B = args.pairs or 32
+        cfg = G.ref512_config()
+        m = G.Mastr(cfg, B)
+        m.init_seeded(0)
+        n = B * 3 * 512 * 512
+        i1 = torch.from_numpy(G.seed_uniform(0, "view1", n).reshape(B, 3, 512, 512)).cuda()
+        i2 = torch.from_numpy(G.seed_uniform(0, "view2", n).reshape(B, 3, 512, 512)).cuda()
+        o = [torch.empty(B, 32, 32, c, device="cuda") for c in (3, 1, 3, 1)]
+        fn = lambda: m.pair(i1, i2, B, o[0], o[1], None, o[2], o[3], None, stream=stream)
+        sec = _timed(fn, args.steps, args.warmup)
+        G.profile_begin()
+        fn()
+        torch.cuda.synchronize()
+        prof = G.profile_end()
+        m.close()
+        out.update(metric="reference-literal MASt3R forward_pair (ref512) pairs/sec, fp32",
+                   value=round(B / sec, 3), unit="pairs/s", ms_per_step=round(sec * 1e3, 3),
+                   config={"workload": f"ref512: {B} pairs at 3x512x512, stub DPT heads on the "
+                                       "32x32 patch grid"},
+                   kernels=_kernel_rates(prof, 1))
+        return out
+    # frames -> point cloud
+    F, sh, sw = 33, 720, 1280
+    cfg = G.default_config(img_h=512, img_w=512)
+    m = G.Mastr(cfg, F - 1)
+    m.init_seeded(0)
+    frames = torch.rand(F, sh, sw, 3, device="cuda", generator=torch.Generator("cuda").manual_seed(0))
+    cap = F * 512 * 512
+    op, oc = torch.empty(cap, 3, device="cuda"), torch.empty(cap, device="cuda")
+    npts = []
+    fn = lambda: npts.append(m.frames_to_pointcloud(frames, 0.3, op, oc, stream=stream))
+    sec = _timed(fn, args.steps, args.warmup)
+    G.profile_begin()
+    fn()
+    torch.cuda.synchronize()
+    prof = G.profile_end()
+    m.close()
+    rates = _kernel_rates(prof, 1)
+    passes = {k: v for k, v in rates.items() if k.startswith(("image_prep", "collect_points"))}
+    dom = max(passes, key=lambda k: passes[k]["ms_per_step"])
+    out.update(metric="MASt3R frames_to_pointcloud, consecutive pairs/sec @512x512 fp32 "
+                      "(device resize/normalise + pairs + compaction)",
+               value=round((F - 1) / sec, 3), unit="pairs/s", ms_per_step=round(sec * 1e3, 3),
+               config={"workload": f"{F} frames 3x{sh}x{sw} -> {F - 1} pairs at 512x512, "
+                                   f"threshold 0.3, {npts[-1]} points"},
+               roofline={"bound": "hbm", "kernel": dom, "achieved": passes[dom]["gbs"],
+                         "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(passes[dom]["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+               caller_passes=passes,
+               caller_share_of_step=round(sum(v["ms_per_step"] for v in passes.values())
+                                          / (sec * 1e3), 5))
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,6 +209,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--per-shape", action="store_true",
                     help="also print a per-shape kernel table (stderr) from a separate step")
+    ap.add_argument("--workload", default="pair", choices=["pair", "frames", "ref512", "checkpoint"])
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device-to-device copies of MIB MiB (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -121,6 +234,9 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_each_way": 4 * n, "copies": 3}))
+        return
+    if args.workload != "pair":
+        print(json.dumps(secondary(args)), flush=True)
         return
     wl = CONFIGS[args.config]
     B = args.pairs or wl["pairs"]
@@ -183,6 +299,18 @@ def main():
         achieved = dom["bytes"] / dom["launches"] / (avg_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None}
+    # HBM traffic per launch of this kernel, from the committed rocprofv3 PMC
+    # summary of the same workload (null when the workload has none)
+    try:
+        tr = json.load(open(os.path.join(ROOT, "profiles", "pmc_traffic.json")))["workloads"]
+        key = f"config{args.config}-{'graph' if args.graph else 'eager'}-" \
+              f"{'bf16' if args.bf16 else 'f32'}-{B}"
+        t = tr.get(key, {}).get(dom_name)
+        if t:
+            roof["traffic"] = (t["fetch_kib"] + t["write_kib"]) * 1024
+            roof["traffic_source"] = f"profiles/pmc_traffic.json [{key}]"
+    except (OSError, ValueError, KeyError):
+        pass
     roof["kernel"] = dom_name
     roof["launches_per_step"] = dom["launches"] // args.steps
     roof["avg_launch_ms"] = round(avg_ms, 4)

@@ -231,8 +231,9 @@ int launch_collect_points(const float* pts, const float* conf, int64_t n, float 
   hipLaunchKernelGGL(cp_scatter_kernel, dim3((uint32_t)nblk), dim3(kCpThreads), 0, s, pts, conf,
                      n, thr, scratch, out_pts, out_conf, cap);
   GS_CHECK_HIP(hipGetLastError());
-  // algorithmic bytes: confidences read twice, points read once (upper bound)
-  prof_stop(s, ev, "collect_points", 0.0, 4.0 * (double)n * 5.0);
+  // bytes with every point selected: confidences read twice, points read,
+  // points and confidences written (36 B per point; an upper bound otherwise)
+  prof_stop(s, ev, "collect_points", 0.0, 36.0 * (double)n);
   return 0;
 }
 
