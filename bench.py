@@ -18,6 +18,11 @@ Secondary workloads (each its own JSON line, not the headline metric):
               32 pairs per step; pairs/s.
   checkpoint  gs_hip_mastr_load_safetensors of an fp32 checkpoint of the
               default configuration written to a temporary file; GB/s.
+  block       config 0: one ViT-L encoder block, 768 tokens; ms per block.
+  encoder     config 1: the full ViT-L encoder on one 384x512 image.
+  cpu         the oracle's literal reference loops on the host: config 0 at 1 and
+              all threads, config 1 (24 blocks, progress on stderr) at 1 and all
+              threads; config 2 extrapolated by FLOPs.
 """
 import argparse
 import json
@@ -92,6 +97,51 @@ def cpu_baseline():
     }
 
 
+def cpu_table():
+    """Oracle (literal reference loops) timings on the host for BASELINE's table."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import gsplat_hip as G
+    import pyoracle as O
+    cfg = G.default_config(enc_depth=24, dec_depth=1, dpt_hooks=[0, 1, 1, 1])
+    inv = G.weight_inventory(cfg)
+    w = {n: G.weight_values(cfg, i, int(np.prod(s))).reshape(s)
+         for i, (n, s, k) in enumerate(inv) if n.startswith(("enc_blocks.", "patch_embed.", "enc_norm."))}
+    nthreads = os.cpu_count()
+    O.set_naive(True)
+    res = {}
+    x = G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)
+    for T in (1, nthreads):
+        O.set_threads(T)
+        t0 = time.perf_counter()
+        O.encoder_block(cfg.as_dict(), w, "enc_blocks.0", x, 24, 32)
+        res[f"config0_s_{T}t"] = round(time.perf_counter() - t0, 3)
+        print(f"[cpu] config 0, {T} threads: {res[f'config0_s_{T}t']} s", file=sys.stderr, flush=True)
+    img = G.seed_uniform(0, "view1", 3 * 384 * 512).reshape(1, 3, 384, 512)
+    for T in (nthreads, 1):
+        O.set_threads(T)
+        t0 = time.perf_counter()
+        # the encoder block by block (same work as O.encoder), so progress shows
+        pe = O.unfold(img, 16)
+        h = O.linear(pe.reshape(-1, 768), w["patch_embed.proj.weight"].reshape(1024, -1),
+                     w["patch_embed.proj.bias"], naive=True).reshape(1, 768, 1024)
+        for l in range(24):
+            h = O.encoder_block(cfg.as_dict(), w, f"enc_blocks.{l}", h, 24, 32)
+            print(f"[cpu] config 1, {T} threads: block {l} at {time.perf_counter() - t0:.1f} s",
+                  file=sys.stderr, flush=True)
+        O.layernorm(h, w["enc_norm.weight"], w["enc_norm.bias"], cfg.ln_eps)
+        res[f"config1_s_{T}t"] = round(time.perf_counter() - t0, 2)
+    O.set_naive(False)
+    O.set_threads(0)
+    ratio = PAIR_GFLOP_384x512 / 523.0
+    return {"metric": "reference CPU path (oracle literal loops) seconds", "unit": "s",
+            "cpu": cpu_model(), "threads_all": nthreads, **res,
+            "config2_s_per_pair_1t_extrapolated": round(res["config1_s_1t"] * ratio, 1),
+            "config2_s_per_pair_all_extrapolated": round(res[f"config1_s_{nthreads}t"] * ratio, 1),
+            "extrapolation": f"config 1 x {ratio:.3f} (2037.2 / 523.0 GFLOP)"}
+
+
 def _timed(fn, steps, warmup):
     import torch
     for _ in range(warmup):
@@ -138,6 +188,45 @@ def secondary(args):
                    config={"workload": f"{counts['loaded']} tensors, {nbytes / 1e9:.2f} GB F32, "
                                        "page-cached file"})
         return out
+    if args.workload in ("block", "encoder"):
+        cfg = G.default_config()
+        m = G.Mastr(cfg, 1)
+        m.init_seeded(0)
+        if args.workload == "block":
+            x0 = torch.from_numpy(G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)).cuda()
+            x = torch.empty_like(x0)
+            def fn():
+                x.copy_(x0)
+                m.encoder_block(0, x, 1, stream=stream)
+            gflop, what = BLOCK_GFLOP, "config 0: one ViT-L block, 768 tokens, batch 1"
+        else:
+            img = torch.from_numpy(G.seed_uniform(0, "view1", 3 * 384 * 512).reshape(1, 3, 384, 512)).cuda()
+            enc = torch.empty(1, 768, 1024, device="cuda")
+            fn = lambda: m.encoder(img, 1, enc, stream=stream)
+            gflop, what = 523.0, "config 1: ViT-L encoder, one 3x384x512 image"
+        sec = _timed(fn, args.steps, args.warmup)
+        G.profile_begin()
+        fn()
+        torch.cuda.synchronize()
+        prof = G.profile_end()
+        if args.per_shape:
+            G.profile_begin(per_shape=True)
+            fn()
+            torch.cuda.synchronize()
+            for k, v in sorted(G.profile_end().items(), key=lambda kv: -kv[1]["ms"]):
+                tf = v["flops"] / (v["ms"] * 1e-3) / 1e12 if v["flops"] else 0.0
+                print(f"{v['ms']:9.3f} ms {v['launches']:4d}x {tf:7.1f} TF/s  {k}", file=sys.stderr)
+        m.close()
+        mm = [v for k, v in prof.items() if k.startswith(("gemm", "attn"))]
+        frac = sum(v["flops"] for v in mm) / (sum(v["ms"] for v in mm) * 1e-3) / 1e12 / MFMA_FP32_PEAK_TFLOPS
+        out.update(metric=f"MASt3R {args.workload} forward time, fp32", value=round(sec * 1e3, 4),
+                   unit="ms", higher_is_better=False, ms_per_step=round(sec * 1e3, 4),
+                   config={"workload": what},
+                   achieved_tflops=round(gflop / sec / 1e3, 2),
+                   gemm_attn_frac_mfma_peak=round(frac, 4), kernels=_kernel_rates(prof, 1))
+        return out
+    if args.workload == "cpu":
+        return cpu_table()
     if args.workload == "ref512":
         B = args.pairs or 32
         cfg = G.ref512_config()
@@ -209,7 +298,11 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--per-shape", action="store_true",
                     help="also print a per-shape kernel table (stderr) from a separate step")
-    ap.add_argument("--workload", default="pair", choices=["pair", "frames", "ref512", "checkpoint"])
+    ap.add_argument("--workload", default="pair",
+                    choices=["pair", "frames", "ref512", "checkpoint", "block", "encoder", "cpu"])
+    ap.add_argument("--e2e", action="store_true",
+                    help="pair workload: include the host->device image copies and the "
+                         "device->host output copies (pinned host buffers) in the timed step")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run 3 plain device-to-device copies of MIB MiB (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
@@ -257,6 +350,17 @@ def main():
 
     def step():
         m.pair(img1, img2, B, *outs, stream=stream)
+
+    if args.e2e:  # pinned host images in, pinned host outputs back, every step
+        h_img = [img1.cpu().pin_memory(), img2.cpu().pin_memory()]
+        h_out = [torch.empty(o.shape, pin_memory=True) for o in outs]
+
+        def step():  # noqa: F811
+            img1.copy_(h_img[0], non_blocking=True)
+            img2.copy_(h_img[1], non_blocking=True)
+            m.pair(img1, img2, B, *outs, stream=stream)
+            for h, d in zip(h_out, outs):
+                h.copy_(d, non_blocking=True)
 
     for _ in range(args.warmup):
         step()
@@ -338,7 +442,9 @@ def main():
                                f"MASt3R two-view inference (ViT-L encoder x2 views, ViT-B "
                                f"decoder, 2 DPT heads, 2 local-feature heads)",
                    "pairs_per_step": B, "img": [3, H, W], "parallelism": "single GPU",
-                   "launch": "hipGraph replay" if args.graph else "eager stream"},
+                   "launch": "hipGraph replay" if args.graph else "eager stream",
+                   "timed": "H2D images + pair + D2H outputs (PCIe-inclusive, not the "
+                            "headline)" if args.e2e else "device-resident inputs and outputs"},
         "gemm_attn_frac_mfma_peak": round(mfma_fl / (mfma_ms * 1e-3) / 1e12 / peak, 4),
         "kernel_share_of_step": round(sum(v["ms"] for v in prof.values()) / ms, 4),
         "roofline": roof,

@@ -29,15 +29,21 @@ constexpr int QT = 128;  // queries per workgroup
 constexpr int KT = 64;   // keys per LDS tile
 constexpr int HD = 64;
 
+// SPLIT: workgroup (query tile, key range) = (blockIdx.x / kv_split,
+// blockIdx.x % kv_split) processes keys [range * kv_chunk, + kv_chunk) and
+// writes its unnormalised output with the running max and sum to the
+// scratch; attn_merge_kernel combines the ranges.
+template <bool SPLIT>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32_t Bcount) {
+  constexpr int NW = 4, KTT = KT, KP = KTT / (4 * NW);  // K/V fx4 loads per thread per tile
   const int grp = blockIdx.z / Bcount;
   const int b = blockIdx.z - grp * Bcount;
   const AttnArgs& p = batch.g[grp];
   const int head = blockIdx.y;
   const int Nq = p.Nq, Nkv = p.Nkv;
 
-  __shared__ __attribute__((aligned(16))) float Ks[KT][HD + 4];
-  __shared__ __attribute__((aligned(16))) float Vs[KT][HD];
+  __shared__ __attribute__((aligned(16))) float Ks[KTT][HD + 4];
+  __shared__ __attribute__((aligned(16))) float Vs[KTT][HD];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -48,7 +54,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
   const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)head * p.v_sh;
   float* ob = p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh;
 
-  const int q0 = blockIdx.x * QT + wave * 32;
+  const int ns = SPLIT ? batch.kv_split : 1;
+  const int qtile = SPLIT ? blockIdx.x / ns : blockIdx.x;
+  const int krange = SPLIT ? blockIdx.x - qtile * ns : 0;
+  const int kbeg = SPLIT ? krange * batch.kv_chunk : 0;
+  const int kend = SPLIT ? min(kbeg + batch.kv_chunk, Nkv) : Nkv;
+  const int q0 = qtile * (32 * NW) + wave * 32;
   // Q fragment: lane holds q[query l32][32*hl .. 32*hl+31], pre-scaled so the
   // softmax runs in base 2: exp(s - m) == exp2(s*log2e - m*log2e).
   const float qscale = p.scale * 1.4426950408889634f;
@@ -69,15 +80,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
   floatx16 o0 = {}, o1 = {};
   float m_run = -INFINITY, l_run = 0.f;
 
-  // Tile load assignment: key rows tid/16 + 16*i, fx4 column tid%16.
+  // Tile load assignment: key rows tid/16 + 4*NW*i, fx4 column tid%16.
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
-  fx4 rk[4], rv[4];
+  fx4 rk[KP], rv[KP];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
   auto load_kv = [&](int kbase) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = kbase + lrow + 16 * i;
-      if (key < Nkv) {
+    for (int i = 0; i < KP; ++i) {
+      const int key = kbase + lrow + 4 * NW * i;
+      if (key < kend) {
         rk[i] = *(const fx4*)(kb + (int64_t)key * p.k_sn + lc4);
         rv[i] = *(const fx4*)(vb + (int64_t)key * p.v_sn + lc4);
       } else {
@@ -87,21 +98,21 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
     }
   };
 
-  load_kv(0);
-  for (int kbase = 0; kbase < Nkv; kbase += KT) {
+  load_kv(kbeg);
+  for (int kbase = kbeg; kbase < kend; kbase += KTT) {
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      *(fx4*)&Ks[lrow + 16 * i][lc4] = rk[i];
-      *(fx4*)&Vs[lrow + 16 * i][lc4] = rv[i];
+    for (int i = 0; i < KP; ++i) {
+      *(fx4*)&Ks[lrow + 4 * NW * i][lc4] = rk[i];
+      *(fx4*)&Vs[lrow + 4 * NW * i][lc4] = rv[i];
     }
     __syncthreads();
-    if (kbase + KT < Nkv) load_kv(kbase + KT);
+    if (kbase + KTT < kend) load_kv(kbase + KTT);
 
 #pragma unroll
-    for (int sub = 0; sub < KT / 32; ++sub) {
+    for (int sub = 0; sub < KTT / 32; ++sub) {
       const int sb = kbase + sub * 32;
-      if (sb >= Nkv) break;
+      if (sb >= kend) break;
       // S^T block: A = K rows (key l32, k = 32*hl + t), B = Q^T.
       floatx16 s = {};
       const float* kr = &Ks[sub * 32 + l32][hl * 32];
@@ -113,11 +124,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.z, qf[4 * t + 2], s, 0, 0, 0);
         s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf.w, qf[4 * t + 3], s, 0, 0, 0);
       }
-      if (sb + 32 > Nkv) {
+      if (sb + 32 > kend) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int key = sb + 8 * (r >> 2) + 4 * hl + (r & 3);
-          if (key >= Nkv) s[r] = -INFINITY;
+          if (key >= kend) s[r] = -INFINITY;
         }
       }
       float mb = s[0];
@@ -152,8 +163,27 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
   }
 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = 1.0f / l_tot;
   const int q = q0 + l32;
+  if (SPLIT) {
+    if (q < Nq) {
+      const int64_t slot =
+          (((int64_t)(grp * Bcount + b) * p.H + head) * Nq + q) * ns + krange;
+      float* po = batch.part_ws + slot * 64;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        *(fx4*)(po + 8 * g + 4 * hl) = mk4(o0[4 * g], o0[4 * g + 1], o0[4 * g + 2], o0[4 * g + 3]);
+        *(fx4*)(po + 32 + 8 * g + 4 * hl) =
+            mk4(o1[4 * g], o1[4 * g + 1], o1[4 * g + 2], o1[4 * g + 3]);
+      }
+      if (hl == 0) {
+        float* pml = batch.part_ws + batch.part_ws_elems - 2 * (slot + 1);
+        pml[0] = m_run;
+        pml[1] = l_tot;
+      }
+    }
+    return;
+  }
+  const float inv = 1.0f / l_tot;
   if (q < Nq) {
     float* orow = ob + (int64_t)q * p.o_sn;
     // O^T layout: lane holds hd 8*g + 4*hl + {0..3} (+32 for o1) of query l32.
@@ -169,6 +199,41 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
   }
 }
 
+
+// Merge of the key ranges of one (image, head, query): with M = max of the
+// ranges' running maxima (base 2), O = sum_r O_r 2^(m_r - M) and
+// l = sum_r l_r 2^(m_r - M) in range order, out = O / l. One thread per 4
+// output dims.
+__global__ __launch_bounds__(256) void attn_merge_kernel(AttnBatch batch, int32_t Bcount) {
+  const AttnArgs& p0 = batch.g[0];
+  const int ns = batch.kv_split, H = p0.H, Nq = p0.Nq;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t total = (int64_t)batch.ngroups * Bcount * H * Nq * 16;
+  if (i >= total) return;
+  const int d4 = (int)(i & 15) * 4;
+  const int64_t uq = i >> 4;  // (unit, query)
+  const int q = (int)(uq % Nq);
+  const int64_t u = uq / Nq;
+  const int head = (int)(u % H);
+  const int gb = (int)(u / H);
+  const int grp = gb / Bcount, b = gb - grp * Bcount;
+  const AttnArgs& p = batch.g[grp];
+  const float* pml_end = batch.part_ws + batch.part_ws_elems;
+  float mmax = -INFINITY;
+  for (int r = 0; r < ns; ++r) mmax = fmaxf(mmax, pml_end[-2 * (uq * ns + r + 1)]);
+  float l = 0.f;
+  fx4 o = mk4(0.f, 0.f, 0.f, 0.f);
+  for (int r = 0; r < ns; ++r) {
+    const int64_t slot = uq * ns + r;
+    const float w = exp2f(pml_end[-2 * (slot + 1)] - mmax);
+    l = l + pml_end[-2 * (slot + 1) + 1] * w;
+    const fx4 v = *(const fx4*)(batch.part_ws + slot * 64 + d4);
+    o = mk4(o.x + v.x * w, o.y + v.y * w, o.z + v.z * w, o.w + v.w * w);
+  }
+  const float inv = 1.0f / l;
+  *(fx4*)(p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)q * p.o_sn + d4) =
+      mk4(o.x * inv, o.y * inv, o.z * inv, o.w * inv);
+}
 
 // bf16-input / fp32-accumulate variant (v_mfma_f32_32x32x16_bf16), softmax in
 // fp32. Q, K and V are read in fp32 and rounded to bf16 (nearest even).
@@ -351,19 +416,46 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, bool bf16) {
   }
   GS_REQUIRE(a0.B > 0 && a0.H > 0 && a0.Nq > 0 && a0.Nkv > 0, "attention: bad sizes");
   GS_REQUIRE((int64_t)a0.B * bt.ngroups <= 65535 && a0.H <= 65535, "attention: grid too large");
-  dim3 grid((a0.Nq + QT - 1) / QT, a0.H, a0.B * bt.ngroups), block(256);
+  // fp32 launches that would leave CUs idle split the keys into ranges of a
+  // multiple of 64 keys, enough ranges for 512 workgroups (two per CU).
+  AttnBatch b = bt;
+  const int64_t units = (int64_t)a0.H * a0.B * bt.ngroups;
+  const int qtiles = (a0.Nq + QT - 1) / QT;
+  b.kv_split = 1;
+  if (!bf16 && b.part_ws && units * qtiles < 512 && a0.Nkv >= 2 * KT) {
+    int want = (int)((512 + units * qtiles - 1) / (units * qtiles));
+    for (; want >= 2; --want) {
+      const int chunk = ((a0.Nkv + want - 1) / want + KT - 1) / KT * KT;
+      const int ns = (a0.Nkv + chunk - 1) / chunk;
+      if (ns >= 2 && units * a0.Nq * ns * 66 <= b.part_ws_elems) {
+        b.kv_split = ns;
+        b.kv_chunk = chunk;
+        break;
+      }
+    }
+  }
+  dim3 grid(qtiles * b.kv_split, a0.H, a0.B * bt.ngroups), block(256);
   hipEvent_t ev = prof_start(s);
-  if (bf16)
-    hipLaunchKernelGGL(attn_fwd_bf16_kernel, grid, block, 0, s, bt, a0.B);
-  else
-    hipLaunchKernelGGL(attn_fwd_kernel, grid, block, 0, s, bt, a0.B);
+  if (bf16) {
+    hipLaunchKernelGGL(attn_fwd_bf16_kernel, grid, block, 0, s, b, a0.B);
+  } else if (b.kv_split > 1) {
+    GS_REQUIRE(aligned16(b.part_ws) && b.part_ws_elems % 4 == 0,
+               "attention: scratch must be 16-byte aligned");
+    hipLaunchKernelGGL((attn_fwd_kernel<true>), grid, block, 0, s, b, a0.B);
+    const int64_t items = units * a0.Nq * 16;
+    hipLaunchKernelGGL(attn_merge_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, s,
+                       b, a0.B);
+  } else {
+    hipLaunchKernelGGL((attn_fwd_kernel<false>), grid, block, 0, s, b, a0.B);
+  }
   GS_CHECK_HIP(hipGetLastError());
   if (ev) {
     const double units = (double)a0.B * a0.H * bt.ngroups;
     std::string nm = bf16 ? "attn_fwd_bf16_kernel" : "attn_fwd_kernel";
     if (prof_per_shape())
       nm += " B=" + std::to_string(a0.B) + " H=" + std::to_string(a0.H) + " Nq=" +
-            std::to_string(a0.Nq) + " groups=" + std::to_string(bt.ngroups);
+            std::to_string(a0.Nq) + " groups=" + std::to_string(bt.ngroups) +
+            (b.kv_split > 1 ? " kvsplit=" + std::to_string(b.kv_split) : std::string());
     prof_stop(s, ev, nm.c_str(), units * 4.0 * a0.Nq * (double)a0.Nkv * 64.0,
               units * 4.0 * 64.0 * (2.0 * a0.Nq + 2.0 * a0.Nkv));
   }

@@ -15,6 +15,7 @@
 // LDS rows are padded to 36 floats so the 8 lanes of each ds_read_b128 phase
 // hit 32 distinct banks. The next K step is prefetched into registers while
 // the current one runs on the matrix cores.
+#include <algorithm>
 #include <string>
 
 #include "internal.h"
@@ -108,6 +109,74 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16&
       }
     }
   }
+}
+
+// Split-K: the raw accumulators of K range blockIdx.y go to
+// part[blockIdx.y][row][col]; gemm_splitk_reduce applies the epilogue.
+__device__ __forceinline__ void store_partial(const GemmArgs& p, const floatx16& acc00,
+                                              const floatx16& acc01, const floatx16& acc10,
+                                              const floatx16& acc11, int m0, int n0, int wm,
+                                              int wn, int l32, int hl) {
+  float* part = p.part + (int64_t)blockIdx.y * p.M * p.N;
+#pragma unroll
+  for (int bi = 0; bi < 2; ++bi) {
+#pragma unroll
+    for (int bj = 0; bj < 2; ++bj) {
+      const floatx16 c = bi == 0 ? (bj == 0 ? acc00 : acc01) : (bj == 0 ? acc10 : acc11);
+      const int col = n0 + wn * 64 + bj * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = m0 + wm * 64 + bi * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+        if (row < p.M && col < p.N) part[(int64_t)row * p.N + col] = c[r];
+      }
+    }
+  }
+}
+
+// Sum of the ksplit partials in split order, then the epilogue of
+// gemm_epilogue in the same operation order (bias, RoPE, GELU / ReLU,
+// residuals, store, dual store). One thread per 4 consecutive columns; RoPE
+// reads the partner columns (col ^ 16) the same way. N % 4 == 0, no scatter.
+__device__ __forceinline__ fx4 splitk_sum(const GemmArgs& p, int S, int64_t off) {
+  const int64_t plane = (int64_t)p.M * p.N;
+  fx4 v = *(const fx4*)(p.part + off);
+  for (int s = 1; s < S; ++s) v = v + *(const fx4*)(p.part + s * plane + off);
+  return v;
+}
+
+__global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int nq = p.N >> 2;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)p.M * nq) return;
+  const int row = (int)(i / nq), c0 = (int)(i - (int64_t)row * nq) * 4;
+  const int S = batch.ksplit, flags = p.flags;
+  fx4 v = splitk_sum(p, S, (int64_t)row * p.N + c0);
+  if (flags & EPI_BIAS) v = v + *(const fx4*)(p.bias + c0);
+  const int cblk = c0 & ~31;
+  if ((flags & EPI_ROPE) && cblk < p.rope_ncols) {
+    const int cp = c0 ^ 16;
+    fx4 w = splitk_sum(p, S, (int64_t)row * p.N + cp);
+    if (flags & EPI_BIAS) w = w + *(const fx4*)(p.bias + cp);
+    const int tok = row % p.tok_per_img;
+    const int ty = tok / p.grid_w, tx = tok - ty * p.grid_w;
+    const int pos = ((cblk >> 5) & 1) ? tx : ty;
+    const bool first = (c0 & 31) < 16;
+    float out[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int f = (c0 + u) & 15;
+      const float cs = p.rope_cos[pos * 16 + f], sn = p.rope_sin[pos * 16 + f];
+      out[u] = first ? (v[u] * cs - w[u] * sn) : (v[u] * cs + w[u] * sn);
+    }
+    v = mk4(out[0], out[1], out[2], out[3]);
+  }
+  if (flags & EPI_GELU) v = mk4(gelu_tanh(v.x), gelu_tanh(v.y), gelu_tanh(v.z), gelu_tanh(v.w));
+  if (flags & EPI_RELU) v = relu4(v);
+  if (flags & EPI_RES1) v = v + *(const fx4*)(p.R1 + (int64_t)row * p.ldr1 + c0);
+  if (flags & EPI_RES2) v = *(const fx4*)(p.R2 + (int64_t)row * p.ldr2 + c0) + v;
+  *(fx4*)(p.C + (int64_t)row * p.ldc + c0) = v;
+  if (flags & EPI_DUAL) *(fx4*)(p.C2 + (int64_t)row * p.ldc + c0) = v;
 }
 
 // Global loads of one K step into registers (macros rather than lambdas so the
@@ -243,9 +312,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
 
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
 
-  GS_LOAD_A(0)
-  GS_LOAD_B_F32(0)
-  for (int k0 = 0; k0 < K; k0 += BK) {
+  // split-K: this workgroup's contiguous K range (the whole K when ksplit == 1)
+  const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
+  GS_LOAD_A(kbeg)
+  GS_LOAD_B_F32(kbeg)
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -264,8 +335,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
     __syncthreads();
     // Prefetch the next K step (the last iteration reloads its own step:
     // in bounds, and the values are never stored).
-    GS_LOAD_A(min(k0 + BK, K - BK))
-    GS_LOAD_B_F32(min(k0 + BK, K - BK))
+    GS_LOAD_A(min(k0 + BK, kend - BK))
+    GS_LOAD_B_F32(min(k0 + BK, kend - BK))
     const float* a0p = &As[wm * 64 + l32][hl * 16];
     const float* a1p = &As[wm * 64 + 32 + l32][hl * 16];
     const float* b0p = &Bs[wn * 64 + l32][hl * 16];
@@ -289,7 +360,10 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
     }
   }
 
-  gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+  if (batch.ksplit > 1)
+    store_partial(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+  else
+    gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
 }
 
 
@@ -346,9 +420,10 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
     rbh[j] = bok[j] ? w : zero8;                                                 \
   }
 
-  GS_LOAD_A(0)
-  GS_LOAD_B_BF16(0)
-  for (int k0 = 0; k0 < K; k0 += BK) {
+  const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
+  GS_LOAD_A(kbeg)
+  GS_LOAD_B_BF16(kbeg)
+  for (int k0 = kbeg; k0 < kend; k0 += BK) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -362,8 +437,8 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) *(bf16x8*)&Bs[brow + 64 * j][bc8] = rbh[j];
     __syncthreads();
-    GS_LOAD_A(min(k0 + BK, K - BK))
-    GS_LOAD_B_BF16(min(k0 + BK, K - BK))
+    GS_LOAD_A(min(k0 + BK, kend - BK))
+    GS_LOAD_B_BF16(min(k0 + BK, kend - BK))
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl) {
       const int kc = sl * 16 + hl * 8;
@@ -378,7 +453,10 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
     }
   }
 #undef GS_LOAD_B_BF16
-  gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+  if (batch.ksplit > 1)
+    store_partial(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+  else
+    gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
 }
 
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
@@ -390,6 +468,7 @@ std::string gemm_prof_name(const char* base, const GemmBatch& b) {
     n += " M=" + std::to_string(g.M) + " N=" + std::to_string(g.N) + " K=" + std::to_string(g.K) +
          " groups=" + std::to_string(b.ngroups);
     if (g.flags & EPI_GELU) n += " gelu";
+    if (b.ksplit > 1) n += " splitk=" + std::to_string(b.ksplit);
   }
   return n;
 }
@@ -438,9 +517,43 @@ int check_gemm(const GemmArgs& a, int aload, int blayout) {
   return 0;
 }
 
-int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
+namespace {
+
+// Split factor for a launch that would leave CUs idle: the smallest divisor S
+// of the K-step count (at least 4 K steps per range, S <= 16) that gives 512
+// workgroups (two per CU), else the largest such divisor; 1 when the launch
+// already fills the GPU, when there is no scratch, or for scatter epilogues.
+int plan_ksplit(const GemmBatch& b, int max_tiles) {
+  if (!b.part_ws) return 1;
+  const GemmArgs& g0 = b.g[0];
+  for (int i = 0; i < b.ngroups; ++i) {
+    const GemmArgs& g = b.g[i];
+    if (g.M != g0.M || g.N != g0.N || g.K != g0.K) return 1;
+    if ((g.flags & EPI_SCATTER) || g.N % 4 || g.ldc % 4 || !aligned16(g.C)) return 1;
+    if ((g.flags & EPI_BIAS) && !aligned16(g.bias)) return 1;
+    if ((g.flags & EPI_RES1) && (g.ldr1 % 4 || !aligned16(g.R1))) return 1;
+    if ((g.flags & EPI_RES2) && (g.ldr2 % 4 || !aligned16(g.R2))) return 1;
+    if ((g.flags & EPI_DUAL) && !aligned16(g.C2)) return 1;
+  }
+  const int tiles = max_tiles * b.ngroups;
+  if (tiles >= 512) return 1;
+  const int steps = g0.K / BK;
+  int best = 1;
+  for (int cand = 2; cand <= 16; ++cand) {
+    if (steps % cand || steps / cand < 4) continue;
+    if ((int64_t)cand * g0.M * g0.N * b.ngroups > b.part_ws_elems) continue;
+    best = cand;
+    if (tiles * cand >= 512) break;
+  }
+  return best;
+}
+
+}  // namespace
+
+int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
                 hipStream_t s, bool bf16) {
-  GS_REQUIRE(b.ngroups >= 1 && b.ngroups <= kMaxGroups, "gemm: bad group count");
+  GS_REQUIRE(b_in.ngroups >= 1 && b_in.ngroups <= kMaxGroups, "gemm: bad group count");
+  GemmBatch b = b_in;
   int max_tiles = 0;
   for (int i = 0; i < b.ngroups; ++i) {
     int rc = check_gemm(b.g[i], aload, blayout);
@@ -452,7 +565,17 @@ int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
     max_tiles = t > max_tiles ? t : max_tiles;
   }
   if (max_tiles == 0) return 0;
-  dim3 grid(max_tiles, 1, b.ngroups), block(256);
+  b.ksplit = plan_ksplit(b, max_tiles);
+  int64_t reduce_items = 0;
+  if (b.ksplit > 1) {
+    GS_REQUIRE(aligned16(b.part_ws), "gemm: split-K scratch must be 16-byte aligned");
+    for (int i = 0; i < b.ngroups; ++i) {
+      b.g[i].part = b.part_ws + (int64_t)i * b.ksplit * b.g[0].M * b.g[0].N;
+      reduce_items = std::max(reduce_items, (int64_t)b.g[i].M * (b.g[i].N / 4));
+    }
+  }
+  dim3 grid(max_tiles, b.ksplit, b.ngroups), block(256);
+  const dim3 rgrid((unsigned)((reduce_items + 255) / 256), 1, b.ngroups);
   double flops = 0.0, bytes = 0.0;
   if (prof_on())
     for (int i = 0; i < b.ngroups; ++i) {
@@ -464,6 +587,8 @@ int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
   if (bf16 && aload == AL && a_relu == RL) {                                  \
     hipEvent_t ev = prof_start(s);                                            \
     hipLaunchKernelGGL((gemm_bf16_kernel<AL, RL>), grid, block, 0, s, b);     \
+    if (b.ksplit > 1)                                                         \
+      hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
     GS_CHECK_HIP(hipGetLastError());                                          \
     if (ev) prof_stop(s, ev, gemm_prof_name("gemm_bf16_kernel<" #AL "," #RL ">", b).c_str(), \
                       flops, bytes);                                          \
@@ -478,6 +603,8 @@ int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
   if (!bf16 && aload == AL && blayout == BL && a_relu == RL) {                \
     hipEvent_t ev = prof_start(s);                                            \
     hipLaunchKernelGGL((gemm_f32_kernel<AL, BL, RL>), grid, block, 0, s, b);  \
+    if (b.ksplit > 1)                                                         \
+      hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
     GS_CHECK_HIP(hipGetLastError());                                          \
     if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_kernel<" #AL "," #BL "," #RL ">", b).c_str(), \
                       flops, bytes);                                          \

@@ -99,12 +99,21 @@ struct GemmArgs {
   // n = (i*sc_r + j)*sc_C + c -> C[((img*sc_gh*sc_r + y*sc_r + i)*sc_gw*sc_r
   // + x*sc_r + j)*sc_C + c]; columns with c >= sc_Cout are dropped.
   int32_t sc_r, sc_C, sc_gh, sc_gw, sc_Cout;
+  // split-K partials [ksplit][M][N] of this group (set by launch_gemm)
+  float* part;
 };
 
 constexpr int kMaxGroups = 2;
 struct GemmBatch {
   GemmArgs g[kMaxGroups];
   int32_t ngroups;
+  // Optional split-K scratch (floats). When it is given and the launch would
+  // leave most CUs idle, launch_gemm splits K into ksplit contiguous ranges
+  // whose partial tiles a second kernel sums in a fixed order (so results are
+  // deterministic) before the epilogue; ksplit is chosen by launch_gemm.
+  float* part_ws = nullptr;
+  int64_t part_ws_elems = 0;
+  int32_t ksplit = 1;
 };
 
 // Launch a grouped GEMM (all groups must share the loader / layout kinds).
@@ -126,6 +135,13 @@ struct AttnArgs {
 struct AttnBatch {
   AttnArgs g[kMaxGroups];
   int32_t ngroups;
+  // Optional scratch (floats). When it is given and the launch would leave
+  // most CUs idle, launch_attention splits the keys into kv_split ranges of
+  // kv_chunk keys; a second kernel merges the ranges' softmax states in range
+  // order (deterministic). kv_split / kv_chunk are chosen by launch_attention.
+  float* part_ws = nullptr;
+  int64_t part_ws_elems = 0;
+  int32_t kv_split = 1, kv_chunk = 0;
 };
 int launch_attention(const AttnBatch& b, hipStream_t s, bool bf16 = false);
 

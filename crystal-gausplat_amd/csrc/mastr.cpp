@@ -177,6 +177,7 @@ struct Ctx {
   // workspaces
   float *P, *x, *h, *qkv, *att, *mlp, *enc, *d, *ym, *kv, *q, *hook1, *hook2, *dfin;
   float* dmem;  // composite 1: decoder_embed output, the fixed cross-attention memory
+  float* splitk;  // split-K partial tiles of small GEMM launches (kSplitkElems floats)
   // DPT / descriptor workspaces, one slot per head of a grouped launch
   float *t0[2], *act[2][4], *L[2][4], *u[2], *s[2], *t[2], *up[2], *rA[2], *rB[2], *hd0[2],
       *hup[2], *hd2[2], *lf[2];
@@ -195,6 +196,10 @@ struct Ctx {
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Split-K scratch per context: 64 MB covers the partial tiles of every launch
+// that leaves CUs idle at one pair (launch_gemm lowers the split otherwise).
+constexpr int64_t kSplitkElems = (int64_t)16 << 20;
 
 GemmArgs blank() {
   GemmArgs a;
@@ -238,7 +243,16 @@ int gemm(const Ctx& c, GemmBatch& b, int aload, bool relu_in, hipStream_t s) {
       GS_REQUIRE(w >= c.warena && w < c.warena + c.warena_size, "gemm: weight outside the arena");
       b.g[i].Bh = c.wbf16 + (w - c.warena) / 2;
     }
+  b.part_ws = c.splitk;
+  b.part_ws_elems = kSplitkElems;
   return launch_gemm(b, aload, B_NT, relu_in, s, bf);
+}
+
+// All context attention launches go through here (scratch for key splits).
+int attention(const Ctx& c, AttnBatch& ab, hipStream_t s) {
+  ab.part_ws = c.splitk;
+  ab.part_ws_elems = kSplitkElems;
+  return launch_attention(ab, s, c.cfg.precision == 1);
 }
 
 int run1(const Ctx& c, const GemmArgs& a, int aload, hipStream_t s, bool relu_in = false) {
@@ -349,7 +363,7 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   ab.g[0] = attn_args(c.qkv, 3 * D, c.qkv + D, 3 * D, c.qkv + 2 * D, 3 * D, c.att, D,
                       (int)(M / c.N), H, c.N);
   ab.ngroups = 1;
-  RC(launch_attention(ab, s, c.cfg.precision == 1));
+  RC(attention(c, ab, s));
   RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s));
   RC(layernorm1(x, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias"), c.h, M, D, f.ln_eps, s));
   RC(linear_mode(c, p + ".mlp.fc1", c.h, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D, EPI_GELU, s));
@@ -438,7 +452,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
         ab.g[k] = attn_args(qkvc[k], 3 * D, qkvc[k] + D, 3 * D, qkvc[k] + 2 * D, 3 * D, ac[k], D, B,
                             H, c.N);
       ab.ngroups = 2;
-      RC(launch_attention(ab, s, c.cfg.precision == 1));
+      RC(attention(c, ab, s));
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(ac[k], D, W(c, p[k] + ".attn.proj.weight"), W(c, p[k] + ".attn.proj.bias"),
                    dc[k], D, Mv, D, D, EPI_RES1);
@@ -461,7 +475,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       for (int k = 0; k < 2; ++k)
         ab.g[k] = attn_args(qc[k], D, kvc[k], 2 * D, kvc[k] + D, 2 * D, ac[k], D, B, H, c.N);
       ab.ngroups = 2;
-      RC(launch_attention(ab, s, c.cfg.precision == 1));
+      RC(attention(c, ab, s));
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(ac[k], D, W(c, p[k] + ".cross_attn.proj.weight"),
                    W(c, p[k] + ".cross_attn.proj.bias"), dc[k], D, Mv, D, D, EPI_RES1);
@@ -903,6 +917,7 @@ int build_workspace(Ctx& c) {
       {&c.hook2, M * Dd},
       {&c.dfin, M * Dd},
       {&c.dmem, f.composite == 1 ? M * Dd : 0},
+      {&c.splitk, kSplitkElems},
       {&c.rope_cos, 512 * 16},
       {&c.rope_sin, 512 * 16},
       {&c.ref_cos, 512 * (De / f.enc_heads / 2)},

@@ -107,9 +107,29 @@ def test_tiny_pair_parity_and_taps(tiny_cfg):
     m.close()
 
 
+def test_ragged_grid_split_paths(tiny_cfg):
+    """A 12x26 patch grid (312 tokens) at one pair: the small launches split K
+    (GEMMs) and the key range (attention, last range ragged: 312 = 4 x 64 + 56)
+    and must still match the oracle."""
+    case("ragged grid 192x416 split paths")
+    cfg = G.default_config(**dict(tiny_cfg, img_h=192, img_w=416))
+    w = weights_for(cfg, 0, bias_std=0.02, ln_std=0.1)
+    n = 3 * cfg.img_h * cfg.img_w
+    i1 = G.seed_uniform(4, "view1", n).reshape(1, 3, cfg.img_h, cfg.img_w)
+    i2 = G.seed_uniform(4, "view2", n).reshape(1, 3, cfg.img_h, cfg.img_w)
+    m = load_ctx(cfg, w, max_pairs=1)
+    got = run_pair(m, cfg, i1, i2, 1)
+    check_pair(got, O.mastr_pair(cfg.as_dict(), w, i1, i2), "ragged")
+    again = run_pair(m, cfg, i1, i2, 1)
+    for k in got:  # fixed-order merges: deterministic
+        np.testing.assert_array_equal(got[k], again[k])
+    m.close()
+
+
 def test_tiny_batch_invariance_and_determinism(tiny_cfg):
-    """Pair p of a batch equals the same pair run alone, bit for bit, and a
-    rerun is bit-identical (no split reductions, no atomics)."""
+    """Pair p of a batch equals the same pair run alone, bit for bit (at this
+    size both batch sizes use the same K split of every GEMM), and a rerun
+    is bit-identical (fixed-order reductions, no atomics)."""
     case("tiny batch invariance")
     cfg = G.default_config(**tiny_cfg)
     B = 3
@@ -151,7 +171,7 @@ def test_config2_full_pair():
 def test_config4_grid_pair():
     """Config 4 geometry: 512x512 images (32x32 grid, 1024 tokens), full model,
     one pair against the oracle; the batched 32-pair run is covered by batch
-    invariance (bit-exact) below."""
+    invariance below."""
     case("config4 512x512 pair")
     cfg = G.default_config(img_h=512, img_w=512)
     w = weights_for(cfg)
@@ -171,7 +191,10 @@ def test_config4_grid_pair():
 
 def test_config4_batch_invariance_32_pairs():
     """32 pairs at 512x512 in one launch sequence: pairs 0 and 31 equal the
-    same pairs run alone, bit for bit."""
+    same pairs run alone. A single pair leaves CUs idle, so its small GEMMs
+    split K (a different fp32 summation order), hence the parity tolerance
+    rather than bit equality (measured: <= 2.1e-5 abs on desc, 2.4e-7 on
+    conf)."""
     case("config4 32-pair batch invariance")
     cfg = G.default_config(img_h=512, img_w=512)
     B = 32
@@ -184,7 +207,8 @@ def test_config4_batch_invariance_32_pairs():
     for b in (0, B - 1):
         one = run_pair(m, cfg, i1[b:b + 1], i2[b:b + 1], 1)
         for k in full:
-            np.testing.assert_array_equal(one[k][0], full[k][b], err_msg=f"{k} pair {b}")
+            err = assert_close(one[k][0], full[k][b], name=f"{k} pair {b}")
+            print(f"pair {b} {k}: max abs diff single vs batched {err:.2e}")
     m.close()
 
 
