@@ -520,30 +520,40 @@ int check_gemm(const GemmArgs& a, int aload, int blayout) {
 namespace {
 
 // Split factor for a launch that would leave CUs idle: the smallest divisor S
-// of the K-step count (at least 4 K steps per range, S <= 16) that gives 512
-// workgroups (two per CU), else the largest such divisor; 1 when the launch
-// already fills the GPU, when there is no scratch, or for scatter epilogues.
-int plan_ksplit(const GemmBatch& b, int max_tiles) {
-  if (!b.part_ws) return 1;
+// of the K-step count (at least 4 K steps per range, S <= 16) that gives
+// kSplitTarget workgroups, else the largest such divisor; 1 when the launch
+// already has that many tiles, when there is no scratch, or for scatter
+// epilogues. kSplitTarget (~1.7 workgroups per CU) is measured: over the
+// one-image / one-pair encoder and decoder shapes (M 768..1536, N 768..4096,
+// K 768..4096) the fastest split was the smallest giving >= 432 workgroups.
+constexpr int kSplitTarget = 432;
+bool splitk_eligible(const GemmBatch& b) {
+  if (!b.part_ws || !aligned16(b.part_ws)) return false;
   const GemmArgs& g0 = b.g[0];
   for (int i = 0; i < b.ngroups; ++i) {
     const GemmArgs& g = b.g[i];
-    if (g.M != g0.M || g.N != g0.N || g.K != g0.K) return 1;
-    if ((g.flags & EPI_SCATTER) || g.N % 4 || g.ldc % 4 || !aligned16(g.C)) return 1;
-    if ((g.flags & EPI_BIAS) && !aligned16(g.bias)) return 1;
-    if ((g.flags & EPI_RES1) && (g.ldr1 % 4 || !aligned16(g.R1))) return 1;
-    if ((g.flags & EPI_RES2) && (g.ldr2 % 4 || !aligned16(g.R2))) return 1;
-    if ((g.flags & EPI_DUAL) && !aligned16(g.C2)) return 1;
+    if (g.M != g0.M || g.N != g0.N || g.K != g0.K) return false;
+    if ((g.flags & EPI_SCATTER) || g.N % 4 || g.ldc % 4 || !aligned16(g.C)) return false;
+    if ((g.flags & EPI_BIAS) && !aligned16(g.bias)) return false;
+    if ((g.flags & EPI_RES1) && (g.ldr1 % 4 || !aligned16(g.R1))) return false;
+    if ((g.flags & EPI_RES2) && (g.ldr2 % 4 || !aligned16(g.R2))) return false;
+    if ((g.flags & EPI_DUAL) && !aligned16(g.C2)) return false;
   }
+  return true;
+}
+
+int plan_ksplit(const GemmBatch& b, int max_tiles) {
+  if (!splitk_eligible(b)) return 1;
+  const GemmArgs& g0 = b.g[0];
   const int tiles = max_tiles * b.ngroups;
-  if (tiles >= 512) return 1;
+  if (tiles >= kSplitTarget) return 1;
   const int steps = g0.K / BK;
   int best = 1;
   for (int cand = 2; cand <= 16; ++cand) {
     if (steps % cand || steps / cand < 4) continue;
     if ((int64_t)cand * g0.M * g0.N * b.ngroups > b.part_ws_elems) continue;
     best = cand;
-    if (tiles * cand >= 512) break;
+    if (tiles * cand >= kSplitTarget) break;
   }
   return best;
 }
@@ -565,7 +575,14 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     max_tiles = t > max_tiles ? t : max_tiles;
   }
   if (max_tiles == 0) return 0;
-  b.ksplit = plan_ksplit(b, max_tiles);
+  if (b.ksplit > 1) {  // requested split
+    GS_REQUIRE(splitk_eligible(b), "gemm: this launch cannot split K");
+    GS_REQUIRE((b.g[0].K / BK) % b.ksplit == 0 &&
+                   (int64_t)b.ksplit * b.g[0].M * b.g[0].N * b.ngroups <= b.part_ws_elems,
+               "gemm: requested split-K must divide the K steps and fit the scratch");
+  } else {
+    b.ksplit = plan_ksplit(b, max_tiles);
+  }
   int64_t reduce_items = 0;
   if (b.ksplit > 1) {
     GS_REQUIRE(aligned16(b.part_ws), "gemm: split-K scratch must be 16-byte aligned");

@@ -110,10 +110,10 @@ struct GemmBatch {
   // Optional split-K scratch (floats). When it is given and the launch would
   // leave most CUs idle, launch_gemm splits K into ksplit contiguous ranges
   // whose partial tiles a second kernel sums in a fixed order (so results are
-  // deterministic) before the epilogue; ksplit is chosen by launch_gemm.
+  // deterministic) before the epilogue.
   float* part_ws = nullptr;
   int64_t part_ws_elems = 0;
-  int32_t ksplit = 1;
+  int32_t ksplit = 0;  // 0: chosen by launch_gemm; > 0: requested split (validated)
 };
 
 // Launch a grouped GEMM (all groups must share the loader / layout kinds).
@@ -138,10 +138,11 @@ struct AttnBatch {
   // Optional scratch (floats). When it is given and the launch would leave
   // most CUs idle, launch_attention splits the keys into kv_split ranges of
   // kv_chunk keys; a second kernel merges the ranges' softmax states in range
-  // order (deterministic). kv_split / kv_chunk are chosen by launch_attention.
+  // order (deterministic).
   float* part_ws = nullptr;
   int64_t part_ws_elems = 0;
-  int32_t kv_split = 1, kv_chunk = 0;
+  int32_t kv_split = 0;  // 0: chosen by launch_attention; > 0: requested ranges
+  int32_t kv_chunk = 0;
 };
 int launch_attention(const AttnBatch& b, hipStream_t s, bool bf16 = false);
 
