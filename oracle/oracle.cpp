@@ -1019,6 +1019,16 @@ extern "C" int32_t orc_mastr_pair(const orc_config* cfg, orc_weight_fn wf,
   return 0;
 }
 
+extern "C" int32_t orc_dpt_head(const orc_config* cfg, orc_weight_fn wf, void* user,
+                                const char* prefix, const float* const hooks[4],
+                                int32_t B, int32_t gh, int32_t gw, float* pts,
+                                float* conf) {
+  if ((gh & 1) || (gw & 1)) return -1;
+  Ctx c{cfg, wf, user};
+  dpt_head(c, prefix, hooks, B, gh, gw, pts, conf);
+  return 0;
+}
+
 extern "C" int32_t orc_mastr_pair_taps(const orc_config* cfg, orc_weight_fn wf,
                                        void* user, const float* img1,
                                        const float* img2, int32_t B, float* enc1,

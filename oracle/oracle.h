@@ -146,6 +146,12 @@ int32_t orc_mastr_pair(const orc_config* cfg, orc_weight_fn wf, void* user,
                        const float* img1, const float* img2, int32_t B,
                        float* pts1, float* conf1, float* desc1, float* pts2,
                        float* conf2, float* desc2);
+/* One full DPT head (composite 0) on its four hooks: hooks[0] [B,N,enc_dim],
+ * hooks[1..3] [B,N,dec_dim] on the gh x gw grid; prefix e.g.
+ * "downstream_head1"; pts [B,H,W,3], conf [B,H,W,1] at 16x the grid. */
+int32_t orc_dpt_head(const orc_config* cfg, orc_weight_fn wf, void* user,
+                     const char* prefix, const float* const hooks[4], int32_t B,
+                     int32_t gh, int32_t gw, float* pts, float* conf);
 /* Intermediate taps for debugging the pair path (all nullable):
  * enc1/enc2 [B,N,enc_dim]; dec1/dec2 [B,N,dec_dim] = dec_norm(d^depth). */
 int32_t orc_mastr_pair_taps(const orc_config* cfg, orc_weight_fn wf,

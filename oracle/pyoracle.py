@@ -74,6 +74,8 @@ _SIGS = [
     ("orc_encoder", C.c_int32, [C.POINTER(OrcConfig), WEIGHT_FN, vp, vp, C.c_int32, vp]),
     ("orc_mastr_pair", C.c_int32, [C.POINTER(OrcConfig), WEIGHT_FN, vp, vp, vp, C.c_int32, vp, vp,
                                    vp, vp, vp, vp]),
+    ("orc_dpt_head", C.c_int32, [C.POINTER(OrcConfig), WEIGHT_FN, vp, C.c_char_p, C.POINTER(vp),
+                                 C.c_int32, C.c_int32, C.c_int32, vp, vp]),
     ("orc_mastr_pair_taps", C.c_int32, [C.POINTER(OrcConfig), WEIGHT_FN, vp, vp, vp, C.c_int32,
                                         vp, vp, vp, vp]),
 ]
@@ -373,3 +375,19 @@ def mastr_pair_taps(cfgd, weights, img1, img2):
                                    _p(d1), _p(d2))
     assert rc == 0 and not W.missing, (rc, W.missing)
     return e1, e2, d1, d2
+
+
+def dpt_head(cfgd, weights, prefix, hooks, gh, gw):
+    """One full DPT head on hooks (enc [B,N,enc_dim], three [B,N,dec_dim])."""
+    cfg = config_from(cfgd)
+    W = _Weights(weights)
+    hs = [f32(h) for h in hooks]
+    B = hs[0].shape[0]
+    arr = (vp * 4)(*[h.ctypes.data_as(vp) for h in hs])
+    Hi, Wi = gh * cfgd["patch"], gw * cfgd["patch"]
+    pts = np.empty((B, Hi, Wi, 3), np.float32)
+    conf = np.empty((B, Hi, Wi, 1), np.float32)
+    rc = lib().orc_dpt_head(C.byref(cfg), W.cb, None, prefix.encode(), arr, B, gh, gw, _p(pts),
+                            _p(conf))
+    assert rc == 0 and not W.missing, (rc, W.missing)
+    return pts, conf
