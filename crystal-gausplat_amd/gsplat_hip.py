@@ -127,6 +127,13 @@ def lib():
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise RuntimeError(f"{LIB_PATH} not built: run crystal-gausplat_amd/build.py")
+        # torch carries its own HIP runtime; loading it first makes the library
+        # bind to that same runtime (one HIP runtime per process). Loaded the
+        # other way round, two runtimes coexist and the second sees no device.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         L = C.CDLL(LIB_PATH)
         for name, res, args in _SIGS:
             f = getattr(L, name)
