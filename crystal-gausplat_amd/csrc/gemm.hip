@@ -367,6 +367,138 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
 }
 
 
+// Direct-to-LDS variant of the fp32 kernel for plain / concat A and NT B:
+// global_load_lds_dwordx4 streams each K step straight into one of two LDS
+// buffers (no VGPR staging, no ds_write), so the next step's tiles are in
+// flight while the MFMAs consume the current one. LDS rows are 32 floats with
+// the 16-byte chunks XOR-swizzled by row (chunk c of row r at slot c ^ (r&7)):
+// a wave's load instruction writes 8 contiguous rows (lane -> row lane>>3,
+// slot lane&7), and the MFMA reads of 8 consecutive rows at one chunk hit 8
+// distinct slots (conflict-free). Same per-element MFMA sequence as
+// gemm_f32_kernel, so results are bit-identical to it. Synchronisation is
+// explicit: s_waitcnt vmcnt leaves the next step's 8 loads in flight, and
+// the barriers are bare s_barrier (a __syncthreads fence would also wait for
+// the prefetch).
+// LDS byte address of a __shared__ pointer.
+__device__ __forceinline__ uint32_t lds_addr(const float* ptr) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) float*)ptr;
+}
+// One wave-wide global_load_lds_dwordx4: lane l's 16 bytes at gptr land at
+// LDS byte lds + 16*l (lds is wave-uniform, passed through M0). Issued as
+// inline asm so that the compiler does not track it as an LDS store: its
+// wait insertion cannot tell the two LDS buffers apart and would otherwise
+// wait for the in-flight prefetch before every LDS read. The kernel waits
+// for these loads itself (s_waitcnt vmcnt).
+__device__ __forceinline__ void lds_dma16(const float* gptr, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds), "v"(gptr)
+               : "memory", "m0");
+}
+
+template <int ALOAD>
+__global__ __launch_bounds__(256, 2) void gemm_f32_dl_kernel(GemmBatch batch) {
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int M = p.M, N = p.N;
+  int m0, n0;
+  if (!gemm_tile(p, m0, n0)) return;
+
+  __shared__ __attribute__((aligned(16))) float As0[BM * BK];
+  __shared__ __attribute__((aligned(16))) float Bs0[BN * BK];
+  __shared__ __attribute__((aligned(16))) float As1[BM * BK];
+  __shared__ __attribute__((aligned(16))) float Bs1[BN * BK];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  // loader: wave w, instruction i fills tile rows 32w + 8i .. +7
+  const int rin = lane >> 3, chunk = (lane & 7) ^ rin;
+  const float* ag[4];
+  const float* ag2[4];
+  const float* bg[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 32 * wave + 8 * i + rin;
+    const int64_t m = min(m0 + row, M - 1), n = min(n0 + row, N - 1);
+    ag[i] = p.A + m * p.lda + 4 * chunk;
+    ag2[i] = ALOAD == A_CONCAT ? p.A2 + m * p.lda2 + 4 * chunk - p.K1 : nullptr;
+    bg[i] = p.B + n * p.ldb + 4 * chunk;
+  }
+#define GS_DL_ISSUE(BUF, K0)                                                            \
+  {                                                                                     \
+    const int k_ = (K0);                                                                \
+    const bool first_ = ALOAD != A_CONCAT || k_ < p.K1;                                 \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i)                                       \
+      lds_dma16((first_ ? ag[i] : ag2[i]) + k_, a_lds[BUF] + (32 * wave + 8 * i) * BK * 4); \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i)                                       \
+      lds_dma16(bg[i] + k_, b_lds[BUF] + (32 * wave + 8 * i) * BK * 4);                 \
+  }
+  // per-lane LDS byte offsets of the MFMA operand rows; chunk c of row r sits
+  // at slot c ^ (r & 7) and r & 7 == l32 & 7 for every operand row
+  const int swz = l32 & 7;
+  const int fa0 = (wm * 64 + l32) * BK, fa1 = fa0 + 32 * BK;
+  const int fb0 = (wn * 64 + l32) * BK, fb1 = fb0 + 32 * BK;
+  const uint32_t a_lds[2] = {lds_addr(As0), lds_addr(As1)};
+  const uint32_t b_lds[2] = {lds_addr(Bs0), lds_addr(Bs1)};
+#define GS_MFMA4(AX, BX)                                                           \
+  acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.AX, b0.BX, acc00, 0, 0, 0);     \
+  acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.AX, b1.BX, acc01, 0, 0, 0);     \
+  acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.AX, b0.BX, acc10, 0, 0, 0);     \
+  acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.AX, b1.BX, acc11, 0, 0, 0);
+#define GS_DL_COMPUTE(AS, BS)                                                           \
+  _Pragma("unroll") for (int t4 = 0; t4 < 4; ++t4) {                                    \
+    const int co = ((hl * 4 + t4) ^ swz) << 2;                                          \
+    const fx4 a0 = *(const fx4*)((AS) + fa0 + co);                                      \
+    const fx4 a1 = *(const fx4*)((AS) + fa1 + co);                                      \
+    const fx4 b0 = *(const fx4*)((BS) + fb0 + co);                                      \
+    const fx4 b1 = *(const fx4*)((BS) + fb1 + co);                                      \
+    GS_MFMA4(x, x)                                                                      \
+    GS_MFMA4(y, y)                                                                      \
+    GS_MFMA4(z, z)                                                                      \
+    GS_MFMA4(w, w)                                                                      \
+  }
+
+  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+  const int Kc = p.K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
+  int k0 = kbeg;
+  GS_DL_ISSUE(0, k0)
+  while (true) {
+    // K step k0 in buffer 0; step k0 + BK streams into buffer 1. Each wave
+    // waits for its own 8 loads of step k0, then the barrier makes every
+    // wave's loads visible; after the step every wave drains its LDS reads
+    // (lgkmcnt(0)) before the barrier that lets buffer 0 be refilled.
+    if (k0 + BK < kend) {
+      GS_DL_ISSUE(1, k0 + BK)
+      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    GS_DL_COMPUTE(As0, Bs0)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    k0 += BK;
+    if (k0 >= kend) break;
+    if (k0 + BK < kend) {
+      GS_DL_ISSUE(0, k0 + BK)
+      asm volatile("s_waitcnt vmcnt(8)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    GS_DL_COMPUTE(As1, Bs1)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    k0 += BK;
+    if (k0 >= kend) break;
+  }
+#undef GS_MFMA4
+#undef GS_DL_ISSUE
+#undef GS_DL_COMPUTE
+  if (batch.ksplit > 1)
+    store_partial(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+  else
+    gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+}
+
 // bf16-input / fp32-accumulate variant (v_mfma_f32_32x32x16_bf16): same tile,
 // loaders and epilogue as the fp32 kernel; A is read in fp32 and rounded to
 // bf16 (round-to-nearest-even) on its way into LDS, B is a bf16 copy of the
@@ -627,6 +759,26 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
                       flops, bytes);                                          \
     return 0;                                                                 \
   }
+  // long-K launches take the direct-to-LDS kernel: its double buffer (64 KB
+  // of LDS, two workgroups per CU) pays off from ~2048 K, while shorter K
+  // runs faster on the register-staged kernel at three workgroups per CU
+  // (measured per shape at config 3)
+  bool long_k = true;
+  for (int i = 0; i < b.ngroups; ++i) long_k = long_k && b.g[i].K >= 2048;
+#define GS_GEMM_DL_CASE(AL)                                                   \
+  if (!bf16 && long_k && aload == AL && blayout == B_NT && !a_relu) {         \
+    hipEvent_t ev = prof_start(s);                                            \
+    hipLaunchKernelGGL((gemm_f32_dl_kernel<AL>), grid, block, 0, s, b);       \
+    if (b.ksplit > 1)                                                         \
+      hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
+    GS_CHECK_HIP(hipGetLastError());                                          \
+    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_kernel<" #AL ",B_NT,false>", b).c_str(), \
+                      flops, bytes);                                          \
+    return 0;                                                                 \
+  }
+  GS_GEMM_DL_CASE(A_PLAIN)
+  GS_GEMM_DL_CASE(A_CONCAT)
+#undef GS_GEMM_DL_CASE
   GS_GEMM_CASE(A_PLAIN, B_NT, false)
   GS_GEMM_CASE(A_PLAIN, B_NN, false)
   GS_GEMM_CASE(A_PLAIN, B_NT, true)
