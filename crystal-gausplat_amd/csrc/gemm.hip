@@ -772,7 +772,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     if (b.ksplit > 1)                                                         \
       hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
     GS_CHECK_HIP(hipGetLastError());                                          \
-    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_kernel<" #AL ",B_NT,false>", b).c_str(), \
+    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_dl_kernel<" #AL ">", b).c_str(), \
                       flops, bytes);                                          \
     return 0;                                                                 \
   }
