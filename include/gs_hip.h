@@ -251,7 +251,11 @@ int32_t gs_mastr_weight_values(const gs_mastr_config* cfg, int32_t i,
                                float* host_out, int64_t n);
 
 /* Context: device weights (re-laid for the kernels) + workspaces for up to
- * max_pairs pairs. Weights start uninitialised. */
+ * max_pairs pairs (including a 64 MB scratch for the split-K partial tiles
+ * and key-range attention states of small launches). Weights start
+ * uninitialised. A context's calls share its workspaces: calls on one
+ * context must not overlap in time (one stream per context, or order them);
+ * separate contexts are independent. */
 int32_t gs_hip_mastr_create(const gs_mastr_config* cfg, int32_t max_pairs,
                             void** ctx_out);
 void gs_hip_mastr_destroy(void* ctx);
