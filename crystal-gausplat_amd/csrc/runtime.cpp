@@ -260,6 +260,54 @@ int32_t gs_hip_profile_entry(int32_t i, char* name, int32_t cap, int64_t* launch
   return 0;
 }
 
+int32_t gs_buffer_write_async(void* handle, const void* host, int64_t size, int64_t offset,
+                              void* stream) {
+  GS_REQUIRE(handle && host, "gs_buffer_write_async: null argument");
+  Buffer* b = (Buffer*)handle;
+  GS_REQUIRE(size >= 0 && offset >= 0 && offset + size <= b->size,
+             "gs_buffer_write_async: range exceeds the buffer");
+  if (size == 0) return 0;
+  GS_CHECK_HIP(hipMemcpyAsync((char*)b->dev + offset, host, (size_t)size, hipMemcpyHostToDevice,
+                              (hipStream_t)stream));
+  return 0;
+}
+
+int32_t gs_buffer_read_async(void* handle, void* host, int64_t size, int64_t offset,
+                             void* stream) {
+  GS_REQUIRE(handle && host, "gs_buffer_read_async: null argument");
+  Buffer* b = (Buffer*)handle;
+  GS_REQUIRE(size >= 0 && offset >= 0 && offset + size <= b->size,
+             "gs_buffer_read_async: range exceeds the buffer");
+  if (size == 0) return 0;
+  GS_CHECK_HIP(hipMemcpyAsync(host, (const char*)b->dev + offset, (size_t)size,
+                              hipMemcpyDeviceToHost, (hipStream_t)stream));
+  return 0;
+}
+
+void* gs_host_alloc(int64_t size) {
+  if (size <= 0) {
+    set_error("gs_host_alloc: size must be positive");
+    return nullptr;
+  }
+  if (ensure_device()) return nullptr;
+  void* p = nullptr;
+  if (hipHostMalloc(&p, (size_t)size, hipHostMallocDefault) != hipSuccess) {
+    set_error("gs_host_alloc: hipHostMalloc failed");
+    return nullptr;
+  }
+  return p;
+}
+
+void gs_host_free(void* ptr) {
+  if (ptr) hipHostFree(ptr);
+}
+
+int32_t gs_stream_synchronize(void* stream) {
+  if (ensure_device()) return -2;
+  GS_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+  return 0;
+}
+
 void gs_buffer_copy(void* src_handle, void* dst_handle, int64_t size) {
   if (!src_handle || !dst_handle) return;
   Buffer* s = (Buffer*)src_handle;

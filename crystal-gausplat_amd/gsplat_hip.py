@@ -53,6 +53,11 @@ _SIGS = [
     ("gs_buffer_read", None, [vp, vp, C.c_int64]),
     ("gs_buffer_sync", None, [vp]),
     ("gs_buffer_copy", None, [vp, vp, C.c_int64]),
+    ("gs_buffer_write_async", C.c_int32, [vp, vp, C.c_int64, C.c_int64, vp]),
+    ("gs_buffer_read_async", C.c_int32, [vp, vp, C.c_int64, C.c_int64, vp]),
+    ("gs_host_alloc", vp, [C.c_int64]),
+    ("gs_host_free", None, [vp]),
+    ("gs_stream_synchronize", C.c_int32, [vp]),
     ("gs_init_device", C.c_int32, []),
     ("gs_get_device", vp, []),
     ("gs_get_command_queue", vp, []),

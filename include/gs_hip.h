@@ -61,6 +61,22 @@ void gs_buffer_sync(void* handle);
 /* src/metal/bridge.mm:387. Device-to-device copy on the library stream. */
 void gs_buffer_copy(void* src_handle, void* dst_handle, int64_t size);
 
+/* Asynchronous host <-> device copies (no bridge counterpart: Metal's shared
+ * storage needed none; SURVEY's boundary adds them for explicit device
+ * memory): size bytes between host memory and the buffer at byte offset,
+ * enqueued on `stream` (NULL = HIP default stream). The host memory must stay
+ * valid until the stream reaches the copy; pinned memory from gs_host_alloc
+ * makes the copy truly asynchronous. Return 0, or -1 (bad handle / range). */
+int32_t gs_buffer_write_async(void* handle, const void* host, int64_t size,
+                              int64_t offset, void* stream);
+int32_t gs_buffer_read_async(void* handle, void* host, int64_t size,
+                             int64_t offset, void* stream);
+/* Pinned (page-locked) host memory for the async copies; NULL on failure. */
+void* gs_host_alloc(int64_t size);
+void gs_host_free(void* ptr);
+/* Wait for `stream` (NULL = HIP default stream). */
+int32_t gs_stream_synchronize(void* stream);
+
 /* src/metal/bridge.mm:392. 0 = ok, -1 = no device, -2 = stream failure. */
 int32_t gs_init_device(void);
 /* src/metal/bridge.mm:396 / 400. Opaque device handle / the hipStream_t. */

@@ -244,3 +244,33 @@ def test_buffer_api_roundtrip():
     Lb.gs_release_buffer(h1)
     Lb.gs_release_buffer(h2)
     assert Lb.gs_create_buffer(0, 0) is None
+
+
+def test_buffer_async_copies_with_pinned_memory():
+    """gs_buffer_write_async / read_async at byte offsets on a caller stream,
+    through pinned host memory from gs_host_alloc, and their range checks."""
+    case("gs_* async buffer copies")
+    Lb = L()
+    n = 4096
+    a = rnd(n)
+    hbuf = Lb.gs_host_alloc(4 * n)
+    assert hbuf
+    host = np.ctypeslib.as_array((C.c_float * n).from_address(hbuf))
+    host[:] = a
+    h = Lb.gs_create_buffer(4 * n, 0)
+    s = stream()
+    # two halves, the second at a byte offset
+    G.check(Lb.gs_buffer_write_async(h, C.c_void_p(hbuf), 2 * n, 0, s))
+    G.check(Lb.gs_buffer_write_async(h, C.c_void_p(hbuf + 2 * n), 2 * n, 2 * n, s))
+    out = np.zeros(n, np.float32)
+    G.check(Lb.gs_buffer_read_async(h, out.ctypes.data_as(C.c_void_p), 4 * n, 0, s))
+    G.check(Lb.gs_stream_synchronize(s))
+    np.testing.assert_array_equal(out, a)
+    part = np.zeros(10, np.float32)
+    G.check(Lb.gs_buffer_read_async(h, part.ctypes.data_as(C.c_void_p), 40, 400, s))
+    G.check(Lb.gs_stream_synchronize(s))
+    np.testing.assert_array_equal(part, a[100:110])
+    assert Lb.gs_buffer_write_async(h, C.c_void_p(hbuf), 8, 4 * n - 4, s) == -1
+    assert Lb.gs_buffer_read_async(h, out.ctypes.data_as(C.c_void_p), 4, -4, s) == -1
+    Lb.gs_release_buffer(h)
+    Lb.gs_host_free(hbuf)
