@@ -383,7 +383,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
   const float l_tot = l_run + __shfl_xor(l_run, 32);
   const float inv = 1.0f / l_tot;
   const int q = q0 + l32;
-  if (q < Nq) {
+  if (q < Nq && p.o_bf16) {  // bf16 output for a bf16-input projection
+    __bf16* orow = (__bf16*)p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh + (int64_t)q * p.o_sn;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const bf16x4 h0 = {(__bf16)(o0[4 * g] * inv), (__bf16)(o0[4 * g + 1] * inv),
+                         (__bf16)(o0[4 * g + 2] * inv), (__bf16)(o0[4 * g + 3] * inv)};
+      const bf16x4 h1 = {(__bf16)(o1[4 * g] * inv), (__bf16)(o1[4 * g + 1] * inv),
+                         (__bf16)(o1[4 * g + 2] * inv), (__bf16)(o1[4 * g + 3] * inv)};
+      *(bf16x4*)(orow + 8 * g + 4 * hl) = h0;
+      *(bf16x4*)(orow + 32 + 8 * g + 4 * hl) = h1;
+    }
+  } else if (q < Nq) {
     float* orow = ob + (int64_t)q * p.o_sn;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -407,6 +418,7 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, bool bf16) {
     GS_REQUIRE(a.B == a0.B && a.H == a0.H && a.Nq == a0.Nq && a.Nkv == a0.Nkv,
                "attention: grouped problems must share shapes");
     GS_REQUIRE(a.q && a.k && a.v && a.o, "attention: null operand");
+    GS_REQUIRE(!a.o_bf16 || bf16, "attention: bf16 output needs the bf16 kernel");
     GS_REQUIRE(aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o),
                "attention: operands must be 16-byte aligned");
     const int64_t st[12] = {a.q_sb, a.q_sh, a.q_sn, a.k_sb, a.k_sh, a.k_sn,
@@ -460,7 +472,7 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, bool bf16) {
             std::to_string(a0.Nq) + " groups=" + std::to_string(bt.ngroups) +
             (b.kv_split > 1 ? " kvsplit=" + std::to_string(b.kv_split) : std::string());
     prof_stop(s, ev, nm.c_str(), units * 4.0 * a0.Nq * (double)a0.Nkv * 64.0,
-              units * 4.0 * 64.0 * (2.0 * a0.Nq + 2.0 * a0.Nkv));
+              units * 64.0 * ((a0.o_bf16 ? 6.0 : 8.0) * a0.Nq + 8.0 * a0.Nkv));
   }
   return 0;
 }

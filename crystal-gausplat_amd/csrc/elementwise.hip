@@ -61,7 +61,17 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnBatch bt) {
       o.y = (v[i].y - mean) * inv * g.y + bb.y;
       o.z = (v[i].z - mean) * inv * g.z + bb.z;
       o.w = (v[i].w - mean) * inv * g.w + bb.w;
-      yr[idx] = o;
+      if (p.y_bf16) {
+        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+        bf16x4_t h;
+        h.x = (__bf16)o.x;
+        h.y = (__bf16)o.y;
+        h.z = (__bf16)o.z;
+        h.w = (__bf16)o.w;
+        ((bf16x4_t*)((__bf16*)p.y + row * D))[idx] = h;
+      } else {
+        yr[idx] = o;
+      }
     }
   }
 }
@@ -231,9 +241,12 @@ int launch_layernorm(const LnBatch& bt, hipStream_t s) {
     hipLaunchKernelGGL(layernorm_kernel<16>, grid, block, 0, s, bt);
   GS_CHECK_HIP(hipGetLastError());
   if (ev) {
-    double rows = 0;
-    for (int i = 0; i < bt.ngroups; ++i) rows += (double)bt.g[i].rows;
-    prof_stop(s, ev, "layernorm_kernel", 8.0 * rows * D, 4.0 * rows * D * 2.0 + 8.0 * D);
+    double rows = 0, bytes = 0;
+    for (int i = 0; i < bt.ngroups; ++i) {
+      rows += (double)bt.g[i].rows;
+      bytes += (bt.g[i].y_bf16 ? 6.0 : 8.0) * (double)bt.g[i].rows * D + 8.0 * D;
+    }
+    prof_stop(s, ev, "layernorm_kernel", 8.0 * rows * D, bytes);
   }
   return 0;
 }

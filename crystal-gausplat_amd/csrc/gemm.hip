@@ -101,6 +101,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16&
               const int64_t ox = (int64_t)x * p.sc_r + sc_j;
               p.C[(oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c] = v;
             }
+          } else if (flags & EPI_BF16OUT) {
+            ((__bf16*)p.C)[(int64_t)row * p.ldc + col] = (__bf16)v;
           } else {
             p.C[(int64_t)row * p.ldc + col] = v;
             if (flags & EPI_DUAL) p.C2[(int64_t)row * p.ldc + col] = v;
@@ -175,6 +177,16 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
   if (flags & EPI_RELU) v = relu4(v);
   if (flags & EPI_RES1) v = v + *(const fx4*)(p.R1 + (int64_t)row * p.ldr1 + c0);
   if (flags & EPI_RES2) v = *(const fx4*)(p.R2 + (int64_t)row * p.ldr2 + c0) + v;
+  if (flags & EPI_BF16OUT) {
+    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+    bf16x4_t h;
+    h.x = (__bf16)v.x;
+    h.y = (__bf16)v.y;
+    h.z = (__bf16)v.z;
+    h.w = (__bf16)v.w;
+    *(bf16x4_t*)((__bf16*)p.C + (int64_t)row * p.ldc + c0) = h;
+    return;
+  }
   *(fx4*)(p.C + (int64_t)row * p.ldc + c0) = v;
   if (flags & EPI_DUAL) *(fx4*)(p.C2 + (int64_t)row * p.ldc + c0) = v;
 }
@@ -540,12 +552,23 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   }
 
   fx4 ra[4];
+  bf16x4 rah[4];  // A_PLAIN_H: bf16 A rows, stored to LDS as loaded
   bf16x8 rbh[2];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
   const bf16x8 zero8 = {};
 
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
 
+#define GS_LOAD_AH(K0)                                                           \
+  if (ALOAD == A_PLAIN_H) {                                                      \
+    const __bf16* Ah = (const __bf16*)p.A;                                       \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                              \
+      const bf16x4 v = *(const bf16x4*)(Ah + (int64_t)arow[i] * p.lda + (K0) + lc4); \
+      rah[i] = aval[i] ? v : bf16x4{};                                           \
+    }                                                                            \
+  } else {                                                                       \
+    GS_LOAD_A(K0)                                                                \
+  }
 #define GS_LOAD_B_BF16(K0)                                                       \
   _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                \
     const bf16x8 w = *(const bf16x8*)(Bh + bo[j] + (K0));                        \
@@ -553,23 +576,27 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   }
 
   const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
-  GS_LOAD_A(kbeg)
+  GS_LOAD_AH(kbeg)
   GS_LOAD_B_BF16(kbeg)
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       bf16x4 h;
-      h.x = (__bf16)ra[i].x;
-      h.y = (__bf16)ra[i].y;
-      h.z = (__bf16)ra[i].z;
-      h.w = (__bf16)ra[i].w;
+      if (ALOAD == A_PLAIN_H) {
+        h = rah[i];
+      } else {
+        h.x = (__bf16)ra[i].x;
+        h.y = (__bf16)ra[i].y;
+        h.z = (__bf16)ra[i].z;
+        h.w = (__bf16)ra[i].w;
+      }
       *(bf16x4*)&As[lrow + 32 * i][lc4] = h;
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) *(bf16x8*)&Bs[brow + 64 * j][bc8] = rbh[j];
     __syncthreads();
-    GS_LOAD_A(min(k0 + BK, kend - BK))
+    GS_LOAD_AH(min(k0 + BK, kend - BK))
     GS_LOAD_B_BF16(min(k0 + BK, kend - BK))
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl) {
@@ -585,6 +612,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
     }
   }
 #undef GS_LOAD_B_BF16
+#undef GS_LOAD_AH
   if (batch.ksplit > 1)
     store_partial(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
   else
@@ -607,7 +635,7 @@ std::string gemm_prof_name(const char* base, const GemmBatch& b) {
 
 }  // namespace
 
-int check_gemm(const GemmArgs& a, int aload, int blayout) {
+int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16) {
   GS_REQUIRE(a.M >= 0 && a.N > 0 && a.K > 0, "gemm: bad sizes");
   GS_REQUIRE(a.K % BK == 0, "gemm: K must be a multiple of 32");
   GS_REQUIRE(a.A && a.B && a.C, "gemm: null operand");
@@ -615,6 +643,8 @@ int check_gemm(const GemmArgs& a, int aload, int blayout) {
   GS_REQUIRE(a.ldb % 4 == 0, "gemm: ldb must be a multiple of 4");
   if (aload != A_CONV) GS_REQUIRE(a.lda % 4 == 0 && a.lda >= (aload == A_CONCAT ? a.K1 : a.K),
                                   "gemm: bad lda");
+  if (aload == A_PLAIN_H)
+    GS_REQUIRE(blayout == B_NT && bf16, "gemm: bf16 A needs the bf16 kernel and the NT layout");
   if (aload == A_CONCAT)
     GS_REQUIRE(a.A2 && aligned16(a.A2) && a.K1 % BK == 0 && a.K1 > 0 && a.K1 < a.K &&
                    a.lda2 % 4 == 0 && a.lda2 >= a.K - a.K1,
@@ -639,6 +669,9 @@ int check_gemm(const GemmArgs& a, int aload, int blayout) {
                "gemm: bad rope epilogue");
   if (a.flags & EPI_DUAL)
     GS_REQUIRE(a.C2 != nullptr && !(a.flags & EPI_SCATTER), "gemm: bad dual store");
+  if (a.flags & EPI_BF16OUT)
+    GS_REQUIRE(!(a.flags & (EPI_SCATTER | EPI_DUAL)) && a.ldc % 4 == 0,
+               "gemm: bf16 output excludes scatter / dual stores");
   if (a.flags & EPI_SCATTER)
     GS_REQUIRE(a.sc_r > 0 && a.sc_C > 0 && a.N == a.sc_r * a.sc_r * a.sc_C &&
                    a.sc_Cout <= a.sc_C && a.sc_gh > 0 && a.sc_gw > 0 &&
@@ -698,7 +731,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   GemmBatch b = b_in;
   int max_tiles = 0;
   for (int i = 0; i < b.ngroups; ++i) {
-    int rc = check_gemm(b.g[i], aload, blayout);
+    int rc = check_gemm(b.g[i], aload, blayout, bf16);
     if (rc) return rc;
     if (bf16)
       GS_REQUIRE(blayout == B_NT && b.g[i].Bh && aligned16(b.g[i].Bh) && b.g[i].ldb % 8 == 0,
@@ -730,7 +763,9 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     for (int i = 0; i < b.ngroups; ++i) {
       const GemmArgs& g = b.g[i];
       flops += 2.0 * g.M * (double)g.N * g.K;
-      bytes += 4.0 * ((double)g.M * g.K + (double)g.N * g.K + (double)g.M * g.N);
+      const double ea = aload == A_PLAIN_H ? 2.0 : 4.0, eb = bf16 ? 2.0 : 4.0,
+                   ec = (g.flags & EPI_BF16OUT) ? 2.0 : 4.0;
+      bytes += ea * g.M * (double)g.K + eb * g.N * (double)g.K + ec * g.M * (double)g.N;
     }
 #define GS_GEMM_BF16_CASE(AL, RL)                                             \
   if (bf16 && aload == AL && a_relu == RL) {                                  \
@@ -744,6 +779,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     return 0;                                                                 \
   }
   GS_GEMM_BF16_CASE(A_PLAIN, false)
+  GS_GEMM_BF16_CASE(A_PLAIN_H, false)
   GS_GEMM_BF16_CASE(A_CONCAT, false)
   GS_GEMM_BF16_CASE(A_CONV, false)
   GS_GEMM_BF16_CASE(A_CONV, true)

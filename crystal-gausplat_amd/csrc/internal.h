@@ -53,7 +53,8 @@ void prof_stop(hipStream_t s, hipEvent_t start, const char* kernel, double flops
 // ---- GEMM ------------------------------------------------------------------
 // C[M,N] = A[M,K] . B (+ epilogue). One GEMM problem of a (possibly grouped)
 // launch. All pointers are device pointers.
-enum ALoad : int { A_PLAIN = 0, A_CONCAT = 1, A_CONV = 2 };
+// A_PLAIN_H: plain rows of a bf16 A (the bf16 kernels only; lda in elements)
+enum ALoad : int { A_PLAIN = 0, A_CONCAT = 1, A_CONV = 2, A_PLAIN_H = 3 };
 enum BLayout : int { B_NT = 0, B_NN = 1 };
 
 enum EpiFlags : int {
@@ -65,6 +66,7 @@ enum EpiFlags : int {
   EPI_ROPE = 32,     // RoPE on columns [0, rope_ncols)
   EPI_SCATTER = 64,  // sub-pixel scatter store (ConvT / pixel shuffle)
   EPI_DUAL = 128,    // also store the result to C2 (same ldc)
+  EPI_BF16OUT = 256, // C holds bf16 (ldc in elements); not with SCATTER / DUAL
 };
 
 struct GemmArgs {
@@ -120,7 +122,7 @@ struct GemmBatch {
 // bf16: bf16-input / fp32-accumulate MFMA on the groups' Bh weight copies.
 int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
                 hipStream_t s, bool bf16 = false);
-int check_gemm(const GemmArgs& a, int aload, int blayout);
+int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16 = false);
 
 // ---- attention -----------------------------------------------------------------
 struct AttnArgs {
@@ -131,6 +133,7 @@ struct AttnArgs {
   int64_t q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn;
   int32_t B, H, Nq, Nkv;
   float scale;
+  int32_t o_bf16 = 0;  // o holds bf16 (strides in elements); bf16 kernel only
 };
 struct AttnBatch {
   AttnArgs g[kMaxGroups];
@@ -155,6 +158,7 @@ struct LnArgs {
   int64_t rows;
   int32_t D;
   float eps;
+  int32_t y_bf16 = 0;  // y holds bf16
 };
 struct LnBatch {
   LnArgs g[kMaxGroups];

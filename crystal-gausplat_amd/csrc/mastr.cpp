@@ -285,7 +285,7 @@ const float* W(Ctx& c, const std::string& n) {
 // weight into that many reference Linear modules for the literal layout.
 int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, float* C,
                 int64_t ldc, int64_t M, int N, int K, int flags, hipStream_t s, int groups = 1,
-                int rope_cols = 0) {
+                int rope_cols = 0, int aload = A_PLAIN) {
   const float* Wt = W(c, name + ".weight");
   const float* b = W(c, name + ".bias");
   if (c.cfg.linear_layout == 0) {
@@ -295,8 +295,9 @@ int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, fl
       a.R1 = C;
       a.ldr1 = ldc;
     }
-    return run1(c, a, A_PLAIN, s);
+    return run1(c, a, aload, s);
   }
+  GS_REQUIRE(aload == A_PLAIN, "linear: the literal layout takes fp32 activations");
   const int Ng = N / groups;
   for (int g = 0; g < groups; ++g) {
     GemmArgs a = lin(A, lda, Wt + (int64_t)g * Ng * K, b ? b + (int64_t)g * Ng : nullptr,
@@ -317,9 +318,9 @@ int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, fl
 }
 
 int layernorm1(const float* x, const float* g, const float* b, float* y, int64_t rows, int D,
-               float eps, hipStream_t s) {
+               float eps, hipStream_t s, bool y_bf16 = false) {
   LnBatch bt;
-  bt.g[0] = LnArgs{x, g, b, y, rows, D, eps};
+  bt.g[0] = LnArgs{x, g, b, y, rows, D, eps, y_bf16};
   bt.ngroups = 1;
   return launch_layernorm(bt, s);
 }
@@ -357,17 +358,26 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   const int D = f.enc_dim, H = f.enc_heads;
   const std::string p = "enc_blocks." + std::to_string(l);
   const int rope = f.rope_mode == 1 ? 2 * D : 0;
-  RC(layernorm1(x, W(c, p + ".norm1.weight"), W(c, p + ".norm1.bias"), c.h, M, D, f.ln_eps, s));
-  RC(linear_mode(c, p + ".attn.qkv", c.h, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope));
+  // bf16 mode: the LN, attention and fc1 outputs that only feed bf16 GEMMs
+  // are stored as bf16 (the same rounding the GEMM's A load applies to fp32)
+  const bool hb = f.precision == 1;
+  const int aH = hb ? A_PLAIN_H : A_PLAIN;
+  RC(layernorm1(x, W(c, p + ".norm1.weight"), W(c, p + ".norm1.bias"), c.h, M, D, f.ln_eps, s,
+                hb));
+  RC(linear_mode(c, p + ".attn.qkv", c.h, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope, aH));
   AttnBatch ab;
   ab.g[0] = attn_args(c.qkv, 3 * D, c.qkv + D, 3 * D, c.qkv + 2 * D, 3 * D, c.att, D,
                       (int)(M / c.N), H, c.N);
+  ab.g[0].o_bf16 = hb;
   ab.ngroups = 1;
   RC(attention(c, ab, s));
-  RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s));
-  RC(layernorm1(x, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias"), c.h, M, D, f.ln_eps, s));
-  RC(linear_mode(c, p + ".mlp.fc1", c.h, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D, EPI_GELU, s));
-  RC(linear_mode(c, p + ".mlp.fc2", c.mlp, f.enc_mlp, x, D, M, D, f.enc_mlp, EPI_RES1, s));
+  RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s, 1, 0, aH));
+  RC(layernorm1(x, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias"), c.h, M, D, f.ln_eps, s,
+                hb));
+  RC(linear_mode(c, p + ".mlp.fc1", c.h, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D,
+                 EPI_GELU | (hb ? EPI_BF16OUT : 0), s, 1, 0, aH));
+  RC(linear_mode(c, p + ".mlp.fc2", c.mlp, f.enc_mlp, x, D, M, D, f.enc_mlp, EPI_RES1, s, 1, 0,
+                 aH));
   return 0;
 }
 
@@ -396,6 +406,9 @@ int decoder(Ctx& c, int B, hipStream_t s) {
   const float eps = f.ln_eps;
   const bool rope = f.rope_mode == 1;
   const bool own_memory = f.composite == 1;
+  // bf16 mode: LN, attention and fc1 outputs stored as bf16 (see encoder_block)
+  const bool hb = f.precision == 1;
+  const int aH = hb ? A_PLAIN_H : A_PLAIN;
   {
     GemmArgs a = lin(c.enc, De, W(c, "decoder_embed.weight"), W(c, "decoder_embed.bias"), c.d, D, M,
                      D, De, own_memory ? EPI_DUAL : 0);
@@ -416,7 +429,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       LnBatch bt;
       for (int k = 0; k < 2; ++k)
         bt.g[k] = LnArgs{src[k], W(c, p[k] + nm + ".weight"), W(c, p[k] + nm + ".bias"), dst[k],
-                         Mv, D, eps};
+                         Mv, D, eps, hb};
       bt.ngroups = 2;
       return launch_layernorm(bt, s);
     };
@@ -435,7 +448,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
                    2 * D, Mv, 2 * D, D, 0);
         if (rope) with_rope(a[k], c, D);
       }
-      RC(run2(c, a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], aH, s));
     }
     // self-attention
     RC(ln2(".norm1", dc, hc));
@@ -446,11 +459,13 @@ int decoder(Ctx& c, int B, hipStream_t s) {
                    qkvc[k], 3 * D, Mv, 3 * D, D, 0);
         if (rope) with_rope(a[k], c, 2 * D);
       }
-      RC(run2(c, a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], aH, s));
       AttnBatch ab;
-      for (int k = 0; k < 2; ++k)
+      for (int k = 0; k < 2; ++k) {
         ab.g[k] = attn_args(qkvc[k], 3 * D, qkvc[k] + D, 3 * D, qkvc[k] + 2 * D, 3 * D, ac[k], D, B,
                             H, c.N);
+        ab.g[k].o_bf16 = hb;
+      }
       ab.ngroups = 2;
       RC(attention(c, ab, s));
       for (int k = 0; k < 2; ++k) {
@@ -459,7 +474,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
         a[k].R1 = dc[k];
         a[k].ldr1 = D;
       }
-      RC(run2(c, a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], aH, s));
     }
     // cross-attention (query norm3, reference role naming)
     RC(ln2(".norm3", dc, hc));
@@ -470,10 +485,12 @@ int decoder(Ctx& c, int B, hipStream_t s) {
                    W(c, p[k] + ".cross_attn.projq.bias"), qc[k], D, Mv, D, D, 0);
         if (rope) with_rope(a[k], c, D);
       }
-      RC(run2(c, a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], aH, s));
       AttnBatch ab;
-      for (int k = 0; k < 2; ++k)
+      for (int k = 0; k < 2; ++k) {
         ab.g[k] = attn_args(qc[k], D, kvc[k], 2 * D, kvc[k] + D, 2 * D, ac[k], D, B, H, c.N);
+        ab.g[k].o_bf16 = hb;
+      }
       ab.ngroups = 2;
       RC(attention(c, ab, s));
       for (int k = 0; k < 2; ++k) {
@@ -482,7 +499,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
         a[k].R1 = dc[k];
         a[k].ldr1 = D;
       }
-      RC(run2(c, a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], aH, s));
     }
     // MLP (norm2, reference role naming)
     RC(ln2(".norm2", dc, hc));
@@ -490,8 +507,8 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k)
         a[k] = lin(hc[k], D, W(c, p[k] + ".mlp.fc1.weight"), W(c, p[k] + ".mlp.fc1.bias"), mc[k],
-                   f.dec_mlp, Mv, f.dec_mlp, D, EPI_GELU);
-      RC(run2(c, a[0], a[1], A_PLAIN, s));
+                   f.dec_mlp, Mv, f.dec_mlp, D, EPI_GELU | (hb ? EPI_BF16OUT : 0));
+      RC(run2(c, a[0], a[1], aH, s));
       // the DPT hooks snapshot the state after blocks hooks[1] and hooks[2]:
       // the fc2 epilogue stores that block's output a second time
       float* hook = f.dpt_hooks[1] == l + 1 ? c.hook1 : (f.dpt_hooks[2] == l + 1 ? c.hook2 : nullptr);
@@ -503,7 +520,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
         a[k].ldr1 = D;
         if (hook) a[k].C2 = hook + (int64_t)k * Mv * D;
       }
-      RC(run2(c, a[0], a[1], A_PLAIN, s));
+      RC(run2(c, a[0], a[1], aH, s));
       if (hook2)  // both hooks on the same block
         GS_CHECK_HIP(hipMemcpyAsync(hook2, hook, M * D * sizeof(float), hipMemcpyDeviceToDevice, s));
     }
