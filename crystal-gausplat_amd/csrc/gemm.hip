@@ -49,12 +49,28 @@ __device__ __forceinline__ fx4 relu4(fx4 v) {
 // Bias, RoPE, GELU / ReLU, residuals and the (scatter) store of a wave's
 // 64x64 sub-tile. Accumulator layout of a 32x32 block: lane l, register r
 // holds row 8*(r/4) + 4*(l/32) + (r%4), column l%32.
-__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16& acc00,
-                                              const floatx16& acc01, const floatx16& acc10,
-                                              const floatx16& acc11, int m0, int n0, int wm,
-                                              int wn, int l32, int hl) {
+// Every operand a block needs (bias, RoPE table entries, residuals) is read
+// into registers before its first store: the residual may alias C, so a load
+// placed after a store could not be moved above it, and the 16 rows of a
+// block would pay 16 serial memory latencies. Each element of C depends only
+// on the same element of the residuals, so reading them all first is exact
+// also in place. Addresses are clamped into the operands; out-of-range rows
+// and columns are not stored.
+// ROPE selects the RoPE form (no residuals, checked on the host); the two
+// forms are separate branches so that their registers are not live together.
+template <bool ROPE>
+__device__ __forceinline__ void gemm_epilogue_t(const GemmArgs& p, const floatx16& acc00,
+                                                const floatx16& acc01, const floatx16& acc10,
+                                                const floatx16& acc11, int m0, int n0, int wm,
+                                                int wn, int l32, int hl) {
   const int M = p.M, N = p.N;
-  const int flags = p.flags;
+  const int flags = ROPE ? p.flags & ~(EPI_RES1 | EPI_RES2) : p.flags & ~EPI_ROPE;
+  float bval[2];
+#pragma unroll
+  for (int bj = 0; bj < 2; ++bj) {
+    const int col = n0 + wn * 64 + bj * 32 + l32;
+    bval[bj] = (flags & EPI_BIAS) ? p.bias[min(col, N - 1)] : 0.f;
+  }
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi) {
 #pragma unroll
@@ -62,8 +78,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16&
       const floatx16 c = bi == 0 ? (bj == 0 ? acc00 : acc01) : (bj == 0 ? acc10 : acc11);
       const int cblk = n0 + wn * 64 + bj * 32;
       const int col = cblk + l32;
-      const float bval = ((flags & EPI_BIAS) && col < N) ? p.bias[col] : 0.f;
-      const bool rope = (flags & EPI_ROPE) && cblk < p.rope_ncols;
+      const int colc = min(col, N - 1);
+      const int row0 = m0 + wm * 64 + bi * 32 + 4 * hl;
+      const bool rope = ROPE && cblk < p.rope_ncols;
       // scatter column decode (wave-uniform kind, per-lane values)
       int sc_i = 0, sc_j = 0, sc_c = 0;
       if (flags & EPI_SCATTER) {
@@ -72,45 +89,80 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16&
         sc_i = s / p.sc_r;
         sc_j = s - sc_i * p.sc_r;
       }
+      // Half a block (8 rows) at a time: its residuals are read into
+      // registers first (x: residual 1, y: residual 2). RoPE table reads stay
+      // in the row loop: they hit in cache, and their index arithmetic would
+      // cost more registers than it saves.
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int row = m0 + wm * 64 + bi * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-        float v = c[r];
-        if (flags & EPI_BIAS) v = v + bval;
-        if (rope) {
-          const int tok = row % p.tok_per_img;
-          const int ty = tok / p.grid_w, tx = tok - ty * p.grid_w;
-          const int pos = ((cblk >> 5) & 1) ? tx : ty;
-          const int f = l32 & 15;
-          const float cs = p.rope_cos[pos * 16 + f], sn = p.rope_sin[pos * 16 + f];
-          const float partner = __shfl_xor(v, 16);
-          v = (l32 < 16) ? (v * cs - partner * sn) : (v * cs + partner * sn);
+      for (int h = 0; h < 2; ++h) {
+        float x[8], y[8];
+        if (flags & EPI_RES1) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int r = 8 * h + u;
+            const int row = min(row0 + 8 * (r >> 2) + (r & 3), M - 1);
+            x[u] = p.R1[(int64_t)row * p.ldr1 + colc];
+          }
         }
-        if (flags & EPI_GELU) v = gelu_tanh(v);
-        if (flags & EPI_RELU) v = fmaxf(v, 0.f);
-        if (row < M && col < N) {
-          if (flags & EPI_RES1) v = v + p.R1[(int64_t)row * p.ldr1 + col];
-          if (flags & EPI_RES2) v = p.R2[(int64_t)row * p.ldr2 + col] + v;
-          if (flags & EPI_SCATTER) {
-            if (sc_c < p.sc_Cout) {
-              const int hw = p.sc_gh * p.sc_gw;
-              const int img = row / hw;
-              const int rem = row - img * hw;
-              const int y = rem / p.sc_gw, x = rem - (rem / p.sc_gw) * p.sc_gw;
-              const int64_t oy = (int64_t)img * p.sc_gh * p.sc_r + y * p.sc_r + sc_i;
-              const int64_t ox = (int64_t)x * p.sc_r + sc_j;
-              p.C[(oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c] = v;
+        if (flags & EPI_RES2) {
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int r = 8 * h + u;
+            const int row = min(row0 + 8 * (r >> 2) + (r & 3), M - 1);
+            y[u] = p.R2[(int64_t)row * p.ldr2 + colc];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int r = 8 * h + u;
+          const int row = row0 + 8 * (r >> 2) + (r & 3);
+          float v = c[r];
+          if (flags & EPI_BIAS) v = v + bval[bj];
+          if (rope) {
+            const int tok = row % p.tok_per_img;
+            const int ty = tok / p.grid_w, tx = tok - ty * p.grid_w;
+            const int pos = ((cblk >> 5) & 1) ? tx : ty;
+            const int f = l32 & 15;
+            const float cs = p.rope_cos[pos * 16 + f], sn = p.rope_sin[pos * 16 + f];
+            const float partner = __shfl_xor(v, 16);
+            v = (l32 < 16) ? (v * cs - partner * sn) : (v * cs + partner * sn);
+          }
+          if (flags & EPI_GELU) v = gelu_tanh(v);
+          if (flags & EPI_RELU) v = fmaxf(v, 0.f);
+          if (row < M && col < N) {
+            if (flags & EPI_RES1) v = v + x[u];
+            if (flags & EPI_RES2) v = y[u] + v;
+            if (flags & EPI_SCATTER) {
+              if (sc_c < p.sc_Cout) {
+                const int hw = p.sc_gh * p.sc_gw;
+                const int img = row / hw;
+                const int rem = row - img * hw;
+                const int yy = rem / p.sc_gw, xx = rem - (rem / p.sc_gw) * p.sc_gw;
+                const int64_t oy = (int64_t)img * p.sc_gh * p.sc_r + yy * p.sc_r + sc_i;
+                const int64_t ox = (int64_t)xx * p.sc_r + sc_j;
+                p.C[(oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c] = v;
+              }
+            } else if (flags & EPI_BF16OUT) {
+              ((__bf16*)p.C)[(int64_t)row * p.ldc + col] = (__bf16)v;
+            } else {
+              p.C[(int64_t)row * p.ldc + col] = v;
+              if (flags & EPI_DUAL) p.C2[(int64_t)row * p.ldc + col] = v;
             }
-          } else if (flags & EPI_BF16OUT) {
-            ((__bf16*)p.C)[(int64_t)row * p.ldc + col] = (__bf16)v;
-          } else {
-            p.C[(int64_t)row * p.ldc + col] = v;
-            if (flags & EPI_DUAL) p.C2[(int64_t)row * p.ldc + col] = v;
           }
         }
       }
     }
   }
+}
+
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16& acc00,
+                                              const floatx16& acc01, const floatx16& acc10,
+                                              const floatx16& acc11, int m0, int n0, int wm,
+                                              int wn, int l32, int hl) {
+  if (p.flags & EPI_ROPE)
+    gemm_epilogue_t<true>(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+  else
+    gemm_epilogue_t<false>(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
 }
 
 // Split-K: the raw accumulators of K range blockIdx.y go to
@@ -260,6 +312,19 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
     }                                                                                    \
   }
 
+// Origin of logical tile t of a problem. Grouped ordering: GROUP_M row tiles
+// sweep the column tiles together, so consecutive tiles share A rows and B
+// columns.
+__device__ __forceinline__ void tile_mn(const GemmArgs& p, int t, int& m0, int& n0) {
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + BN - 1) / BN;
+  const int per_group = GROUP_M * tiles_n;
+  const int gid = t / per_group;
+  const int first_m = gid * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  m0 = (first_m + (t % per_group) % gsz) * BM;
+  n0 = ((t % per_group) / gsz) * BN;
+}
+
 // Tile coordinates of this workgroup (XCD-aware remap + grouped ordering);
 // false when the workgroup has no tile in this group's problem.
 __device__ __forceinline__ bool gemm_tile(const GemmArgs& p, int& m0, int& n0) {
@@ -272,13 +337,7 @@ __device__ __forceinline__ bool gemm_tile(const GemmArgs& p, int& m0, int& n0) {
   const int nb = gridDim.x;
   if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
   if (bid >= ntiles) return false;
-  // Grouped ordering: GROUP_M row tiles sweep the column tiles together.
-  const int per_group = GROUP_M * tiles_n;
-  const int gid = bid / per_group;
-  const int first_m = gid * GROUP_M;
-  const int gsz = min(tiles_m - first_m, GROUP_M);
-  m0 = (first_m + (bid % per_group) % gsz) * BM;
-  n0 = ((bid % per_group) / gsz) * BN;
+  tile_mn(p, bid, m0, n0);
   return true;
 }
 
@@ -669,6 +728,8 @@ int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16) {
                "gemm: bad rope epilogue");
   if (a.flags & EPI_DUAL)
     GS_REQUIRE(a.C2 != nullptr && !(a.flags & EPI_SCATTER), "gemm: bad dual store");
+  if (a.flags & EPI_ROPE)
+    GS_REQUIRE(!(a.flags & (EPI_RES1 | EPI_RES2)), "gemm: RoPE excludes residual epilogues");
   if (a.flags & EPI_BF16OUT)
     GS_REQUIRE(!(a.flags & (EPI_SCATTER | EPI_DUAL)) && a.ldc % 4 == 0,
                "gemm: bf16 output excludes scatter / dual stores");
@@ -795,14 +856,22 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
                       flops, bytes);                                          \
     return 0;                                                                 \
   }
-  // long-K launches take the direct-to-LDS kernel: its double buffer (64 KB
-  // of LDS, two workgroups per CU) pays off from ~2048 K, while shorter K
-  // runs faster on the register-staged kernel at three workgroups per CU
-  // (measured per shape at config 3)
+  // fp32 kernel choice. long-K launches take the direct-to-LDS kernel: its
+  // double buffer (64 KB of LDS, two workgroups per CU) pays off from ~2048 K,
+  // while shorter K runs faster on the register-staged kernel at three
+  // workgroups per CU (measured per shape at config 3)
   bool long_k = true;
   for (int i = 0; i < b.ngroups; ++i) long_k = long_k && b.g[i].K >= 2048;
+  const bool dl_ok = !bf16 && blayout == B_NT && !a_relu && (aload == A_PLAIN || aload == A_CONCAT);
+  int kern = b.kernel;
+  if (kern == 0) {
+    kern = dl_ok && long_k ? 2 : 1;
+  } else {
+    GS_REQUIRE(kern >= 1 && kern <= 2 && !bf16, "gemm: unknown fp32 kernel request");
+    GS_REQUIRE(kern == 1 || dl_ok, "gemm: the direct-to-LDS kernel takes plain / concat A, NT B");
+  }
 #define GS_GEMM_DL_CASE(AL)                                                   \
-  if (!bf16 && long_k && aload == AL && blayout == B_NT && !a_relu) {         \
+  if (!bf16 && kern == 2 && aload == AL && blayout == B_NT && !a_relu) {      \
     hipEvent_t ev = prof_start(s);                                            \
     hipLaunchKernelGGL((gemm_f32_dl_kernel<AL>), grid, block, 0, s, b);       \
     if (b.ksplit > 1)                                                         \

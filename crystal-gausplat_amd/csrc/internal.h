@@ -116,6 +116,9 @@ struct GemmBatch {
   float* part_ws = nullptr;
   int64_t part_ws_elems = 0;
   int32_t ksplit = 0;  // 0: chosen by launch_gemm; > 0: requested split (validated)
+  // fp32 kernel: 0 chosen by launch_gemm; requested (validated): 1 register-staged,
+  // 2 direct-to-LDS
+  int32_t kernel = 0;
 };
 
 // Launch a grouped GEMM (all groups must share the loader / layout kinds).
