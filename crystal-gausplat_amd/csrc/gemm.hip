@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
 
 // Global loads of one K step into registers (macros rather than lambdas so the
 // register arrays stay in VGPRs). They use the kernel's per-row state
-// (arow, aval, cimg/coh/cow, boff/bval_, bncol/bnval).
+// (arow, aval, ohs/ows/cbase, boff/bval_, bncol/bnval).
 #define GS_LOAD_A(K0)                                                                    \
   {                                                                                      \
     const int k0_ = (K0);                                                                \
@@ -261,15 +261,15 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
         const int kc = first ? k0_ : k0_ - p.K1;                                         \
         v = *(const fx4*)(base + (int64_t)arow[i] * ld + kc + lc4);                      \
       } else {                                                                           \
+        /* tap (kh, kw), channels ic0..: one offset on the row's base; */                \
+        /* padded taps read A[lc4..] (in bounds) and are zeroed below */                 \
         const int kk = k0_ / p.cCin;                                                     \
         const int ic0 = k0_ - kk * p.cCin;                                               \
         const int kh = kk / p.ck, kw = kk - kh * p.ck;                                   \
-        const int ih = coh[i] * p.cs + kh - p.cp;                                        \
-        const int iw = cow[i] * p.cs + kw - p.cp;                                        \
-        ok = ok && ih >= 0 && ih < p.cH && iw >= 0 && iw < p.cW;                         \
-        const int ihc = min(max(ih, 0), p.cH - 1), iwc = min(max(iw, 0), p.cW - 1);      \
-        v = *(const fx4*)(p.A + (((int64_t)cimg[i] * p.cH + ihc) * p.cW + iwc) * p.cCin + \
-                          ic0 + lc4);                                                    \
+        const int64_t toff = ((int64_t)kh * p.cW + kw) * p.cCin + ic0;                   \
+        const int ih = ohs[i] + kh, iw = ows[i] + kw;                                    \
+        ok = ok && (unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW;       \
+        v = *(const fx4*)(p.A + (ok ? cbase[i] + toff : 0) + lc4);                       \
       }                                                                                  \
       v = ok ? v : zero4;                                                                \
       if (A_RELU) v = relu4(v);                                                          \
@@ -298,17 +298,22 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
 #define GS_ROW_STATE()                                                                   \
   int arow[4];                                                                           \
   bool aval[4];                                                                          \
-  int cimg[4], coh[4], cow[4];                                                           \
+  /* implicit conv: top-left input coordinate of the row's window and the */          \
+  /* offset of that (possibly padded) pixel's channel 0 */                               \
+  int ohs[4], ows[4];                                                                    \
+  int64_t cbase[4];                                                                      \
   _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                        \
     const int m = m0 + lrow + 32 * i;                                                    \
     aval[i] = m < M;                                                                     \
     arow[i] = min(m, M - 1);                                                             \
     if (ALOAD == A_CONV) {                                                               \
       const int hw = p.cHo * p.cWo;                                                      \
-      cimg[i] = arow[i] / hw;                                                            \
-      const int rem = arow[i] - cimg[i] * hw;                                            \
-      coh[i] = rem / p.cWo;                                                              \
-      cow[i] = rem - coh[i] * p.cWo;                                                     \
+      const int img = arow[i] / hw;                                                      \
+      const int rem = arow[i] - img * hw;                                                \
+      const int oh = rem / p.cWo, ow = rem - oh * p.cWo;                                 \
+      ohs[i] = oh * p.cs - p.cp;                                                         \
+      ows[i] = ow * p.cs - p.cp;                                                         \
+      cbase[i] = (((int64_t)img * p.cH + ohs[i]) * p.cW + ows[i]) * p.cCin;              \
     }                                                                                    \
   }
 
