@@ -16,6 +16,10 @@
 // and the exponentiated scores are already the B operand of the P.V product:
 // MFMA step s takes key 8*(s/4) + 4*(lane/32) + s%4 -- exactly the key the
 // lane holds in accumulator register s. No LDS round trip for P.
+// The exponentials are the hardware exp2 (v_exp_f32, one instruction): it
+// flushes results below 2^-126 to zero, i.e. it drops only terms that are
+// 2^-126 below the running row maximum (exp2(-inf) = 0 for masked keys and
+// for the first rescale).
 #include <string>
 
 #include "internal.h"
@@ -136,11 +140,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
       for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
       mb = fmaxf(mb, __shfl_xor(mb, 32));
       const float m_new = fmaxf(m_run, mb);
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[r] = exp2f(s[r] - m_new);
+        s[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
         ps += s[r];
       }
       l_run = l_run * alpha + ps;
@@ -347,11 +351,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
       for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
       mb = fmaxf(mb, __shfl_xor(mb, 32));
       const float m_new = fmaxf(m_run, mb);
-      const float alpha = exp2f(m_run - m_new);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[r] = exp2f(s[r] - m_new);
+        s[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
         ps += s[r];
       }
       l_run = l_run * alpha + ps;
