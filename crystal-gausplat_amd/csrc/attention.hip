@@ -139,21 +139,29 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
 #pragma unroll
       for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
       mb = fmaxf(mb, __shfl_xor(mb, 32));
-      const float m_new = fmaxf(m_run, mb);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      // Lazy rescaling: the reference maximum m_run only moves (and O, l
+      // are rescaled) when some query of the wave sees a score more than
+      // 2^8 above it, so exp2(s - m_run) <= 256 and the rescale multiplies
+      // are skipped for most blocks (the first block always moves it from
+      // -inf). O / l is unchanged by the choice of reference.
+      const float m_cand = fmaxf(m_run, mb);
+      if (__any(m_cand > m_run + 8.0f)) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
+        l_run *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          o0[r] *= alpha;
+          o1[r] *= alpha;
+        }
+        m_run = m_cand;
+      }
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
+        s[r] = __builtin_amdgcn_exp2f(s[r] - m_run);
         ps += s[r];
       }
-      l_run = l_run * alpha + ps;
-      m_run = m_new;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        o0[r] *= alpha;
-        o1[r] *= alpha;
-      }
+      l_run += ps;
       // O^T += V^T P^T: A = V^T (hd row l32, k = key of register st).
 #pragma unroll
       for (int st = 0; st < 16; ++st) {
@@ -350,21 +358,29 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
 #pragma unroll
       for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
       mb = fmaxf(mb, __shfl_xor(mb, 32));
-      const float m_new = fmaxf(m_run, mb);
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+      // Lazy rescaling: the reference maximum m_run only moves (and O, l
+      // are rescaled) when some query of the wave sees a score more than
+      // 2^8 above it, so exp2(s - m_run) <= 256 and the rescale multiplies
+      // are skipped for most blocks (the first block always moves it from
+      // -inf). O / l is unchanged by the choice of reference.
+      const float m_cand = fmaxf(m_run, mb);
+      if (__any(m_cand > m_run + 8.0f)) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
+        l_run *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          o0[r] *= alpha;
+          o1[r] *= alpha;
+        }
+        m_run = m_cand;
+      }
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[r] = __builtin_amdgcn_exp2f(s[r] - m_new);
+        s[r] = __builtin_amdgcn_exp2f(s[r] - m_run);
         ps += s[r];
       }
-      l_run = l_run * alpha + ps;
-      m_run = m_new;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        o0[r] *= alpha;
-        o1[r] *= alpha;
-      }
+      l_run += ps;
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl) {
         bf16x8 pb;
