@@ -36,6 +36,20 @@ sys.path.insert(0, os.path.join(ROOT, "crystal-gausplat_amd"))
 
 MFMA_FP32_PEAK_TFLOPS = 157.3
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+# fp32 through bf16x6 split products: six bf16 MFMAs per fp32-equivalent
+# product, so its fp32-equivalent ceiling is the bf16 peak / 6
+MFMA_X6_PEAK_TFLOPS = MFMA_BF16_PEAK_TFLOPS / 6
+
+
+def kernel_peak(name):
+    """MFMA ceiling of a library kernel in the units bench.py counts its flops:
+    bf16 kernels 2.5 PFLOP/s, bf16x6 kernels (fp32-equivalent flops) 2.5/6,
+    fp32 kernels 157.3 TFLOP/s."""
+    if "bf16" in name:
+        return MFMA_BF16_PEAK_TFLOPS
+    if "_x6_" in name:
+        return MFMA_X6_PEAK_TFLOPS
+    return MFMA_FP32_PEAK_TFLOPS
 HBM_PEAK_GBS = 8000.0
 # Algorithmic work of one 384x512 pair and of one config-0 encoder block
 # (GFLOP), from the FLOP model of the path.
@@ -282,6 +296,40 @@ def secondary(args):
     return out
 
 
+def fp32x6_variant(args, B, H, W):
+    """The same workload in precision 2 (fp32 GEMMs and convolutions on bf16
+    matrix cores through exact three-term splits, attention in fp32), timed
+    the same way. Reported beside the fp32 headline, never as `value`."""
+    import torch
+
+    import gsplat_hip as G
+    cfg = G.default_config(img_h=H, img_w=W, precision=2)
+    m = G.Mastr(cfg, B)
+    m.init_seeded(0)
+    n = B * 3 * H * W
+    img1 = torch.from_numpy(G.seed_uniform(0, "view1", n).reshape(B, 3, H, W)).cuda()
+    img2 = torch.from_numpy(G.seed_uniform(0, "view2", n).reshape(B, 3, H, W)).cuda()
+    outs = [torch.empty(B, H, W, c, device="cuda") for c in (3, 1, cfg.desc_dim) * 2]
+    stream = torch.cuda.current_stream().cuda_stream
+    step = lambda: m.pair(img1, img2, B, *outs, stream=stream)
+    sec = _timed(step, args.steps, args.warmup)
+    G.profile_begin()
+    step()
+    torch.cuda.synchronize()
+    prof = G.profile_end()
+    m.close()
+    dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
+    tf = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
+    return {"value": round(B / sec, 3), "ms_per_step": round(sec * 1e3, 3),
+            "dtype": "f32 (bf16x6 split products, f32 acc)",
+            "precision_note": "error against an fp64 product at or below the fp32 MFMA "
+                              "kernel's (tests/test_gpu_ops.py::"
+                              "test_linear_f32x6_accuracy_vs_fp64); pair outputs at the fp32 "
+                              "parity bar (test_gpu_model.py::test_tiny_pair_f32x6_parity)",
+            "dominant_kernel": dom_name, "dominant_tflops_fp32_equivalent": round(tf, 2),
+            "dominant_frac_of_bf16_peak_div6": round(tf / MFMA_X6_PEAK_TFLOPS, 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -292,9 +340,14 @@ def main():
     ap.add_argument("--graph", action="store_true",
                     help="replay the launch sequence as a hipGraph (the per-kernel roofline "
                          "then comes from one extra eager, profiled step)")
-    ap.add_argument("--bf16", action="store_true",
-                    help="bf16-input / fp32-accumulate MFMA variant (reported separately; the "
-                         "headline metric is fp32)")
+    ap.add_argument("--precision", default="fp32", choices=["fp32", "bf16", "fp32x6"],
+                    help="fp32: fp32 MFMA (the headline); bf16: bf16-input / fp32-accumulate "
+                         "variant; fp32x6: fp32 GEMMs and convolutions on bf16 matrix cores "
+                         "through exact three-term bf16 splits (six term products, fp32 "
+                         "accumulate; fp32-level accuracy), attention in fp32")
+    ap.add_argument("--bf16", action="store_true", help="same as --precision bf16")
+    ap.add_argument("--no-variants", action="store_true",
+                    help="skip the fp32x6 line reported beside the fp32 headline")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--per-shape", action="store_true",
                     help="also print a per-shape kernel table (stderr) from a separate step")
@@ -307,6 +360,8 @@ def main():
                     help="only run 3 plain device-to-device copies of MIB MiB (the known-size "
                          "kernel that scales the FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
+    if args.bf16:
+        args.precision = "bf16"
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only. MASt3R pairs are independent, so "
@@ -333,7 +388,8 @@ def main():
         return
     wl = CONFIGS[args.config]
     B = args.pairs or wl["pairs"]
-    cfg = G.default_config(img_h=wl["img_h"], img_w=wl["img_w"], precision=1 if args.bf16 else 0)
+    cfg = G.default_config(img_h=wl["img_h"], img_w=wl["img_w"],
+                           precision={"fp32": 0, "bf16": 1, "fp32x6": 2}[args.precision])
     H, W = cfg.img_h, cfg.img_w
 
     m = G.Mastr(cfg, B)
@@ -394,7 +450,7 @@ def main():
     # roofline of the dominant kernel (largest summed event time)
     dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
     avg_ms = dom["ms"] / dom["launches"]
-    peak = MFMA_BF16_PEAK_TFLOPS if args.bf16 else MFMA_FP32_PEAK_TFLOPS
+    peak = kernel_peak(dom_name)
     if dom["flops"] > 0 and dom_name.startswith(("gemm", "attn")):
         achieved = dom["flops"] / dom["launches"] / (avg_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 2), "peak": peak,
@@ -408,7 +464,7 @@ def main():
     try:
         tr = json.load(open(os.path.join(ROOT, "profiles", "pmc_traffic.json")))["workloads"]
         key = f"config{args.config}-{'graph' if args.graph else 'eager'}-" \
-              f"{'bf16' if args.bf16 else 'f32'}-{B}"
+              f"{ {'fp32': 'f32', 'bf16': 'bf16', 'fp32x6': 'f32x6'}[args.precision]}-{B}"
         t = tr.get(key, {}).get(dom_name)
         if t:
             roof["traffic"] = (t["fetch_kib"] + t["write_kib"]) * 1024
@@ -418,8 +474,9 @@ def main():
     roof["kernel"] = dom_name
     roof["launches_per_step"] = dom["launches"] // args.steps
     roof["avg_launch_ms"] = round(avg_ms, 4)
-    mfma_ms = sum(v["ms"] for k, v in prof.items() if k.startswith(("gemm", "attn")))
-    mfma_fl = sum(v["flops"] for k, v in prof.items() if k.startswith(("gemm", "attn")))
+    mm = [(k, v) for k, v in prof.items() if k.startswith(("gemm", "attn"))]
+    mfma_fl = sum(v["flops"] for k, v in mm)
+    mfma_cap = sum(v["ms"] * 1e-3 * kernel_peak(k) * 1e12 for k, v in mm)
     kernels = {k: {"launches": v["launches"] // args.steps, "ms_per_step": round(v["ms"] / args.steps, 3),
                    "tflops": round(v["flops"] / (v["ms"] * 1e-3) / 1e12, 2) if v["flops"] else None,
                    "gbs": round(v["bytes"] / (v["ms"] * 1e-3) / 1e9, 1) if v["bytes"] else None}
@@ -436,7 +493,8 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16-in/f32-acc" if args.bf16 else "f32",
+        "dtype": {"fp32": "f32", "bf16": "bf16-in/f32-acc",
+                  "fp32x6": "f32 (bf16x6 split products, f32 acc)"}[args.precision],
         "data": "synthetic (seeded U(-1,1) images, seeded N(0,0.02) weights)",
         "config": {"workload": f"config {args.config}: {B} image pairs at 3x{H}x{W}, full "
                                f"MASt3R two-view inference (ViT-L encoder x2 views, ViT-B "
@@ -445,7 +503,7 @@ def main():
                    "launch": "hipGraph replay" if args.graph else "eager stream",
                    "timed": "H2D images + pair + D2H outputs (PCIe-inclusive, not the "
                             "headline)" if args.e2e else "device-resident inputs and outputs"},
-        "gemm_attn_frac_mfma_peak": round(mfma_fl / (mfma_ms * 1e-3) / 1e12 / peak, 4),
+        "gemm_attn_frac_mfma_peak": round(mfma_fl / mfma_cap, 4),
         "kernel_share_of_step": round(sum(v["ms"] for v in prof.values()) / ms, 4),
         "roofline": roof,
         "kernels": kernels,
@@ -458,9 +516,11 @@ def main():
         for k, v in sorted(shp.items(), key=lambda kv: -kv[1]["ms"]):
             tf = v["flops"] / (v["ms"] * 1e-3) / 1e12 if v["flops"] else 0.0
             print(f"{v['ms']:9.3f} ms {v['launches']:4d}x {tf:7.1f} TF/s  {k}", file=sys.stderr)
+    m.close()
+    if args.precision == "fp32" and not (args.graph or args.e2e or args.no_variants):
+        out["variants"] = {"fp32x6": fp32x6_variant(args, B, H, W)}
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
-    m.close()
     print(json.dumps(out), flush=True)
 
 

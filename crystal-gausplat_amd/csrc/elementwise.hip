@@ -422,7 +422,33 @@ __global__ void f32_to_bf16_kernel(const float* __restrict__ in, __bf16* __restr
   }
 }
 
+// Exact three-term bf16 split (x0 = bf16(x), x1 = bf16(x - x0), x2 =
+// bf16(x - x0 - x1)), the same arithmetic as the bf16x6 GEMM's on-the-fly
+// split, so pre-split weights give bit-identical products.
+__global__ void f32_to_bf16x3_kernel(const float* __restrict__ in, __bf16* __restrict__ out,
+                                     int64_t n, int64_t plane) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float v = in[i];
+  const __bf16 h = (__bf16)v;
+  const float r1 = v - (float)h;
+  const __bf16 m = (__bf16)r1;
+  const float r2 = r1 - (float)m;
+  out[i] = h;
+  out[plane + i] = m;
+  out[2 * plane + i] = (__bf16)r2;
+}
+
 }  // namespace
+
+int launch_f32_to_bf16x3(const float* in, void* out, int64_t n, int64_t plane, hipStream_t s) {
+  if (n <= 0) return 0;
+  GS_REQUIRE(in && out && plane >= n, "f32_to_bf16x3: bad arguments");
+  hipLaunchKernelGGL(f32_to_bf16x3_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, in,
+                     (__bf16*)out, n, plane);
+  GS_CHECK_HIP(hipGetLastError());
+  return 0;
+}
 
 int launch_f32_to_bf16(const float* in, void* out, int64_t n, hipStream_t s) {
   if (n <= 0) return 0;

@@ -700,6 +700,169 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
     gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
 }
 
+// fp32 GEMM through bf16 matrix cores ("bf16x6"): every fp32 operand x is
+// split exactly into three bf16 terms x = x0 + x1 + x2 (x0 = bf16(x),
+// x1 = bf16(x - x0), x2 = bf16(x - x0 - x1); each remainder is exact in fp32)
+// and the product is accumulated in fp32 from the six term products whose
+// relative size is at least 2^-16 (x0y0, x0y1, x1y0, x1y1, x0y2, x2y0; the
+// dropped x1y2, x2y1, x2y2 are <= 2^-24 relative, the size of one fp32
+// rounding). Each bf16 x bf16 product is exact in the fp32 accumulation, so
+// the result has fp32-level accuracy at 6 bf16 MFMAs (32 cycles each) per
+// 32x32x16 block instead of 8 fp32 MFMAs (64 cycles each). Same tile,
+// loaders (plain / concat / conv, ReLU prologue) and epilogue as
+// gemm_f32_kernel; operands are read in fp32 and split on their way into
+// LDS, three bf16 planes per operand (rows of 40 bf16 as in gemm_bf16_kernel).
+// BSPLIT: B arrives pre-split (planes at Bh + t * bh_plane, same arithmetic,
+// so the products are bit-identical) and is copied into LDS as loaded.
+// Terms are accumulated smallest first.
+__device__ __forceinline__ void split3(const fx4& v, bf16x4& h, bf16x4& m, bf16x4& l) {
+  h = bf16x4{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+  const fx4 r1 = v - mk4((float)h.x, (float)h.y, (float)h.z, (float)h.w);
+  m = bf16x4{(__bf16)r1.x, (__bf16)r1.y, (__bf16)r1.z, (__bf16)r1.w};
+  const fx4 r2 = r1 - mk4((float)m.x, (float)m.y, (float)m.z, (float)m.w);
+  l = bf16x4{(__bf16)r2.x, (__bf16)r2.y, (__bf16)r2.z, (__bf16)r2.w};
+}
+
+template <int ALOAD, bool A_RELU, bool BSPLIT>
+__global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
+  constexpr int BLAYOUT = B_NT;
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int M = p.M, N = p.N, K = p.K;
+  int m0, n0;
+  if (!gemm_tile(p, m0, n0)) return;
+
+  __shared__ __attribute__((aligned(16))) __bf16 As[3][BM][LDSH];
+  __shared__ __attribute__((aligned(16))) __bf16 Bs[3][BN][LDSH];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int lrow = tid >> 3, lc4 = (tid & 7) * 4;
+
+  GS_ROW_STATE()
+  int boff[4];
+  bool bval_[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int n = n0 + lrow + 32 * i;
+    bval_[i] = n < N;
+    boff[i] = min(n, N - 1) * (int)p.ldb + lc4;
+  }
+  const int bncol = 0;  // NN-layout state of the shared loader macro (unused here)
+  const bool bnval = true;
+  // pre-split B: rows tid/4 + 64*j (j < 2), 8 bf16 at column 8*(tid%4) per plane
+  const __bf16* Bh = (const __bf16*)p.Bh;
+  const int brow = tid >> 2, bc8 = (tid & 3) * 8;
+  int bo[2];
+  bool bok[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int n = n0 + brow + 64 * j;
+    bok[j] = n < N;
+    bo[j] = min(n, N - 1) * (int)p.ldb + bc8;
+  }
+  // two register stages: the loads of K step k + 2 are issued at step k, so
+  // they have two steps of MFMA work to land (one step of this kernel is a
+  // third of the fp32 kernel's MFMA time, too short to hide them alone)
+  fx4 ra0[4], ra1[4], rb0[BSPLIT ? 1 : 4], rb1[BSPLIT ? 1 : 4];
+  bf16x8 rbp0[BSPLIT ? 3 : 1][2], rbp1[BSPLIT ? 3 : 1][2];
+  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+  const bf16x8 zero8 = {};
+  floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
+  // loads of one K step into register stage S (0 or 1), through the shared
+  // loader macros (which write ra / rb)
+#define GS_X6_LOAD(K0, S)                                                        \
+  {                                                                              \
+    fx4* const ra = S ? ra1 : ra0;                                               \
+    fx4* const rb = S ? rb1 : rb0;                                               \
+    (void)rb;                                                                    \
+    GS_LOAD_A(K0)                                                                \
+    if (BSPLIT) {                                                                \
+      bf16x8(*const rbp)[2] = S ? rbp1 : rbp0;                                   \
+      _Pragma("unroll") for (int t = 0; t < 3; ++t)                              \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j) {                            \
+        const bf16x8 w = *(const bf16x8*)(Bh + t * p.bh_plane + bo[j] + (K0));   \
+        rbp[t][j] = bok[j] ? w : zero8;                                          \
+      }                                                                          \
+    } else {                                                                     \
+      GS_LOAD_B_F32(K0)                                                          \
+    }                                                                            \
+  }
+  // one K step from register stage S: split into the LDS planes, then the
+  // loads of step k0 + 2 BK into the freed stage, then the MFMAs
+#define GS_X6_STEP(S)                                                            \
+  {                                                                              \
+    fx4* const ra = S ? ra1 : ra0;                                               \
+    fx4* const rb = S ? rb1 : rb0;                                               \
+    __syncthreads();                                                             \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                              \
+      bf16x4 h, m, l;                                                            \
+      split3(ra[i], h, m, l);                                                    \
+      *(bf16x4*)&As[0][lrow + 32 * i][lc4] = h;                                  \
+      *(bf16x4*)&As[1][lrow + 32 * i][lc4] = m;                                  \
+      *(bf16x4*)&As[2][lrow + 32 * i][lc4] = l;                                  \
+      if (!BSPLIT) {                                                             \
+        split3(rb[i], h, m, l);                                                  \
+        *(bf16x4*)&Bs[0][lrow + 32 * i][lc4] = h;                                \
+        *(bf16x4*)&Bs[1][lrow + 32 * i][lc4] = m;                                \
+        *(bf16x4*)&Bs[2][lrow + 32 * i][lc4] = l;                                \
+      }                                                                          \
+    }                                                                            \
+    if (BSPLIT) {                                                                \
+      bf16x8(*const rbp)[2] = S ? rbp1 : rbp0;                                   \
+      _Pragma("unroll") for (int t = 0; t < 3; ++t)                              \
+      _Pragma("unroll") for (int j = 0; j < 2; ++j)                              \
+        *(bf16x8*)&Bs[t][brow + 64 * j][bc8] = rbp[t][j];                        \
+    }                                                                            \
+    __syncthreads();                                                             \
+    if (k0 + 2 * BK < kend) GS_X6_LOAD(k0 + 2 * BK, S)                           \
+    GS_X6_MMA()                                                                  \
+    k0 += BK;                                                                    \
+  }
+#define GS_X6_MMA()                                                              \
+  _Pragma("unroll") for (int sl = 0; sl < 2; ++sl) {                             \
+    const int kc = sl * 16 + hl * 8;                                             \
+    bf16x8 a0[3], a1[3], b0[3], b1[3];                                           \
+    _Pragma("unroll") for (int t = 0; t < 3; ++t) {                              \
+      a0[t] = *(const bf16x8*)&As[t][wm * 64 + l32][kc];                         \
+      a1[t] = *(const bf16x8*)&As[t][wm * 64 + 32 + l32][kc];                    \
+      b0[t] = *(const bf16x8*)&Bs[t][wn * 64 + l32][kc];                         \
+      b1[t] = *(const bf16x8*)&Bs[t][wn * 64 + 32 + l32][kc];                    \
+    }                                                                            \
+    GS_X6(2, 0)                                                                  \
+    GS_X6(0, 2)                                                                  \
+    GS_X6(1, 1)                                                                  \
+    GS_X6(1, 0)                                                                  \
+    GS_X6(0, 1)                                                                  \
+    GS_X6(0, 0)                                                                  \
+  }
+#define GS_X6(TA, TB)                                                                \
+  acc00 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[TA], b0[TB], acc00, 0, 0, 0);   \
+  acc01 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0[TA], b1[TB], acc01, 0, 0, 0);   \
+  acc10 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[TA], b0[TB], acc10, 0, 0, 0);   \
+  acc11 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[TA], b1[TB], acc11, 0, 0, 0);
+
+  const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
+  int k0 = kbeg;
+  GS_X6_LOAD(kbeg, 0)
+  if (kbeg + BK < kend) GS_X6_LOAD(kbeg + BK, 1)
+  while (true) {
+    GS_X6_STEP(0)
+    if (k0 >= kend) break;
+    GS_X6_STEP(1)
+    if (k0 >= kend) break;
+  }
+#undef GS_X6
+#undef GS_X6_MMA
+#undef GS_X6_STEP
+#undef GS_X6_LOAD
+  if (batch.ksplit > 1)
+    store_partial(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+  else
+    gemm_epilogue(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+}
+
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 std::string gemm_prof_name(const char* base, const GemmBatch& b) {
@@ -869,6 +1032,27 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   GS_GEMM_BF16_CASE(A_CONV, false)
   GS_GEMM_BF16_CASE(A_CONV, true)
 #undef GS_GEMM_BF16_CASE
+  bool presplit = true;
+  for (int i = 0; i < b.ngroups; ++i) presplit = presplit && b.g[i].bh_plane > 0;
+  if (!bf16 && b.kernel == 4 && presplit)
+    for (int i = 0; i < b.ngroups; ++i)
+      GS_REQUIRE(b.g[i].Bh && aligned16(b.g[i].Bh) && b.g[i].ldb % 8 == 0 &&
+                     b.g[i].bh_plane % 8 == 0,
+                 "gemm: pre-split B planes must be 16-byte aligned with ldb % 8 == 0");
+#define GS_GEMM_X6_CASE(AL, RL, NM)                                           \
+  if (!bf16 && kern == 4 && aload == AL && blayout == B_NT && a_relu == RL) { \
+    hipEvent_t ev = prof_start(s);                                            \
+    if (presplit)                                                             \
+      hipLaunchKernelGGL((gemm_x6_kernel<AL, RL, true>), grid, block, 0, s, b); \
+    else                                                                      \
+      hipLaunchKernelGGL((gemm_x6_kernel<AL, RL, false>), grid, block, 0, s, b); \
+    if (b.ksplit > 1)                                                         \
+      hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
+    GS_CHECK_HIP(hipGetLastError());                                          \
+    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_x6_kernel<" NM ">", b).c_str(), \
+                      flops, bytes);                                          \
+    return 0;                                                                 \
+  }
 #define GS_GEMM_CASE(AL, BL, RL)                                              \
   if (!bf16 && aload == AL && blayout == BL && a_relu == RL) {                \
     hipEvent_t ev = prof_start(s);                                            \
@@ -891,8 +1075,9 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   if (kern == 0) {
     kern = dl_ok && long_k ? 2 : 1;
   } else {
-    GS_REQUIRE(kern >= 1 && kern <= 2 && !bf16, "gemm: unknown fp32 kernel request");
-    GS_REQUIRE(kern == 1 || dl_ok, "gemm: the direct-to-LDS kernel takes plain / concat A, NT B");
+    GS_REQUIRE(kern >= 1 && kern <= 4 && kern != 3 && !bf16, "gemm: unknown fp32 kernel request");
+    GS_REQUIRE(kern != 4 || blayout == B_NT, "gemm: the bf16x6 kernel takes NT B");
+    GS_REQUIRE(kern != 2 || dl_ok, "gemm: the direct-to-LDS kernel takes plain / concat A, NT B");
   }
 #define GS_GEMM_DL_CASE(AL)                                                   \
   if (!bf16 && kern == 2 && aload == AL && blayout == B_NT && !a_relu) {      \
@@ -908,6 +1093,11 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   GS_GEMM_DL_CASE(A_PLAIN)
   GS_GEMM_DL_CASE(A_CONCAT)
 #undef GS_GEMM_DL_CASE
+  GS_GEMM_X6_CASE(A_PLAIN, false, "A_PLAIN")
+  GS_GEMM_X6_CASE(A_CONCAT, false, "A_CONCAT")
+  GS_GEMM_X6_CASE(A_CONV, false, "A_CONV")
+  GS_GEMM_X6_CASE(A_CONV, true, "A_CONV,relu")
+#undef GS_GEMM_X6_CASE
   GS_GEMM_CASE(A_PLAIN, B_NT, false)
   GS_GEMM_CASE(A_PLAIN, B_NN, false)
   GS_GEMM_CASE(A_PLAIN, B_NT, true)

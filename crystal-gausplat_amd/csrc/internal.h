@@ -80,7 +80,10 @@ struct GemmArgs {
   // (kh*ck + kw)*cCin + ic
   int32_t cH, cW, cCin, ck, cs, cp, cHo, cWo;
   const float* B;   // NT: B[n*ldb + k]; NN: B[k*ldb + n]
-  const void* Bh;   // bf16 copy of B (NT layout, same ldb) for the bf16 kernels
+  const void* Bh;   // bf16 copy of B (NT layout, same ldb) for the bf16 kernels;
+                    // for the bf16x6 kernel with bh_plane > 0: plane 0 of the
+                    // three-term bf16 split of B, plane t at Bh + t * bh_plane
+  int64_t bh_plane; // elements between the split planes (0: split B on the fly)
   int64_t ldb;
   float* C;
   int64_t ldc;
@@ -117,7 +120,7 @@ struct GemmBatch {
   int64_t part_ws_elems = 0;
   int32_t ksplit = 0;  // 0: chosen by launch_gemm; > 0: requested split (validated)
   // fp32 kernel: 0 chosen by launch_gemm; requested (validated): 1 register-staged,
-  // 2 direct-to-LDS
+  // 2 direct-to-LDS, 4 bf16x6 (fp32-accurate products on bf16 matrix cores)
   int32_t kernel = 0;
 };
 
@@ -195,6 +198,9 @@ int launch_convt_relayout(const float* w, const float* b, int32_t Cin,
 
 // fp32 -> bf16 (round to nearest even), n elements.
 int launch_f32_to_bf16(const float* in, void* out, int64_t n, hipStream_t s);
+// Exact three-term bf16 split x = x0 + x1 + x2 of n floats: plane t at
+// out + t * plane (bf16 elements), plane >= n.
+int launch_f32_to_bf16x3(const float* in, void* out, int64_t n, int64_t plane, hipStream_t s);
 
 // RoPE tables for 64-wide heads: cos/sin [max_pos][16], host computed.
 void rope_table_host(int32_t max_pos, float base, float* cos_t, float* sin_t);

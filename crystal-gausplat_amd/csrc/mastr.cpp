@@ -170,7 +170,8 @@ struct Ctx {
   std::map<std::string, float*> derived;  // kv weights etc. by name
   char* warena = nullptr;
   size_t warena_size = 0;
-  char* wbf16 = nullptr;     // bf16 mirror of warena (precision 1)
+  char* wbf16 = nullptr;     // bf16 mirror of warena (precision 1), or its
+                             // three-plane bf16 split (precision 2)
   bool bf16_dirty = true;
   char* arena = nullptr;
   size_t arena_size = 0;
@@ -245,6 +246,15 @@ int gemm(const Ctx& c, GemmBatch& b, int aload, bool relu_in, hipStream_t s) {
     }
   b.part_ws = c.splitk;
   b.part_ws_elems = kSplitkElems;
+  if (c.cfg.precision == 2) {  // fp32 through bf16x6 split products, weights pre-split
+    b.kernel = 4;
+    for (int i = 0; i < b.ngroups; ++i) {
+      const char* w = (const char*)b.g[i].B;
+      GS_REQUIRE(w >= c.warena && w < c.warena + c.warena_size, "gemm: weight outside the arena");
+      b.g[i].Bh = c.wbf16 + (w - c.warena) / 2;
+      b.g[i].bh_plane = (int64_t)(c.warena_size / 4);
+    }
+  }
   return launch_gemm(b, aload, B_NT, relu_in, s, bf);
 }
 
@@ -811,10 +821,15 @@ int place_weight(Ctx& c, const std::string& name, const float* host, int64_t n) 
   return 0;
 }
 
-// Refresh the bf16 weight mirror after weight updates (precision 1).
+// Refresh the bf16 weight mirror (precision 1) or split planes (precision 2)
+// after weight updates.
 int sync_bf16(Ctx& c, hipStream_t s) {
-  if (c.cfg.precision != 1 || !c.bf16_dirty) return 0;
-  RC(launch_f32_to_bf16((const float*)c.warena, c.wbf16, (int64_t)(c.warena_size / 4), s));
+  if (c.cfg.precision == 0 || !c.bf16_dirty) return 0;
+  const int64_t n = (int64_t)(c.warena_size / 4);
+  if (c.cfg.precision == 1)
+    RC(launch_f32_to_bf16((const float*)c.warena, c.wbf16, n, s));
+  else
+    RC(launch_f32_to_bf16x3((const float*)c.warena, c.wbf16, n, n, s));
   c.bf16_dirty = false;
   return 0;
 }
@@ -847,6 +862,7 @@ int build_weights(Ctx& c) {
   GS_CHECK_HIP(hipMalloc(&c.warena, total));
   c.warena_size = total;
   if (f.precision == 1) GS_CHECK_HIP(hipMalloc(&c.wbf16, total / 2));
+  if (f.precision == 2) GS_CHECK_HIP(hipMalloc(&c.wbf16, 3 * (total / 2)));
   char* cur = c.warena;
   auto take = [&](int64_t nfl) {
     float* p = (float*)cur;
@@ -1003,8 +1019,9 @@ int validate_config(const gs_mastr_config& f) {
   GS_REQUIRE(f.desc_dim > 0 && (f.patch * f.patch * f.desc_dim) % 32 == 0, "config: bad desc_dim");
   GS_REQUIRE(f.linear_layout == 0 || f.linear_layout == 1, "config: linear_layout must be 0 or 1");
   GS_REQUIRE(f.rope_mode >= 0 && f.rope_mode <= 2, "config: rope_mode must be 0, 1 or 2");
-  GS_REQUIRE(f.precision == 0 || (f.precision == 1 && f.linear_layout == 0),
-             "config: precision must be 0 (fp32) or 1 (bf16 MFMA, linear_layout 0)");
+  GS_REQUIRE(f.precision == 0 || ((f.precision == 1 || f.precision == 2) && f.linear_layout == 0),
+             "config: precision must be 0 (fp32), 1 (bf16 MFMA) or 2 (fp32 through bf16x6), "
+             "1 and 2 with linear_layout 0");
   GS_REQUIRE(f.enc_dim % 32 == 0 && f.dec_dim % 32 == 0, "config: dims must be multiples of 32");
   GS_REQUIRE(f.composite == 0 || f.composite == 1, "config: composite must be 0 or 1");
   GS_REQUIRE(f.composite == 0 || f.dpt_dims[3] == f.dec_dim,

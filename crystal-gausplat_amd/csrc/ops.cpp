@@ -83,8 +83,12 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   if (ensure_device()) return -2;
   GS_REQUIRE(w_layout == 0 || w_layout == 1, "linear: w_layout must be 0 or 1");
   GS_REQUIRE(M >= 0 && M <= INT32_MAX, "linear: M out of range");
-  GS_REQUIRE((epilogue & ~(GS_EPI_GELU | GS_EPI_RESIDUAL | GS_EPI_RELU | GS_EPI_BF16)) == 0,
+  GS_REQUIRE((epilogue & ~(GS_EPI_GELU | GS_EPI_RESIDUAL | GS_EPI_RELU | GS_EPI_BF16 |
+                          GS_EPI_F32X6)) == 0,
              "linear: unknown epilogue flag");
+  const bool x6 = (epilogue & GS_EPI_F32X6) != 0;
+  GS_REQUIRE(!x6 || (w_layout == 0 && !(epilogue & GS_EPI_BF16)),
+             "linear: the bf16x6 variant needs w_layout 0 and excludes the bf16 variant");
   const bool bf16 = (epilogue & GS_EPI_BF16) != 0;
   GS_REQUIRE(!bf16 || w_layout == 0, "linear: the bf16 variant needs w_layout 0");
   GS_REQUIRE(!(epilogue & GS_EPI_RESIDUAL) || residual, "linear: residual flag without residual");
@@ -118,6 +122,7 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   GemmBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
+  if (x6) bt.kernel = 4;
   int rc = launch_gemm(bt, A_PLAIN, w_layout == 0 ? B_NT : B_NN, false, s, bf16);
   if (rc == 0 && bf16) GS_CHECK_HIP(hipStreamSynchronize(s));  // workspace reuse
   return rc;
@@ -167,7 +172,8 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   GS_REQUIRE(w_layout == 0 || w_layout == 1, "conv2d: w_layout must be 0 or 1");
   GS_REQUIRE(k > 0 && stride > 0 && pad >= 0 && B >= 0 && H > 0 && W > 0 && Cout > 0,
              "conv2d: bad geometry");
-  GS_REQUIRE((flags & ~(GS_CONV_RELU_IN | GS_CONV_RELU_OUT)) == 0, "conv2d: unknown flag");
+  GS_REQUIRE((flags & ~(GS_CONV_RELU_IN | GS_CONV_RELU_OUT | GS_CONV_F32X6)) == 0,
+             "conv2d: unknown flag");
   const int32_t Ho = (H + 2 * pad - k) / stride + 1, Wo = (W + 2 * pad - k) / stride + 1;
   GS_REQUIRE(Ho > 0 && Wo > 0, "conv2d: empty output");
   hipStream_t s = pick(stream);
@@ -208,6 +214,7 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   GemmBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
+  if (flags & GS_CONV_F32X6) bt.kernel = 4;
   int rc = launch_gemm(bt, pointwise ? A_PLAIN : A_CONV, B_NT, (flags & GS_CONV_RELU_IN) != 0, s);
   if (rc == 0 && wk != w) GS_CHECK_HIP(hipStreamSynchronize(s));  // workspace reuse
   return rc;

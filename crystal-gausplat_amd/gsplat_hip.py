@@ -120,8 +120,8 @@ _SIGS = [
                                          C.POINTER(C.c_double)]),
 ]
 
-EPI_GELU, EPI_RESIDUAL, EPI_RELU, EPI_BF16 = 1, 2, 4, 8
-CONV_RELU_IN, CONV_RELU_OUT = 1, 2
+EPI_GELU, EPI_RESIDUAL, EPI_RELU, EPI_BF16, EPI_F32X6 = 1, 2, 4, 8, 16
+CONV_RELU_IN, CONV_RELU_OUT, CONV_F32X6 = 1, 2, 4
 
 _lib = None
 

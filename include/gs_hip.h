@@ -114,6 +114,9 @@ void gs_seed_uniform(uint64_t seed, const char* name, float lo, float hi,
 #define GS_EPI_RESIDUAL 2 /* y = residual + (x.W + b)                        */
 #define GS_EPI_RELU 4     /* y = max(x.W + b, 0)                             */
 #define GS_EPI_BF16 8     /* bf16-input / fp32-accumulate MFMA (w_layout 0)  */
+#define GS_EPI_F32X6 16   /* fp32 through bf16 matrix cores: exact three-term
+                             bf16 split of both operands, six term products,
+                             fp32 accumulate (fp32-level accuracy; w_layout 0) */
 
 /* NN::GPUOps.linear_forward (src/nn/gpu_ops.cr:39-78) plus the bias add the
  * reference does on the CPU (src/nn/linear.cr:206-230).
@@ -163,6 +166,7 @@ int32_t gs_hip_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld,
  * GS_CONV_RELU_OUT after the bias, residual (nullable) is added last. */
 #define GS_CONV_RELU_IN 1
 #define GS_CONV_RELU_OUT 2
+#define GS_CONV_F32X6 4   /* products as GS_EPI_F32X6 */
 int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W,
                       int32_t Cin, const float* w, const float* b, float* y,
                       int32_t Cout, int32_t k, int32_t stride, int32_t pad,
@@ -230,7 +234,13 @@ typedef struct gs_mastr_config {
   int32_t linear_layout; /* 0 = x W^T; 1 = reference CPU literal layout */
   int32_t rope_mode;     /* 0 none, 1 per-attention q/k 2D, 2 ref-token */
   int32_t precision;     /* 0 = fp32 MFMA; 1 = bf16-input / fp32-accumulate
-                            MFMA GEMMs and attention (linear_layout 0 only) */
+                            MFMA GEMMs and attention (linear_layout 0 only);
+                            2 = fp32 GEMMs and convolutions on bf16 matrix
+                            cores through exact three-term bf16 splits of
+                            both operands (six term products, fp32
+                            accumulate; error vs fp64 at or below the fp32
+                            MFMA kernels'), attention in fp32 MFMA
+                            (linear_layout 0 only) */
   int32_t composite;     /* 0 = MASt3R composition (full DPT at image
                             resolution, 1+exp confidence, descriptors, each
                             decoder chain attending to the other view's

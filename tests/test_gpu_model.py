@@ -107,6 +107,43 @@ def test_tiny_pair_parity_and_taps(tiny_cfg):
     m.close()
 
 
+def test_tiny_pair_f32x6_parity(tiny_cfg):
+    """Precision 2 (fp32 GEMMs and convolutions through bf16x6 split
+    products): the whole pair at the fp32 parity bar against the oracle."""
+    case("tiny pair f32x6")
+    cfg = G.default_config(**tiny_cfg, precision=2)
+    w = weights_for(cfg, 0, bias_std=0.02, ln_std=0.1)
+    B = 2
+    n = B * 3 * cfg.img_h * cfg.img_w
+    i1 = G.seed_uniform(0, "view1", n).reshape(B, 3, cfg.img_h, cfg.img_w)
+    i2 = G.seed_uniform(0, "view2", n).reshape(B, 3, cfg.img_h, cfg.img_w)
+    m = load_ctx(cfg, w, max_pairs=B)
+    got = run_pair(m, cfg, i1, i2, B)
+    m.close()
+    check_pair(got, O.mastr_pair(cfg.as_dict(), w, i1, i2), "tiny f32x6")
+
+
+def test_config2_f32x6_vs_fp32():
+    """Config 2 at full size in precision 2 against the fp32 MFMA path (itself
+    checked against the oracle at this size): the fp32 parity bar."""
+    case("config2 f32x6 vs fp32")
+    n = 3 * 384 * 512
+    i1 = G.seed_uniform(0, "view1", n).reshape(1, 3, 384, 512)
+    i2 = G.seed_uniform(0, "view2", n).reshape(1, 3, 384, 512)
+    outs = []
+    for prec in (0, 2):
+        cfg = G.default_config(precision=prec)
+        m = G.Mastr(cfg, 1)
+        m.init_seeded(0)
+        outs.append(run_pair(m, cfg, i1, i2, 1))
+        m.close()
+        del m
+        torch.cuda.empty_cache()
+    for k in outs[0]:
+        assert not np.array_equal(outs[0][k], outs[1][k])
+    check_pair(outs[1], outs[0], "config2 f32x6")
+
+
 def test_ragged_grid_split_paths(tiny_cfg):
     """A 12x26 patch grid (312 tokens) at one pair: the small launches split K
     (GEMMs) and the key range (attention, last range ragged: 312 = 4 x 64 + 56)

@@ -80,6 +80,61 @@ def test_linear_bf16_variant(M, K, N):
     assert rel > 1e-5  # it really ran in bf16
 
 
+@pytest.mark.parametrize("M,K,N", [(256, 1024, 256), (256, 4096, 256), (300, 1792, 7168),
+                                   (129, 96, 130)])
+def test_linear_f32x6_accuracy_vs_fp64(M, K, N):
+    """fp32 through bf16x6 split products against an fp64 product: its error
+    is at the level of the fp32 MFMA kernel's (RMS within 1.5x, max within
+    2x), it meets the fp32 parity bar against the oracle, and it differs from
+    the fp32 kernel in the last bits (it really ran the bf16 matrix cores)."""
+    case(f"linear f32x6 M={M} K={K} N={N}")
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.02), rnd(N, scale=0.1)
+    ref64 = x.astype(np.float64) @ W.astype(np.float64).T + b.astype(np.float64)
+
+    def run(flags):
+        y = empty(M, N)
+        G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, 0, flags, None,
+                                  stream()))
+        return host(y)
+
+    y32, y6 = run(0), run(G.EPI_F32X6)
+    e32, e6 = y32.astype(np.float64) - ref64, y6.astype(np.float64) - ref64
+    rms32, rms6 = np.sqrt(np.mean(e32 ** 2)), np.sqrt(np.mean(e6 ** 2))
+    print(f"f32x6 M={M} K={K} N={N}: rms err fp32 {rms32:.3e} x6 {rms6:.3e}; "
+          f"max fp32 {np.abs(e32).max():.3e} x6 {np.abs(e6).max():.3e}")
+    assert rms6 <= 1.5 * rms32 + 1e-9
+    assert np.abs(e6).max() <= 2.0 * np.abs(e32).max() + 1e-9
+    assert (y6 != y32).mean() > 0.01
+    assert_close(y6, O.linear(x, W, b), name="linear f32x6")
+
+
+@pytest.mark.parametrize("epi", ["gelu", "residual"])
+def test_linear_f32x6_epilogues(epi):
+    case(f"linear f32x6 epilogue {epi}")
+    M, K, N = 200, 256, 384
+    x, W, b, r = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1), rnd(M, N)
+    ref = O.linear(x, W, b)
+    flags = G.EPI_F32X6
+    if epi == "gelu":
+        flags, ref = flags | G.EPI_GELU, O.gelu(ref)
+    else:
+        flags, ref = flags | G.EPI_RESIDUAL, r + ref
+    y = dev(r) if epi == "residual" else empty(M, N)
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, 0, flags,
+                              p(y) if epi == "residual" else None, stream()))
+    assert_close(host(y), ref, name=f"f32x6 {epi}")
+
+
+def test_linear_f32x6_validation():
+    case("linear f32x6 validation")
+    x = empty(4, 32)
+    rc = L().gs_hip_linear(p(x), p(x), None, p(x), 4, 32, 4, 1, G.EPI_F32X6, None, stream())
+    assert rc != 0 and b"w_layout 0" in L().gs_hip_last_error()
+    rc = L().gs_hip_linear(p(x), p(x), None, p(x), 4, 32, 4, 0, G.EPI_F32X6 | G.EPI_BF16, None,
+                           stream())
+    assert rc != 0
+
+
 @pytest.mark.parametrize("M,K,N", [(768, 1024, 1024), (50, 64, 96)])
 def test_linear_literal_layout(M, K, N):
     # D1: the reference CPU path's [out,in] buffer read as [in,out]
@@ -200,6 +255,31 @@ def test_conv2d_parity(B, H, W, Cin, Cout, k, s, pd, flags, res):
     G.check(L().gs_hip_conv2d(p(dev(x)), B, H, W, Cin, p(dev(w)), p(dev(b)), p(y), Cout, k, s, pd,
                               0, flags, p(dev(r)) if res else None, stream()))
     assert_close(host(y), ref, name="conv2d")
+
+
+@pytest.mark.parametrize("B,H,W,Cin,Cout,k,s,pd,flags,res", [CONV_CASES[i] for i in (0, 2, 3, 4, 6)])
+def test_conv2d_f32x6(B, H, W, Cin, Cout, k, s, pd, flags, res):
+    """Implicit-GEMM convolution with bf16x6 split products: the fp32 parity
+    bar against the oracle, and close to the fp32 MFMA kernel."""
+    case(f"conv2d f32x6 B={B} {H}x{W} {Cin}->{Cout} k={k} s={s} p={pd} flags={flags} res={res}")
+    x, w, b = rnd(B, H, W, Cin), rnd(Cout, Cin, k, k, scale=0.05), rnd(Cout, scale=0.1)
+    Ho, Wo = (H + 2 * pd - k) // s + 1, (W + 2 * pd - k) // s + 1
+    r = rnd(B, Ho, Wo, Cout)
+    xin = np.maximum(x, 0) if flags & G.CONV_RELU_IN else x
+    ref = O.conv2d(xin, w, b, s, pd)
+    if flags & G.CONV_RELU_OUT:
+        ref = np.maximum(ref, 0)
+    if res:
+        ref = ref + r
+    ys = []
+    for extra in (0, G.CONV_F32X6):
+        y = empty(B, Ho, Wo, Cout)
+        G.check(L().gs_hip_conv2d(p(dev(x)), B, H, W, Cin, p(dev(w)), p(dev(b)), p(y), Cout, k, s,
+                                  pd, 0, flags | extra, p(dev(r)) if res else None, stream()))
+        ys.append(host(y))
+    assert_close(ys[1], ref, name="conv2d f32x6")
+    scale = np.abs(ys[0]).max()
+    assert np.abs(ys[1] - ys[0]).max() <= 1e-5 * scale + 1e-6
 
 
 @pytest.mark.parametrize("Cin,Cout,k,H,W", [(96, 96, 4, 24, 32), (192, 192, 2, 24, 32),
