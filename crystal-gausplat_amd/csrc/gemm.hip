@@ -711,7 +711,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
 // 32x32x16 block instead of 8 fp32 MFMAs (64 cycles each). Same tile,
 // loaders (plain / concat / conv, ReLU prologue) and epilogue as
 // gemm_f32_kernel; operands are read in fp32 and split on their way into
-// LDS, three bf16 planes per operand (rows of 40 bf16 as in gemm_bf16_kernel).
+// LDS, three bf16 planes per operand.
 // BSPLIT: B arrives pre-split (planes at Bh + t * bh_plane, same arithmetic,
 // so the products are bit-identical) and is copied into LDS as loaded.
 // Terms are accumulated smallest first.
@@ -731,8 +731,12 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   int m0, n0;
   if (!gemm_tile(p, m0, n0)) return;
 
-  __shared__ __attribute__((aligned(16))) __bf16 As[3][BM][LDSH];
-  __shared__ __attribute__((aligned(16))) __bf16 Bs[3][BN][LDSH];
+  // unpadded rows of 32 bf16 (four 16-byte chunks), chunk c of row r at slot
+  // c ^ ((r >> 2) & 3): the MFMA reads of 16 consecutive rows at one chunk
+  // and the split writes of 4 consecutive rows hit distinct bank groups
+  __shared__ __attribute__((aligned(16))) __bf16 As[3][BM][BK];
+  __shared__ __attribute__((aligned(16))) __bf16 Bs[3][BN][BK];
+#define GS_X6_SW(R, K) ((((K) >> 3) ^ (((R) >> 2) & 3)) << 3 | ((K) & 7))
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -799,21 +803,22 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                              \
       bf16x4 h, m, l;                                                            \
       split3(ra[i], h, m, l);                                                    \
-      *(bf16x4*)&As[0][lrow + 32 * i][lc4] = h;                                  \
-      *(bf16x4*)&As[1][lrow + 32 * i][lc4] = m;                                  \
-      *(bf16x4*)&As[2][lrow + 32 * i][lc4] = l;                                  \
+      const int sa_ = GS_X6_SW(lrow + 32 * i, lc4);                              \
+      *(bf16x4*)&As[0][lrow + 32 * i][sa_] = h;                                  \
+      *(bf16x4*)&As[1][lrow + 32 * i][sa_] = m;                                  \
+      *(bf16x4*)&As[2][lrow + 32 * i][sa_] = l;                                  \
       if (!BSPLIT) {                                                             \
         split3(rb[i], h, m, l);                                                  \
-        *(bf16x4*)&Bs[0][lrow + 32 * i][lc4] = h;                                \
-        *(bf16x4*)&Bs[1][lrow + 32 * i][lc4] = m;                                \
-        *(bf16x4*)&Bs[2][lrow + 32 * i][lc4] = l;                                \
+        *(bf16x4*)&Bs[0][lrow + 32 * i][sa_] = h;                                \
+        *(bf16x4*)&Bs[1][lrow + 32 * i][sa_] = m;                                \
+        *(bf16x4*)&Bs[2][lrow + 32 * i][sa_] = l;                                \
       }                                                                          \
     }                                                                            \
     if (BSPLIT) {                                                                \
       bf16x8(*const rbp)[2] = S ? rbp1 : rbp0;                                   \
       _Pragma("unroll") for (int t = 0; t < 3; ++t)                              \
       _Pragma("unroll") for (int j = 0; j < 2; ++j)                              \
-        *(bf16x8*)&Bs[t][brow + 64 * j][bc8] = rbp[t][j];                        \
+        *(bf16x8*)&Bs[t][brow + 64 * j][GS_X6_SW(brow + 64 * j, bc8)] = rbp[t][j]; \
     }                                                                            \
     __syncthreads();                                                             \
     if (k0 + 2 * BK < kend) GS_X6_LOAD(k0 + 2 * BK, S)                           \
@@ -822,7 +827,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   }
 #define GS_X6_MMA()                                                              \
   _Pragma("unroll") for (int sl = 0; sl < 2; ++sl) {                             \
-    const int kc = sl * 16 + hl * 8;                                             \
+    const int kc = GS_X6_SW(l32, sl * 16 + hl * 8); /* rows wm*64 + l32 (+32) */ \
     bf16x8 a0[3], a1[3], b0[3], b1[3];                                           \
     _Pragma("unroll") for (int t = 0; t < 3; ++t) {                              \
       a0[t] = *(const bf16x8*)&As[t][wm * 64 + l32][kc];                         \
@@ -857,6 +862,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
 #undef GS_X6_MMA
 #undef GS_X6_STEP
 #undef GS_X6_LOAD
+#undef GS_X6_SW
   if (batch.ksplit > 1)
     store_partial(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
   else
