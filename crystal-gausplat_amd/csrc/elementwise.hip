@@ -48,6 +48,11 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnBatch bt) {
   }
   const float var = wave_sum(q) / (float)D;
   const float inv = 1.0f / sqrtf(var + p.eps);
+  if (p.stats && lane == 0) {  // for GEMMs that apply the normalisation on load
+    p.stats[2 * row] = mean;
+    p.stats[2 * row + 1] = inv;
+  }
+  if (!p.y) return;
   const fx4* g4 = (const fx4*)p.gamma;
   const fx4* b4 = (const fx4*)p.beta;
   fx4* yr = (fx4*)(p.y + row * D);
@@ -226,8 +231,9 @@ int launch_layernorm(const LnBatch& bt, hipStream_t s) {
   for (int i = 0; i < bt.ngroups; ++i) {
     const LnArgs& a = bt.g[i];
     GS_REQUIRE(a.D == D, "layernorm: grouped rows must share D");
-    GS_REQUIRE(a.x && a.y && a.gamma && a.beta, "layernorm: null operand");
-    GS_REQUIRE(aligned16(a.x) && aligned16(a.y) && aligned16(a.gamma) && aligned16(a.beta),
+    GS_REQUIRE(a.x && (a.y || a.stats) && a.gamma && a.beta, "layernorm: null operand");
+    GS_REQUIRE(aligned16(a.x) && (!a.y || aligned16(a.y)) && aligned16(a.gamma) &&
+                   aligned16(a.beta),
                "layernorm: operands must be 16-byte aligned");
     max_rows = a.rows > max_rows ? a.rows : max_rows;
   }
@@ -244,7 +250,8 @@ int launch_layernorm(const LnBatch& bt, hipStream_t s) {
     double rows = 0, bytes = 0;
     for (int i = 0; i < bt.ngroups; ++i) {
       rows += (double)bt.g[i].rows;
-      bytes += (bt.g[i].y_bf16 ? 6.0 : 8.0) * (double)bt.g[i].rows * D + 8.0 * D;
+      const double per = !bt.g[i].y ? 4.0 : (bt.g[i].y_bf16 ? 6.0 : 8.0);  // stats-only: read
+      bytes += per * (double)bt.g[i].rows * D + 8.0 * D + (bt.g[i].stats ? 8.0 * bt.g[i].rows : 0.0);
     }
     prof_stop(s, ev, "layernorm_kernel", 8.0 * rows * D, bytes);
   }

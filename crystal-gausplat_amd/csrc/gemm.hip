@@ -271,6 +271,14 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
       bool ok = aval[i];                                                                 \
       if (ALOAD == A_PLAIN) {                                                            \
         v = *(const fx4*)(p.A + (int64_t)arow[i] * p.lda + k0_ + lc4);                   \
+      } else if (ALOAD == A_LN) {                                                        \
+        const fx4 x_ = *(const fx4*)(p.A + (int64_t)arow[i] * p.lda + k0_ + lc4);        \
+        const fx4 g_ = *(const fx4*)(p.ln_g + k0_ + lc4);                                \
+        const fx4 b_ = *(const fx4*)(p.ln_b + k0_ + lc4);                                \
+        v.x = (x_.x - lnm[i]) * lnr[i] * g_.x + b_.x;                                    \
+        v.y = (x_.y - lnm[i]) * lnr[i] * g_.y + b_.y;                                    \
+        v.z = (x_.z - lnm[i]) * lnr[i] * g_.z + b_.z;                                    \
+        v.w = (x_.w - lnm[i]) * lnr[i] * g_.w + b_.w;                                    \
       } else if (ALOAD == A_CONCAT) {                                                    \
         const bool first = k0_ < p.K1;                                                   \
         const float* base = first ? p.A : p.A2;                                          \
@@ -319,10 +327,15 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
   /* offset of that (possibly padded) pixel's channel 0 */                               \
   int ohs[4], ows[4];                                                                    \
   int64_t cbase[4];                                                                      \
+  float lnm[4], lnr[4]; /* A_LN: the row's mean and inv_std */                           \
   _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                        \
     const int m = m0 + lrow + 32 * i;                                                    \
     aval[i] = m < M;                                                                     \
     arow[i] = min(m, M - 1);                                                             \
+    if (ALOAD == A_LN) {                                                                 \
+      lnm[i] = p.ln_stats[2 * (int64_t)arow[i]];                                         \
+      lnr[i] = p.ln_stats[2 * (int64_t)arow[i] + 1];                                     \
+    }                                                                                    \
     if (ALOAD == A_CONV) {                                                               \
       const int hw = p.cHo * p.cWo;                                                      \
       const int img = arow[i] / hw;                                                      \
@@ -893,6 +906,10 @@ int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16) {
   GS_REQUIRE(a.ldb % 4 == 0, "gemm: ldb must be a multiple of 4");
   if (aload != A_CONV) GS_REQUIRE(a.lda % 4 == 0 && a.lda >= (aload == A_CONCAT ? a.K1 : a.K),
                                   "gemm: bad lda");
+  if (aload == A_LN)
+    GS_REQUIRE(!bf16 && a.ln_stats && a.ln_g && a.ln_b && aligned16(a.ln_g) && aligned16(a.ln_b),
+               "gemm: the fused LayerNorm load needs row statistics, gamma and beta "
+               "(fp32 kernels)");
   if (aload == A_PLAIN_H)
     GS_REQUIRE(blayout == B_NT && bf16, "gemm: bf16 A needs the bf16 kernel and the NT layout");
   if (aload == A_CONCAT)
@@ -1100,11 +1117,13 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   GS_GEMM_DL_CASE(A_CONCAT)
 #undef GS_GEMM_DL_CASE
   GS_GEMM_X6_CASE(A_PLAIN, false, "A_PLAIN")
+  GS_GEMM_X6_CASE(A_LN, false, "A_LN")
   GS_GEMM_X6_CASE(A_CONCAT, false, "A_CONCAT")
   GS_GEMM_X6_CASE(A_CONV, false, "A_CONV")
   GS_GEMM_X6_CASE(A_CONV, true, "A_CONV,relu")
 #undef GS_GEMM_X6_CASE
   GS_GEMM_CASE(A_PLAIN, B_NT, false)
+  GS_GEMM_CASE(A_LN, B_NT, false)
   GS_GEMM_CASE(A_PLAIN, B_NN, false)
   GS_GEMM_CASE(A_PLAIN, B_NT, true)
   GS_GEMM_CASE(A_CONCAT, B_NT, false)

@@ -54,7 +54,11 @@ void prof_stop(hipStream_t s, hipEvent_t start, const char* kernel, double flops
 // C[M,N] = A[M,K] . B (+ epilogue). One GEMM problem of a (possibly grouped)
 // launch. All pointers are device pointers.
 // A_PLAIN_H: plain rows of a bf16 A (the bf16 kernels only; lda in elements)
-enum ALoad : int { A_PLAIN = 0, A_CONCAT = 1, A_CONV = 2, A_PLAIN_H = 3 };
+// A_LN: plain rows with the LayerNorm apply step fused into the load:
+// a = (x - mean[row]) * inv_std[row] * gamma[k] + beta[k], the same
+// expression as the LayerNorm kernel (bit-identical operands), row statistics
+// from its stats pass.
+enum ALoad : int { A_PLAIN = 0, A_CONCAT = 1, A_CONV = 2, A_PLAIN_H = 3, A_LN = 4 };
 enum BLayout : int { B_NT = 0, B_NN = 1 };
 
 enum EpiFlags : int {
@@ -100,6 +104,10 @@ struct GemmArgs {
   const float* rope_cos;
   const float* rope_sin;
   int32_t rope_ncols, tok_per_img, grid_w;
+  // A_LN: per-row (mean, inv_std) pairs and the LayerNorm's gamma / beta [K]
+  const float* ln_stats;
+  const float* ln_g;
+  const float* ln_b;
   // scatter epilogue: row m = (img, y, x) on a sc_gh x sc_gw grid; column
   // n = (i*sc_r + j)*sc_C + c -> C[((img*sc_gh*sc_r + y*sc_r + i)*sc_gw*sc_r
   // + x*sc_r + j)*sc_C + c]; columns with c >= sc_Cout are dropped.
@@ -165,6 +173,7 @@ struct LnArgs {
   int32_t D;
   float eps;
   int32_t y_bf16 = 0;  // y holds bf16
+  float* stats = nullptr;  // optional (mean, inv_std) per row; y may then be null
 };
 struct LnBatch {
   LnArgs g[kMaxGroups];

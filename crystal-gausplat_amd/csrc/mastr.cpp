@@ -177,6 +177,7 @@ struct Ctx {
   size_t arena_size = 0;
   // workspaces
   float *P, *x, *h, *qkv, *att, *mlp, *enc, *d, *ym, *kv, *q, *hook1, *hook2, *dfin;
+  float* lnst;  // (mean, inv_std) per row of the LayerNorms fused into GEMM loads
   float* dmem;  // composite 1: decoder_embed output, the fixed cross-attention memory
   float* splitk;  // split-K partial tiles of small GEMM launches (kSplitkElems floats)
   // DPT / descriptor workspaces, one slot per head of a grouped launch
@@ -293,13 +294,23 @@ const float* W(Ctx& c, const std::string& n) {
 
 // Linear under the context's layout mode (D1). groups > 1 splits a fused
 // weight into that many reference Linear modules for the literal layout.
+// LayerNorm applied in the GEMM's A load (A_LN): row statistics, gamma, beta.
+struct LnFuse {
+  const float* stats = nullptr;
+  const float* g = nullptr;
+  const float* b = nullptr;
+};
+
 int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, float* C,
                 int64_t ldc, int64_t M, int N, int K, int flags, hipStream_t s, int groups = 1,
-                int rope_cols = 0, int aload = A_PLAIN) {
+                int rope_cols = 0, int aload = A_PLAIN, LnFuse lnf = LnFuse()) {
   const float* Wt = W(c, name + ".weight");
   const float* b = W(c, name + ".bias");
   if (c.cfg.linear_layout == 0) {
     GemmArgs a = lin(A, lda, Wt, b, C, ldc, M, N, K, flags);
+    a.ln_stats = lnf.stats;
+    a.ln_g = lnf.g;
+    a.ln_b = lnf.b;
     if (rope_cols) with_rope(a, c, rope_cols);
     if (flags & EPI_RES1) {
       a.R1 = C;
@@ -328,9 +339,9 @@ int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, fl
 }
 
 int layernorm1(const float* x, const float* g, const float* b, float* y, int64_t rows, int D,
-               float eps, hipStream_t s, bool y_bf16 = false) {
+               float eps, hipStream_t s, bool y_bf16 = false, float* stats = nullptr) {
   LnBatch bt;
-  bt.g[0] = LnArgs{x, g, b, y, rows, D, eps, y_bf16};
+  bt.g[0] = LnArgs{x, g, b, y, rows, D, eps, y_bf16, stats};
   bt.ngroups = 1;
   return launch_layernorm(bt, s);
 }
@@ -372,9 +383,19 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   // are stored as bf16 (the same rounding the GEMM's A load applies to fp32)
   const bool hb = f.precision == 1;
   const int aH = hb ? A_PLAIN_H : A_PLAIN;
-  RC(layernorm1(x, W(c, p + ".norm1.weight"), W(c, p + ".norm1.bias"), c.h, M, D, f.ln_eps, s,
-                hb));
-  RC(linear_mode(c, p + ".attn.qkv", c.h, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope, aH));
+  // fp32 products (precisions 0 and 2): the norm1 / norm2 apply steps run in
+  // the qkv / fc1 A loads, after a statistics-only LayerNorm pass
+  const bool fuse = f.precision != 1 && f.linear_layout == 0;
+  const LnFuse ln1{c.lnst, W(c, p + ".norm1.weight"), W(c, p + ".norm1.bias")};
+  const LnFuse ln2{c.lnst, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias")};
+  if (fuse) {
+    RC(layernorm1(x, ln1.g, ln1.b, nullptr, M, D, f.ln_eps, s, false, c.lnst));
+    RC(linear_mode(c, p + ".attn.qkv", x, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope, A_LN,
+                   ln1));
+  } else {
+    RC(layernorm1(x, ln1.g, ln1.b, c.h, M, D, f.ln_eps, s, hb));
+    RC(linear_mode(c, p + ".attn.qkv", c.h, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope, aH));
+  }
   AttnBatch ab;
   ab.g[0] = attn_args(c.qkv, 3 * D, c.qkv + D, 3 * D, c.qkv + 2 * D, 3 * D, c.att, D,
                       (int)(M / c.N), H, c.N);
@@ -382,10 +403,15 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   ab.ngroups = 1;
   RC(attention(c, ab, s));
   RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s, 1, 0, aH));
-  RC(layernorm1(x, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias"), c.h, M, D, f.ln_eps, s,
-                hb));
-  RC(linear_mode(c, p + ".mlp.fc1", c.h, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D,
-                 EPI_GELU | (hb ? EPI_BF16OUT : 0), s, 1, 0, aH));
+  if (fuse) {
+    RC(layernorm1(x, ln2.g, ln2.b, nullptr, M, D, f.ln_eps, s, false, c.lnst));
+    RC(linear_mode(c, p + ".mlp.fc1", x, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D, EPI_GELU, s, 1, 0,
+                   A_LN, ln2));
+  } else {
+    RC(layernorm1(x, ln2.g, ln2.b, c.h, M, D, f.ln_eps, s, hb));
+    RC(linear_mode(c, p + ".mlp.fc1", c.h, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D,
+                   EPI_GELU | (hb ? EPI_BF16OUT : 0), s, 1, 0, aH));
+  }
   RC(linear_mode(c, p + ".mlp.fc2", c.mlp, f.enc_mlp, x, D, M, D, f.enc_mlp, EPI_RES1, s, 1, 0,
                  aH));
   return 0;
@@ -435,13 +461,32 @@ int decoder(Ctx& c, int B, hipStream_t s) {
     float* qc[2] = {c.q, c.q + Mv * D};
     float* ac[2] = {c.att, c.att + Mv * D};
     float* mc[2] = {c.mlp, c.mlp + Mv * f.dec_mlp};
+    // LayerNorm of src per chain. fp32 products (precisions 0 and 2): a
+    // statistics-only pass, the apply step runs in the next GEMM's A load
+    // (A_LN) on src; otherwise the normalised rows are written to dst. Sets
+    // the next GEMM's A sources (asrc) and loader (al).
+    const bool fuse = f.precision != 1 && f.linear_layout == 0;
+    const float* asrc[2];
+    int al = aH;
+    const char* lnm = "";
     auto ln2 = [&](const char* nm, float* const* src, float* const* dst) {
       LnBatch bt;
-      for (int k = 0; k < 2; ++k)
-        bt.g[k] = LnArgs{src[k], W(c, p[k] + nm + ".weight"), W(c, p[k] + nm + ".bias"), dst[k],
-                         Mv, D, eps, hb};
+      for (int k = 0; k < 2; ++k) {
+        bt.g[k] = LnArgs{src[k], W(c, p[k] + nm + ".weight"), W(c, p[k] + nm + ".bias"),
+                         fuse ? nullptr : dst[k], Mv, D, eps, hb,
+                         fuse ? c.lnst + 2 * Mv * k : nullptr};
+        asrc[k] = fuse ? src[k] : dst[k];
+      }
+      al = fuse ? A_LN : aH;
+      lnm = nm;
       bt.ngroups = 2;
       return launch_layernorm(bt, s);
+    };
+    auto lnset = [&](GemmArgs& a, int k) {
+      if (!fuse) return;
+      a.ln_stats = c.lnst + 2 * Mv * k;
+      a.ln_g = W(c, p[k] + lnm + ".weight");
+      a.ln_b = W(c, p[k] + lnm + ".bias");
     };
     // Cross-attention memory: the other view's state before this block, or
     // (composite 1) this view's decoder_embed output.
@@ -454,22 +499,24 @@ int decoder(Ctx& c, int B, hipStream_t s) {
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
-        a[k] = lin(yc[k], D, c.derived[p[k] + ".kv.weight"], c.derived[p[k] + ".kv.bias"], kvc[k],
-                   2 * D, Mv, 2 * D, D, 0);
+        a[k] = lin(asrc[k], D, c.derived[p[k] + ".kv.weight"], c.derived[p[k] + ".kv.bias"],
+                   kvc[k], 2 * D, Mv, 2 * D, D, 0);
+        lnset(a[k], k);
         if (rope) with_rope(a[k], c, D);
       }
-      RC(run2(c, a[0], a[1], aH, s));
+      RC(run2(c, a[0], a[1], al, s));
     }
     // self-attention
     RC(ln2(".norm1", dc, hc));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
-        a[k] = lin(hc[k], D, W(c, p[k] + ".attn.qkv.weight"), W(c, p[k] + ".attn.qkv.bias"),
+        a[k] = lin(asrc[k], D, W(c, p[k] + ".attn.qkv.weight"), W(c, p[k] + ".attn.qkv.bias"),
                    qkvc[k], 3 * D, Mv, 3 * D, D, 0);
+        lnset(a[k], k);
         if (rope) with_rope(a[k], c, 2 * D);
       }
-      RC(run2(c, a[0], a[1], aH, s));
+      RC(run2(c, a[0], a[1], al, s));
       AttnBatch ab;
       for (int k = 0; k < 2; ++k) {
         ab.g[k] = attn_args(qkvc[k], 3 * D, qkvc[k] + D, 3 * D, qkvc[k] + 2 * D, 3 * D, ac[k], D, B,
@@ -491,11 +538,12 @@ int decoder(Ctx& c, int B, hipStream_t s) {
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
-        a[k] = lin(hc[k], D, W(c, p[k] + ".cross_attn.projq.weight"),
+        a[k] = lin(asrc[k], D, W(c, p[k] + ".cross_attn.projq.weight"),
                    W(c, p[k] + ".cross_attn.projq.bias"), qc[k], D, Mv, D, D, 0);
+        lnset(a[k], k);
         if (rope) with_rope(a[k], c, D);
       }
-      RC(run2(c, a[0], a[1], aH, s));
+      RC(run2(c, a[0], a[1], al, s));
       AttnBatch ab;
       for (int k = 0; k < 2; ++k) {
         ab.g[k] = attn_args(qc[k], D, kvc[k], 2 * D, kvc[k] + D, 2 * D, ac[k], D, B, H, c.N);
@@ -515,10 +563,12 @@ int decoder(Ctx& c, int B, hipStream_t s) {
     RC(ln2(".norm2", dc, hc));
     {
       GemmArgs a[2];
-      for (int k = 0; k < 2; ++k)
-        a[k] = lin(hc[k], D, W(c, p[k] + ".mlp.fc1.weight"), W(c, p[k] + ".mlp.fc1.bias"), mc[k],
-                   f.dec_mlp, Mv, f.dec_mlp, D, EPI_GELU | (hb ? EPI_BF16OUT : 0));
-      RC(run2(c, a[0], a[1], aH, s));
+      for (int k = 0; k < 2; ++k) {
+        a[k] = lin(asrc[k], D, W(c, p[k] + ".mlp.fc1.weight"), W(c, p[k] + ".mlp.fc1.bias"),
+                   mc[k], f.dec_mlp, Mv, f.dec_mlp, D, EPI_GELU | (hb ? EPI_BF16OUT : 0));
+        lnset(a[k], k);
+      }
+      RC(run2(c, a[0], a[1], al, s));
       // the DPT hooks snapshot the state after blocks hooks[1] and hooks[2]:
       // the fc2 epilogue stores that block's output a second time
       float* hook = f.dpt_hooks[1] == l + 1 ? c.hook1 : (f.dpt_hooks[2] == l + 1 ? c.hook2 : nullptr);
@@ -949,6 +999,7 @@ int build_workspace(Ctx& c) {
       {&c.hook1, M * Dd},
       {&c.hook2, M * Dd},
       {&c.dfin, M * Dd},
+      {&c.lnst, 2 * M},
       {&c.dmem, f.composite == 1 ? M * Dd : 0},
       {&c.splitk, kSplitkElems},
       {&c.rope_cos, 512 * 16},
