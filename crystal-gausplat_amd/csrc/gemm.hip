@@ -1057,13 +1057,13 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
 #undef GS_GEMM_BF16_CASE
   bool presplit = true;
   for (int i = 0; i < b.ngroups; ++i) presplit = presplit && b.g[i].bh_plane > 0;
-  if (!bf16 && b.kernel == 4 && presplit)
+  if (!bf16 && b.kernel == 3 && presplit)
     for (int i = 0; i < b.ngroups; ++i)
       GS_REQUIRE(b.g[i].Bh && aligned16(b.g[i].Bh) && b.g[i].ldb % 8 == 0 &&
                      b.g[i].bh_plane % 8 == 0,
                  "gemm: pre-split B planes must be 16-byte aligned with ldb % 8 == 0");
 #define GS_GEMM_X6_CASE(AL, RL, NM)                                           \
-  if (!bf16 && kern == 4 && aload == AL && blayout == B_NT && a_relu == RL) { \
+  if (!bf16 && kern == 3 && aload == AL && blayout == B_NT && a_relu == RL) { \
     hipEvent_t ev = prof_start(s);                                            \
     if (presplit)                                                             \
       hipLaunchKernelGGL((gemm_x6_kernel<AL, RL, true>), grid, block, 0, s, b); \
@@ -1098,8 +1098,8 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   if (kern == 0) {
     kern = dl_ok && long_k ? 2 : 1;
   } else {
-    GS_REQUIRE(kern >= 1 && kern <= 4 && kern != 3 && !bf16, "gemm: unknown fp32 kernel request");
-    GS_REQUIRE(kern != 4 || blayout == B_NT, "gemm: the bf16x6 kernel takes NT B");
+    GS_REQUIRE(kern >= 1 && kern <= 3 && !bf16, "gemm: unknown fp32 kernel request");
+    GS_REQUIRE(kern != 3 || blayout == B_NT, "gemm: the bf16x6 kernel takes NT B");
     GS_REQUIRE(kern != 2 || dl_ok, "gemm: the direct-to-LDS kernel takes plain / concat A, NT B");
   }
 #define GS_GEMM_DL_CASE(AL)                                                   \

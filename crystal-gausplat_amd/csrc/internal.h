@@ -128,7 +128,7 @@ struct GemmBatch {
   int64_t part_ws_elems = 0;
   int32_t ksplit = 0;  // 0: chosen by launch_gemm; > 0: requested split (validated)
   // fp32 kernel: 0 chosen by launch_gemm; requested (validated): 1 register-staged,
-  // 2 direct-to-LDS, 4 bf16x6 (fp32-accurate products on bf16 matrix cores)
+  // 2 direct-to-LDS, 3 bf16x6 (fp32-accurate products on bf16 matrix cores)
   int32_t kernel = 0;
 };
 

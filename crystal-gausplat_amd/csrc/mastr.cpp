@@ -248,7 +248,7 @@ int gemm(const Ctx& c, GemmBatch& b, int aload, bool relu_in, hipStream_t s) {
   b.part_ws = c.splitk;
   b.part_ws_elems = kSplitkElems;
   if (c.cfg.precision == 2) {  // fp32 through bf16x6 split products, weights pre-split
-    b.kernel = 4;
+    b.kernel = 3;
     for (int i = 0; i < b.ngroups; ++i) {
       const char* w = (const char*)b.g[i].B;
       GS_REQUIRE(w >= c.warena && w < c.warena + c.warena_size, "gemm: weight outside the arena");

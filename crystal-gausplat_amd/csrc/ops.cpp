@@ -122,7 +122,7 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   GemmBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
-  if (x6) bt.kernel = 4;
+  if (x6) bt.kernel = 3;
   int rc = launch_gemm(bt, A_PLAIN, w_layout == 0 ? B_NT : B_NN, false, s, bf16);
   if (rc == 0 && bf16) GS_CHECK_HIP(hipStreamSynchronize(s));  // workspace reuse
   return rc;
@@ -214,7 +214,7 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   GemmBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
-  if (flags & GS_CONV_F32X6) bt.kernel = 4;
+  if (flags & GS_CONV_F32X6) bt.kernel = 3;
   int rc = launch_gemm(bt, pointwise ? A_PLAIN : A_CONV, B_NT, (flags & GS_CONV_RELU_IN) != 0, s);
   if (rc == 0 && wk != w) GS_CHECK_HIP(hipStreamSynchronize(s));  // workspace reuse
   return rc;
