@@ -426,11 +426,199 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
   }
 }
 
+// fp32 attention through bf16 matrix cores ("bf16x6", precision 2): the
+// operands of both products (Q and K for the scores, P and V for the output)
+// are split exactly into three bf16 terms x = x0 + x1 + x2 and each product
+// is accumulated in fp32 from the six term products of relative size
+// >= 2^-16 (the same scheme as gemm_x6_kernel; fp32-level accuracy). Layout
+// and softmax as attn_fwd_bf16_kernel; the K / V tiles are stored as three
+// bf16 planes each (55 KB of LDS), Q's planes stay in registers.
+__device__ __forceinline__ void split3_8(const float* v, bf16x8& h, bf16x8& m, bf16x8& l) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    h[i] = (__bf16)v[i];
+    const float r1 = v[i] - (float)h[i];
+    m[i] = (__bf16)r1;
+    l[i] = (__bf16)(r1 - (float)m[i]);
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void attn_fwd_x6_kernel(AttnBatch batch, int32_t Bcount) {
+  const int grp = blockIdx.z / Bcount;
+  const int b = blockIdx.z - grp * Bcount;
+  const AttnArgs& p = batch.g[grp];
+  const int head = blockIdx.y;
+  const int Nq = p.Nq, Nkv = p.Nkv;
+
+  __shared__ __attribute__((aligned(16))) __bf16 Ks[3][KT][HD + 8];
+  __shared__ __attribute__((aligned(16))) __bf16 Vt[3][HD][KT + 8];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hl = lane >> 5;
+
+  const float* qb = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh;
+  const float* kb = p.k + (int64_t)b * p.k_sb + (int64_t)head * p.k_sh;
+  const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)head * p.v_sh;
+  float* ob = p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh;
+
+  const int q0 = blockIdx.x * QT + wave * 32;
+  const float qscale = p.scale * 1.4426950408889634f;
+  bf16x8 qf[3][4];  // [term][16-wide head-dim slice], scaled as the fp32 kernel
+  {
+    const int qrow = min(q0 + l32, Nq - 1);
+    const float* qr = qb + (int64_t)qrow * p.q_sn + hl * 8;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const fx4 v0 = *(const fx4*)(qr + 16 * t);
+      const fx4 v1 = *(const fx4*)(qr + 16 * t + 4);
+      const float v[8] = {v0.x * qscale, v0.y * qscale, v0.z * qscale, v0.w * qscale,
+                          v1.x * qscale, v1.y * qscale, v1.z * qscale, v1.w * qscale};
+      split3_8(v, qf[0][t], qf[1][t], qf[2][t]);
+    }
+  }
+
+  floatx16 o0 = {}, o1 = {};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
+  fx4 rk[4], rv[4];
+  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+#define GS_ATT_LOAD(KB)                                                         \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i) {                               \
+    const int key = (KB) + lrow + 16 * i;                                       \
+    const int kc = min(key, Nkv - 1);                                           \
+    const fx4 kk = *(const fx4*)(kb + (int64_t)kc * p.k_sn + lc4);              \
+    const fx4 vv = *(const fx4*)(vb + (int64_t)kc * p.v_sn + lc4);              \
+    rk[i] = key < Nkv ? kk : zero4;                                             \
+    rv[i] = key < Nkv ? vv : zero4;                                             \
+  }
+// product of the three-term operands A[ta] x B[tb], smallest terms first
+#define GS_X6_MM(ACC, A, B)                                                           \
+  ACC = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[2], B[0], ACC, 0, 0, 0);           \
+  ACC = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[0], B[2], ACC, 0, 0, 0);           \
+  ACC = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[1], B[1], ACC, 0, 0, 0);           \
+  ACC = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[1], B[0], ACC, 0, 0, 0);           \
+  ACC = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[0], B[1], ACC, 0, 0, 0);           \
+  ACC = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A[0], B[0], ACC, 0, 0, 0);
+
+  GS_ATT_LOAD(0)
+  for (int kbase = 0; kbase < Nkv; kbase += KT) {
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float kv4[4] = {rk[i].x, rk[i].y, rk[i].z, rk[i].w};
+      const float vv4[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
+      const int key = lrow + 16 * i;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const __bf16 kh = (__bf16)kv4[e];
+        const float kr1 = kv4[e] - (float)kh;
+        const __bf16 km = (__bf16)kr1;
+        Ks[0][key][lc4 + e] = kh;
+        Ks[1][key][lc4 + e] = km;
+        Ks[2][key][lc4 + e] = (__bf16)(kr1 - (float)km);
+        const __bf16 vh = (__bf16)vv4[e];
+        const float vr1 = vv4[e] - (float)vh;
+        const __bf16 vm = (__bf16)vr1;
+        Vt[0][lc4 + e][key] = vh;
+        Vt[1][lc4 + e][key] = vm;
+        Vt[2][lc4 + e][key] = (__bf16)(vr1 - (float)vm);
+      }
+    }
+    __syncthreads();
+    GS_ATT_LOAD(min(kbase + KT, ((Nkv - 1) / KT) * KT))
+
+#pragma unroll
+    for (int sub = 0; sub < KT / 32; ++sub) {
+      const int sb = kbase + sub * 32;
+      if (sb >= Nkv) break;
+      floatx16 s = {};
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        bf16x8 kf[3];
+#pragma unroll
+        for (int u = 0; u < 3; ++u) kf[u] = *(const bf16x8*)&Ks[u][sub * 32 + l32][hl * 8 + 16 * t];
+        const bf16x8 qt[3] = {qf[0][t], qf[1][t], qf[2][t]};
+        GS_X6_MM(s, kf, qt)
+      }
+      if (sb + 32 > Nkv) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = sb + 8 * (r >> 2) + 4 * hl + (r & 3);
+          if (key >= Nkv) s[r] = -INFINITY;
+        }
+      }
+      float mb = s[0];
+#pragma unroll
+      for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
+      mb = fmaxf(mb, __shfl_xor(mb, 32));
+      // lazy rescaling as in attn_fwd_kernel
+      const float m_cand = fmaxf(m_run, mb);
+      if (__any(m_cand > m_run + 8.0f)) {
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
+        l_run *= alpha;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          o0[r] *= alpha;
+          o1[r] *= alpha;
+        }
+        m_run = m_cand;
+      }
+      float ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[r] = __builtin_amdgcn_exp2f(s[r] - m_run);
+        ps += s[r];
+      }
+      l_run += ps;
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+        float pv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pv[i] = s[8 * sl + i];
+        bf16x8 pb[3];
+        split3_8(pv, pb[0], pb[1], pb[2]);
+        const int k0 = sub * 32 + 16 * sl + 4 * hl;
+        bf16x8 v0[3], v1[3];
+#pragma unroll
+        for (int u = 0; u < 3; ++u) {
+          const bf16x4 va0 = *(const bf16x4*)&Vt[u][l32][k0];
+          const bf16x4 va1 = *(const bf16x4*)&Vt[u][l32][k0 + 8];
+          const bf16x4 vb0 = *(const bf16x4*)&Vt[u][32 + l32][k0];
+          const bf16x4 vb1 = *(const bf16x4*)&Vt[u][32 + l32][k0 + 8];
+          v0[u] = bf16x8{va0.x, va0.y, va0.z, va0.w, va1.x, va1.y, va1.z, va1.w};
+          v1[u] = bf16x8{vb0.x, vb0.y, vb0.z, vb0.w, vb1.x, vb1.y, vb1.z, vb1.w};
+        }
+        GS_X6_MM(o0, v0, pb)
+        GS_X6_MM(o1, v1, pb)
+      }
+    }
+  }
+#undef GS_X6_MM
+#undef GS_ATT_LOAD
+
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / l_tot;
+  const int q = q0 + l32;
+  if (q < Nq) {
+    float* orow = ob + (int64_t)q * p.o_sn;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      *(fx4*)(orow + 8 * g + 4 * hl) =
+          mk4(o0[4 * g] * inv, o0[4 * g + 1] * inv, o0[4 * g + 2] * inv, o0[4 * g + 3] * inv);
+      *(fx4*)(orow + 32 + 8 * g + 4 * hl) =
+          mk4(o1[4 * g] * inv, o1[4 * g + 1] * inv, o1[4 * g + 2] * inv, o1[4 * g + 3] * inv);
+    }
+  }
+}
+
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 }  // namespace
 
-int launch_attention(const AttnBatch& bt, hipStream_t s, bool bf16) {
+int launch_attention(const AttnBatch& bt, hipStream_t s, int prec) {
+  const bool bf16 = prec == 1, x6 = prec == 2;
   GS_REQUIRE(bt.ngroups >= 1 && bt.ngroups <= kMaxGroups, "attention: bad group count");
   const AttnArgs& a0 = bt.g[0];
   for (int i = 0; i < bt.ngroups; ++i) {
@@ -473,6 +661,8 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, bool bf16) {
   hipEvent_t ev = prof_start(s);
   if (bf16) {
     hipLaunchKernelGGL(attn_fwd_bf16_kernel, grid, block, 0, s, b, a0.B);
+  } else if (x6 && b.kv_split == 1) {
+    hipLaunchKernelGGL(attn_fwd_x6_kernel, grid, block, 0, s, b, a0.B);
   } else if (b.kv_split > 1) {
     GS_REQUIRE(aligned16(b.part_ws) && b.part_ws_elems % 4 == 0,
                "attention: scratch must be 16-byte aligned");
@@ -486,7 +676,8 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, bool bf16) {
   GS_CHECK_HIP(hipGetLastError());
   if (ev) {
     const double units = (double)a0.B * a0.H * bt.ngroups;
-    std::string nm = bf16 ? "attn_fwd_bf16_kernel" : "attn_fwd_kernel";
+    std::string nm = bf16 ? "attn_fwd_bf16_kernel"
+                          : (x6 && b.kv_split == 1 ? "attn_fwd_x6_kernel" : "attn_fwd_kernel");
     if (prof_per_shape())
       nm += " B=" + std::to_string(a0.B) + " H=" + std::to_string(a0.H) + " Nq=" +
             std::to_string(a0.Nq) + " groups=" + std::to_string(bt.ngroups) +

@@ -161,7 +161,9 @@ struct AttnBatch {
   int32_t kv_split = 0;  // 0: chosen by launch_attention; > 0: requested ranges
   int32_t kv_chunk = 0;
 };
-int launch_attention(const AttnBatch& b, hipStream_t s, bool bf16 = false);
+// prec: 0 fp32 MFMA, 1 bf16-input, 2 bf16x6 split products (fp32 accuracy;
+// launches that split the keys use the fp32 kernel)
+int launch_attention(const AttnBatch& b, hipStream_t s, int prec = 0);
 
 // ---- LayerNorm -----------------------------------------------------------------
 struct LnArgs {

@@ -263,7 +263,7 @@ int gemm(const Ctx& c, GemmBatch& b, int aload, bool relu_in, hipStream_t s) {
 int attention(const Ctx& c, AttnBatch& ab, hipStream_t s) {
   ab.part_ws = c.splitk;
   ab.part_ws_elems = kSplitkElems;
-  return launch_attention(ab, s, c.cfg.precision == 1);
+  return launch_attention(ab, s, c.cfg.precision);
 }
 
 int run1(const Ctx& c, const GemmArgs& a, int aload, hipStream_t s, bool relu_in = false) {

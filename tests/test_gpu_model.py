@@ -144,6 +144,36 @@ def test_config2_f32x6_vs_fp32():
     check_pair(outs[1], outs[0], "config2 f32x6")
 
 
+def test_batched_f32x6_vs_fp32():
+    """8 pairs at 384x512 in precision 2, where the launches are large enough
+    for the bf16x6 attention kernel as well as the bf16x6 GEMMs: every pair
+    against the fp32 MFMA path at the fp32 parity bar."""
+    case("8 pairs f32x6 vs fp32")
+    B = 8
+    n = B * 3 * 384 * 512
+    i1 = G.seed_uniform(0, "view1", n).reshape(B, 3, 384, 512)
+    i2 = G.seed_uniform(0, "view2", n).reshape(B, 3, 384, 512)
+    outs, kernels = [], None
+    for prec in (0, 2):
+        cfg = G.default_config(precision=prec)
+        m = G.Mastr(cfg, B)
+        m.init_seeded(0)
+        if prec == 2:
+            G.profile_begin()
+        outs.append(run_pair(m, cfg, i1, i2, B))
+        if prec == 2:
+            torch.cuda.synchronize()
+            kernels = G.profile_end()
+        m.close()
+        del m
+        torch.cuda.empty_cache()
+    assert any(k.startswith("attn_fwd_x6_kernel") for k in kernels), sorted(kernels)
+    assert any(k.startswith("gemm_x6_kernel") for k in kernels), sorted(kernels)
+    for b in (0, B - 1):
+        check_pair({k: v[b] for k, v in outs[1].items()}, {k: v[b] for k, v in outs[0].items()},
+                   f"8 pairs f32x6 pair {b}")
+
+
 def test_ragged_grid_split_paths(tiny_cfg):
     """A 12x26 patch grid (312 tokens) at one pair: the small launches split K
     (GEMMs) and the key range (attention, last range ragged: 312 = 4 x 64 + 56)
