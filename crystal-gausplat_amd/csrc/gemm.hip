@@ -262,7 +262,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
 
 // Global loads of one K step into registers (macros rather than lambdas so the
 // register arrays stay in VGPRs). They use the kernel's per-row state
-// (arow, aval, ohs/ows/cbase, boff/bval_, bncol/bnval).
+// (arow, aval, ohs/ows/cbase, lnm/lnr, boff, bncol).
 #define GS_LOAD_A(K0)                                                                    \
   {                                                                                      \
     const int k0_ = (K0);                                                                \
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
         ok = ok && (unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW;       \
         v = *(const fx4*)(p.A + (ok ? cbase[i] + toff : 0) + lc4);                       \
       }                                                                                  \
-      v = ok ? v : zero4;                                                                \
+      if (ALOAD == A_CONV) v = ok ? v : zero4; /* padded tap */                         \
       if (A_RELU) v = relu4(v);                                                          \
       ra[i] = v;                                                                         \
     }                                                                                    \
@@ -308,18 +308,20 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                      \
       if (BLAYOUT == B_NT) {                                                             \
         const fx4 w = *(const fx4*)(p.B + boff[i] + k0_);                                \
-        rb[i] = bval_[i] ? w : zero4;                                                    \
+        rb[i] = w;                                                                       \
       } else {                                                                           \
         const int kb = (tid >> 5) + 8 * i;                                               \
         const fx4 w = *(const fx4*)(p.B + (int64_t)(k0_ + kb) * p.ldb + bncol);          \
-        rb[i] = bnval ? w : zero4;                                                       \
+        rb[i] = w;                                                                       \
       }                                                                                  \
     }                                                                                    \
   }
 
 // Per-row load state shared by the fp32 and bf16 kernels: every address is
-// clamped into its buffer and out-of-range rows / taps are zeroed with a
-// select, so the loads of the next K step issue as one straight-line block.
+// clamped into its buffer, so the loads of the next K step issue as one
+// straight-line block. Rows past M (columns past N) then repeat the last
+// row (column): they only feed output rows (columns) that are never stored.
+// Padded conv taps are zeroed.
 #define GS_ROW_STATE()                                                                   \
   int arow[4];                                                                           \
   bool aval[4];                                                                          \
@@ -396,20 +398,16 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
 
   GS_ROW_STATE()
   int boff[4];          // B row offsets (N * ldb < 2^31 is checked on the host)
-  bool bval_[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (BLAYOUT == B_NT) {
       const int n = n0 + lrow + 32 * i;
-      bval_[i] = n < N;
       boff[i] = min(n, N - 1) * (int)p.ldb + lc4;
     }
   }
   int bncol = 0;
-  bool bnval = true;
   if (BLAYOUT == B_NN) {
     const int n = n0 + 4 * (tid & 31);
-    bnval = n < N;
     bncol = min(n, N - 4);
   }
 
@@ -637,11 +635,9 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   const __bf16* Bh = (const __bf16*)p.Bh;
   const int brow = tid >> 2, bc8 = (tid & 3) * 8;
   int bo[2];
-  bool bok[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = n0 + brow + 64 * j;
-    bok[j] = n < N;
     bo[j] = min(n, N - 1) * (int)p.ldb + bc8;
   }
 
@@ -649,7 +645,6 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   bf16x4 rah[4];  // A_PLAIN_H: bf16 A rows, stored to LDS as loaded
   bf16x8 rbh[2];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
-  const bf16x8 zero8 = {};
 
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
 
@@ -658,7 +653,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
     const __bf16* Ah = (const __bf16*)p.A;                                       \
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                              \
       const bf16x4 v = *(const bf16x4*)(Ah + (int64_t)arow[i] * p.lda + (K0) + lc4); \
-      rah[i] = aval[i] ? v : bf16x4{};                                           \
+      rah[i] = v;                                                                \
     }                                                                            \
   } else {                                                                       \
     GS_LOAD_A(K0)                                                                \
@@ -666,7 +661,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
 #define GS_LOAD_B_BF16(K0)                                                       \
   _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                \
     const bf16x8 w = *(const bf16x8*)(Bh + bo[j] + (K0));                        \
-    rbh[j] = bok[j] ? w : zero8;                                                 \
+    rbh[j] = w;                                                                  \
   }
 
   const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
@@ -728,12 +723,26 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
 // BSPLIT: B arrives pre-split (planes at Bh + t * bh_plane, same arithmetic,
 // so the products are bit-identical) and is copied into LDS as loaded.
 // Terms are accumulated smallest first.
+// Two floats to packed bf16 (round to nearest even; the instruction the
+// compiler uses for a scalar __bf16 cast, issued once per pair here).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  uint32_t r;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
 __device__ __forceinline__ void split3(const fx4& v, bf16x4& h, bf16x4& m, bf16x4& l) {
-  h = bf16x4{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
-  const fx4 r1 = v - mk4((float)h.x, (float)h.y, (float)h.z, (float)h.w);
-  m = bf16x4{(__bf16)r1.x, (__bf16)r1.y, (__bf16)r1.z, (__bf16)r1.w};
-  const fx4 r2 = r1 - mk4((float)m.x, (float)m.y, (float)m.z, (float)m.w);
-  l = bf16x4{(__bf16)r2.x, (__bf16)r2.y, (__bf16)r2.z, (__bf16)r2.w};
+  const uint32_t h0 = cvt_pk_bf16(v.x, v.y), h1 = cvt_pk_bf16(v.z, v.w);
+  const float r0 = v.x - bf16_lo(h0), r1 = v.y - bf16_hi(h0);
+  const float r2 = v.z - bf16_lo(h1), r3 = v.w - bf16_hi(h1);
+  const uint32_t m0 = cvt_pk_bf16(r0, r1), m1 = cvt_pk_bf16(r2, r3);
+  const uint32_t l0 = cvt_pk_bf16(r0 - bf16_lo(m0), r1 - bf16_hi(m0)),
+                 l1 = cvt_pk_bf16(r2 - bf16_lo(m1), r3 - bf16_hi(m1));
+  h = __builtin_bit_cast(bf16x4, (uint64_t)h0 | ((uint64_t)h1 << 32));
+  m = __builtin_bit_cast(bf16x4, (uint64_t)m0 | ((uint64_t)m1 << 32));
+  l = __builtin_bit_cast(bf16x4, (uint64_t)l0 | ((uint64_t)l1 << 32));
 }
 
 template <int ALOAD, bool A_RELU, bool BSPLIT>
@@ -759,24 +768,19 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
 
   GS_ROW_STATE()
   int boff[4];
-  bool bval_[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int n = n0 + lrow + 32 * i;
-    bval_[i] = n < N;
     boff[i] = min(n, N - 1) * (int)p.ldb + lc4;
   }
   const int bncol = 0;  // NN-layout state of the shared loader macro (unused here)
-  const bool bnval = true;
   // pre-split B: rows tid/4 + 64*j (j < 2), 8 bf16 at column 8*(tid%4) per plane
   const __bf16* Bh = (const __bf16*)p.Bh;
   const int brow = tid >> 2, bc8 = (tid & 3) * 8;
   int bo[2];
-  bool bok[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int n = n0 + brow + 64 * j;
-    bok[j] = n < N;
     bo[j] = min(n, N - 1) * (int)p.ldb + bc8;
   }
   // two register stages: the loads of K step k + 2 are issued at step k, so
@@ -785,7 +789,6 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   fx4 ra0[4], ra1[4], rb0[BSPLIT ? 1 : 4], rb1[BSPLIT ? 1 : 4];
   bf16x8 rbp0[BSPLIT ? 3 : 1][2], rbp1[BSPLIT ? 3 : 1][2];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
-  const bf16x8 zero8 = {};
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
   // loads of one K step into register stage S (0 or 1), through the shared
   // loader macros (which write ra / rb)
@@ -800,7 +803,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
       _Pragma("unroll") for (int t = 0; t < 3; ++t)                              \
       _Pragma("unroll") for (int j = 0; j < 2; ++j) {                            \
         const bf16x8 w = *(const bf16x8*)(Bh + t * p.bh_plane + bo[j] + (K0));   \
-        rbp[t][j] = bok[j] ? w : zero8;                                          \
+        rbp[t][j] = w;                                                           \
       }                                                                          \
     } else {                                                                     \
       GS_LOAD_B_F32(K0)                                                          \
