@@ -22,6 +22,7 @@
 // for the first rescale).
 #include <string>
 
+#include "bf16_split.h"
 #include "internal.h"
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -433,14 +434,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
 // >= 2^-16 (the same scheme as gemm_x6_kernel; fp32-level accuracy). Layout
 // and softmax as attn_fwd_bf16_kernel; the K / V tiles are stored as three
 // bf16 planes each (55 KB of LDS), Q's planes stay in registers.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void split3_8(const float* v, bf16x8& h, bf16x8& m, bf16x8& l) {
+  u32x4 ph, pm, pl;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    h[i] = (__bf16)v[i];
-    const float r1 = v[i] - (float)h[i];
-    m[i] = (__bf16)r1;
-    l[i] = (__bf16)(r1 - (float)m[i]);
+  for (int i = 0; i < 4; ++i) {
+    uint32_t a, b, c;
+    split3_pk(v[2 * i], v[2 * i + 1], a, b, c);
+    ph[i] = a;
+    pm[i] = b;
+    pl[i] = c;
   }
+  h = __builtin_bit_cast(bf16x8, ph);
+  m = __builtin_bit_cast(bf16x8, pm);
+  l = __builtin_bit_cast(bf16x8, pl);
 }
 
 __global__ __launch_bounds__(256, 2) void attn_fwd_x6_kernel(AttnBatch batch, int32_t Bcount) {
@@ -484,14 +491,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_x6_kernel(AttnBatch batch, in
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
   fx4 rk[4], rv[4];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+  // K rows lrow + 16 i; V rows 4 lrow + i, so each thread holds four
+  // consecutive keys of V and writes its transpose with 8-byte stores
 #define GS_ATT_LOAD(KB)                                                         \
   _Pragma("unroll") for (int i = 0; i < 4; ++i) {                               \
     const int key = (KB) + lrow + 16 * i;                                       \
     const int kc = min(key, Nkv - 1);                                           \
     const fx4 kk = *(const fx4*)(kb + (int64_t)kc * p.k_sn + lc4);              \
-    const fx4 vv = *(const fx4*)(vb + (int64_t)kc * p.v_sn + lc4);              \
     rk[i] = key < Nkv ? kk : zero4;                                             \
-    rv[i] = key < Nkv ? vv : zero4;                                             \
+    const int vkey = (KB) + 4 * lrow + i;                                       \
+    const int vc = min(vkey, Nkv - 1);                                          \
+    const fx4 vv = *(const fx4*)(vb + (int64_t)vc * p.v_sn + lc4);              \
+    rv[i] = vkey < Nkv ? vv : zero4;                                            \
   }
 // product of the three-term operands A[ta] x B[tb], smallest terms first
 #define GS_X6_MM(ACC, A, B)                                                           \
@@ -507,24 +518,24 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_x6_kernel(AttnBatch batch, in
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float kv4[4] = {rk[i].x, rk[i].y, rk[i].z, rk[i].w};
-      const float vv4[4] = {rv[i].x, rv[i].y, rv[i].z, rv[i].w};
       const int key = lrow + 16 * i;
+      uint32_t k0[3], k1[3];
+      split3_pk(rk[i].x, rk[i].y, k0[0], k0[1], k0[2]);
+      split3_pk(rk[i].z, rk[i].w, k1[0], k1[1], k1[2]);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const __bf16 kh = (__bf16)kv4[e];
-        const float kr1 = kv4[e] - (float)kh;
-        const __bf16 km = (__bf16)kr1;
-        Ks[0][key][lc4 + e] = kh;
-        Ks[1][key][lc4 + e] = km;
-        Ks[2][key][lc4 + e] = (__bf16)(kr1 - (float)km);
-        const __bf16 vh = (__bf16)vv4[e];
-        const float vr1 = vv4[e] - (float)vh;
-        const __bf16 vm = (__bf16)vr1;
-        Vt[0][lc4 + e][key] = vh;
-        Vt[1][lc4 + e][key] = vm;
-        Vt[2][lc4 + e][key] = (__bf16)(vr1 - (float)vm);
-      }
+      for (int u = 0; u < 3; ++u)
+        *(uint64_t*)&Ks[u][key][lc4] = (uint64_t)k0[u] | ((uint64_t)k1[u] << 32);
+      // V^T (head-dim major): column lc4 + i of the keys 4 lrow .. 4 lrow + 3
+      const float c0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
+      const float c1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
+      const float c2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
+      const float c3[4] = {rv[3].x, rv[3].y, rv[3].z, rv[3].w};
+      uint32_t v0[3], v1[3];
+      split3_pk(c0[i], c1[i], v0[0], v0[1], v0[2]);
+      split3_pk(c2[i], c3[i], v1[0], v1[1], v1[2]);
+#pragma unroll
+      for (int u = 0; u < 3; ++u)
+        *(uint64_t*)&Vt[u][lc4 + i][4 * lrow] = (uint64_t)v0[u] | ((uint64_t)v1[u] << 32);
     }
     __syncthreads();
     GS_ATT_LOAD(min(kbase + KT, ((Nkv - 1) / KT) * KT))

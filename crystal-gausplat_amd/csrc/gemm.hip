@@ -18,6 +18,7 @@
 #include <algorithm>
 #include <string>
 
+#include "bf16_split.h"
 #include "internal.h"
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -723,23 +724,10 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
 // BSPLIT: B arrives pre-split (planes at Bh + t * bh_plane, same arithmetic,
 // so the products are bit-identical) and is copied into LDS as loaded.
 // Terms are accumulated smallest first.
-// Two floats to packed bf16 (round to nearest even; the instruction the
-// compiler uses for a scalar __bf16 cast, issued once per pair here).
-__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
-  uint32_t r;
-  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-__device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
-
 __device__ __forceinline__ void split3(const fx4& v, bf16x4& h, bf16x4& m, bf16x4& l) {
-  const uint32_t h0 = cvt_pk_bf16(v.x, v.y), h1 = cvt_pk_bf16(v.z, v.w);
-  const float r0 = v.x - bf16_lo(h0), r1 = v.y - bf16_hi(h0);
-  const float r2 = v.z - bf16_lo(h1), r3 = v.w - bf16_hi(h1);
-  const uint32_t m0 = cvt_pk_bf16(r0, r1), m1 = cvt_pk_bf16(r2, r3);
-  const uint32_t l0 = cvt_pk_bf16(r0 - bf16_lo(m0), r1 - bf16_hi(m0)),
-                 l1 = cvt_pk_bf16(r2 - bf16_lo(m1), r3 - bf16_hi(m1));
+  uint32_t h0, m0, l0, h1, m1, l1;
+  split3_pk(v.x, v.y, h0, m0, l0);
+  split3_pk(v.z, v.w, h1, m1, l1);
   h = __builtin_bit_cast(bf16x4, (uint64_t)h0 | ((uint64_t)h1 << 32));
   m = __builtin_bit_cast(bf16x4, (uint64_t)m0 | ((uint64_t)m1 << 32));
   l = __builtin_bit_cast(bf16x4, (uint64_t)l0 | ((uint64_t)l1 << 32));
