@@ -297,8 +297,8 @@ def secondary(args):
 
 
 def fp32x6_variant(args, B, H, W):
-    """The same workload in precision 2 (fp32 GEMMs and convolutions on bf16
-    matrix cores through exact three-term splits, attention in fp32), timed
+    """The same workload in precision 2 (fp32 GEMMs, convolutions and attention
+    on bf16 matrix cores through exact three-term splits), timed
     the same way. Reported beside the fp32 headline, never as `value`."""
     import torch
 
@@ -342,9 +342,9 @@ def main():
                          "then comes from one extra eager, profiled step)")
     ap.add_argument("--precision", default="fp32", choices=["fp32", "bf16", "fp32x6"],
                     help="fp32: fp32 MFMA (the headline); bf16: bf16-input / fp32-accumulate "
-                         "variant; fp32x6: fp32 GEMMs and convolutions on bf16 matrix cores "
-                         "through exact three-term bf16 splits (six term products, fp32 "
-                         "accumulate; fp32-level accuracy), attention in fp32")
+                         "variant; fp32x6: fp32 GEMMs, convolutions and attention on bf16 "
+                         "matrix cores through exact three-term bf16 splits (six term "
+                         "products, fp32 accumulate; fp32-level accuracy)")
     ap.add_argument("--bf16", action="store_true", help="same as --precision bf16")
     ap.add_argument("--no-variants", action="store_true",
                     help="skip the fp32x6 line reported beside the fp32 headline")

@@ -239,7 +239,8 @@ typedef struct gs_mastr_config {
                             cores through exact three-term bf16 splits of
                             both operands (six term products, fp32
                             accumulate; error vs fp64 at or below the fp32
-                            MFMA kernels'), attention in fp32 MFMA
+                            MFMA kernels'), attention the same way
+                            (fp32 MFMA for launches that split the keys)
                             (linear_layout 0 only) */
   int32_t composite;     /* 0 = MASt3R composition (full DPT at image
                             resolution, 1+exp confidence, descriptors, each
