@@ -263,44 +263,54 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
 
 // Global loads of one K step into registers (macros rather than lambdas so the
 // register arrays stay in VGPRs). They use the kernel's per-row state
-// (arow, aval, ohs/ows/cbase, lnm/lnr, boff, bncol).
+// (arow, aval, ohs/ows/cbase, lnm/lnr, boff, bncol). GS_LOAD_A only issues the
+// loads (raw values into ra, the LayerNorm affine columns into lgb, the conv
+// tap validity into aok); GS_FIX_A applies the LayerNorm, the padding zeros
+// and the ReLU prologue when the step is written to LDS, so no arithmetic
+// waits on a prefetch at the point where it is issued.
 #define GS_LOAD_A(K0)                                                                    \
   {                                                                                      \
     const int k0_ = (K0);                                                                \
+    if (ALOAD == A_LN) {                                                                 \
+      lgb[0] = *(const fx4*)(p.ln_g + k0_ + lc4);                                        \
+      lgb[1] = *(const fx4*)(p.ln_b + k0_ + lc4);                                        \
+    }                                                                                    \
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                      \
-      fx4 v;                                                                             \
-      bool ok = aval[i];                                                                 \
-      if (ALOAD == A_PLAIN) {                                                            \
-        v = *(const fx4*)(p.A + (int64_t)arow[i] * p.lda + k0_ + lc4);                   \
-      } else if (ALOAD == A_LN) {                                                        \
-        const fx4 x_ = *(const fx4*)(p.A + (int64_t)arow[i] * p.lda + k0_ + lc4);        \
-        const fx4 g_ = *(const fx4*)(p.ln_g + k0_ + lc4);                                \
-        const fx4 b_ = *(const fx4*)(p.ln_b + k0_ + lc4);                                \
-        v.x = (x_.x - lnm[i]) * lnr[i] * g_.x + b_.x;                                    \
-        v.y = (x_.y - lnm[i]) * lnr[i] * g_.y + b_.y;                                    \
-        v.z = (x_.z - lnm[i]) * lnr[i] * g_.z + b_.z;                                    \
-        v.w = (x_.w - lnm[i]) * lnr[i] * g_.w + b_.w;                                    \
+      if (ALOAD == A_PLAIN || ALOAD == A_LN) {                                           \
+        ra[i] = *(const fx4*)(p.A + (int64_t)arow[i] * p.lda + k0_ + lc4);               \
       } else if (ALOAD == A_CONCAT) {                                                    \
         const bool first = k0_ < p.K1;                                                   \
         const float* base = first ? p.A : p.A2;                                          \
         const int64_t ld = first ? p.lda : p.lda2;                                       \
         const int kc = first ? k0_ : k0_ - p.K1;                                         \
-        v = *(const fx4*)(base + (int64_t)arow[i] * ld + kc + lc4);                      \
+        ra[i] = *(const fx4*)(base + (int64_t)arow[i] * ld + kc + lc4);                  \
       } else {                                                                           \
         /* tap (kh, kw), channels ic0..: one offset on the row's base; */                \
-        /* padded taps read A[lc4..] (in bounds) and are zeroed below */                 \
+        /* padded taps read A[lc4..] (in bounds) and are zeroed by GS_FIX_A */           \
         const int kk = k0_ / p.cCin;                                                     \
         const int ic0 = k0_ - kk * p.cCin;                                               \
         const int kh = kk / p.ck, kw = kk - kh * p.ck;                                   \
         const int64_t toff = ((int64_t)kh * p.cW + kw) * p.cCin + ic0;                   \
         const int ih = ohs[i] + kh, iw = ows[i] + kw;                                    \
-        ok = ok && (unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW;       \
-        v = *(const fx4*)(p.A + (ok ? cbase[i] + toff : 0) + lc4);                       \
+        const bool ok = aval[i] && (unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW; \
+        aok[i] = ok;                                                                     \
+        ra[i] = *(const fx4*)(p.A + (ok ? cbase[i] + toff : 0) + lc4);                   \
       }                                                                                  \
-      if (ALOAD == A_CONV) v = ok ? v : zero4; /* padded tap */                         \
-      if (A_RELU) v = relu4(v);                                                          \
-      ra[i] = v;                                                                         \
     }                                                                                    \
+  }
+#define GS_FIX_A()                                                                       \
+  _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                        \
+    fx4 v = ra[i];                                                                       \
+    if (ALOAD == A_LN) {                                                                 \
+      const fx4 g_ = lgb[0], b_ = lgb[1];                                                \
+      v.x = (v.x - lnm[i]) * lnr[i] * g_.x + b_.x;                                       \
+      v.y = (v.y - lnm[i]) * lnr[i] * g_.y + b_.y;                                       \
+      v.z = (v.z - lnm[i]) * lnr[i] * g_.z + b_.z;                                       \
+      v.w = (v.w - lnm[i]) * lnr[i] * g_.w + b_.w;                                       \
+    }                                                                                    \
+    if (ALOAD == A_CONV) v = aok[i] ? v : zero4; /* padded tap */                        \
+    if (A_RELU) v = relu4(v);                                                            \
+    ra[i] = v;                                                                           \
   }
 
 #define GS_LOAD_B_F32(K0)                                                                \
@@ -412,17 +422,25 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
     bncol = min(n, N - 4);
   }
 
-  fx4 ra[4], rb[4];
+  fx4 ra[4], rb[4], lgb[2];
+  bool aok[4];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
 
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
 
+  // The LayerNorm apply runs where its loads are issued (late in the MFMA
+  // phase, where the compiler places them, so its VALU work hides under the
+  // MFMAs); the conv zeroing and ReLU run at the LDS write (measured: each
+  // placement is the faster one for its loader).
+  constexpr bool fix_at_load = ALOAD == A_LN;
   // split-K: this workgroup's contiguous K range (the whole K when ksplit == 1)
   const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
   GS_LOAD_A(kbeg)
+  if (fix_at_load) GS_FIX_A()
   GS_LOAD_B_F32(kbeg)
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     __syncthreads();
+    if (!fix_at_load) GS_FIX_A()
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       *(fx4*)&As[lrow + 32 * i][lc4] = ra[i];
@@ -441,6 +459,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
     // Prefetch the next K step (the last iteration reloads its own step:
     // in bounds, and the values are never stored).
     GS_LOAD_A(min(k0 + BK, kend - BK))
+    if (fix_at_load) GS_FIX_A()
     GS_LOAD_B_F32(min(k0 + BK, kend - BK))
     const float* a0p = &As[wm * 64 + l32][hl * 16];
     const float* a1p = &As[wm * 64 + 32 + l32][hl * 16];
@@ -642,7 +661,8 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
     bo[j] = min(n, N - 1) * (int)p.ldb + bc8;
   }
 
-  fx4 ra[4];
+  fx4 ra[4], lgb[2];
+  bool aok[4];
   bf16x4 rah[4];  // A_PLAIN_H: bf16 A rows, stored to LDS as loaded
   bf16x8 rbh[2];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
@@ -670,6 +690,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   GS_LOAD_B_BF16(kbeg)
   for (int k0 = kbeg; k0 < kend; k0 += BK) {
     __syncthreads();
+    if (ALOAD != A_PLAIN_H) GS_FIX_A()
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       bf16x4 h;
@@ -774,7 +795,8 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   // two register stages: the loads of K step k + 2 are issued at step k, so
   // they have two steps of MFMA work to land (one step of this kernel is a
   // third of the fp32 kernel's MFMA time, too short to hide them alone)
-  fx4 ra0[4], ra1[4], rb0[BSPLIT ? 1 : 4], rb1[BSPLIT ? 1 : 4];
+  fx4 ra0[4], ra1[4], rb0[BSPLIT ? 1 : 4], rb1[BSPLIT ? 1 : 4], lgb0[2], lgb1[2];
+  bool aok0[4], aok1[4];
   bf16x8 rbp0[BSPLIT ? 3 : 1][2], rbp1[BSPLIT ? 3 : 1][2];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
@@ -784,7 +806,11 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   {                                                                              \
     fx4* const ra = S ? ra1 : ra0;                                               \
     fx4* const rb = S ? rb1 : rb0;                                               \
+    fx4* const lgb = S ? lgb1 : lgb0;                                            \
+    bool* const aok = S ? aok1 : aok0;                                           \
     (void)rb;                                                                    \
+    (void)lgb;                                                                   \
+    (void)aok;                                                                   \
     GS_LOAD_A(K0)                                                                \
     if (BSPLIT) {                                                                \
       bf16x8(*const rbp)[2] = S ? rbp1 : rbp0;                                   \
@@ -803,7 +829,12 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   {                                                                              \
     fx4* const ra = S ? ra1 : ra0;                                               \
     fx4* const rb = S ? rb1 : rb0;                                               \
+    fx4* const lgb = S ? lgb1 : lgb0;                                            \
+    bool* const aok = S ? aok1 : aok0;                                           \
+    (void)lgb;                                                                   \
+    (void)aok;                                                                   \
     __syncthreads();                                                             \
+    GS_FIX_A()                                                                   \
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                              \
       bf16x4 h, m, l;                                                            \
       split3(ra[i], h, m, l);                                                    \
