@@ -433,6 +433,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
   // MFMAs); the conv zeroing and ReLU run at the LDS write (measured: each
   // placement is the faster one for its loader).
   constexpr bool fix_at_load = ALOAD == A_LN;
+  // Where the next step's loads are issued among this step's 64 MFMAs, in
+  // groups of 16 (4 = after all of them, placed by the compiler): measured
+  // per loader on the model's shapes (conv 2 % and plain 2 % faster than at
+  // the end; concat and LayerNorm best at the compiler's placement).
+  constexpr int loadpos = ALOAD == A_CONV ? 3 : ALOAD == A_PLAIN ? 1 : 4;
   // split-K: this workgroup's contiguous K range (the whole K when ksplit == 1)
   const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
   GS_LOAD_A(kbeg)
@@ -458,9 +463,11 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
     __syncthreads();
     // Prefetch the next K step (the last iteration reloads its own step:
     // in bounds, and the values are never stored).
-    GS_LOAD_A(min(k0 + BK, kend - BK))
-    if (fix_at_load) GS_FIX_A()
-    GS_LOAD_B_F32(min(k0 + BK, kend - BK))
+    if (loadpos >= 4) {
+      GS_LOAD_A(min(k0 + BK, kend - BK))
+      if (fix_at_load) GS_FIX_A()
+      GS_LOAD_B_F32(min(k0 + BK, kend - BK))
+    }
     const float* a0p = &As[wm * 64 + l32][hl * 16];
     const float* a1p = &As[wm * 64 + 32 + l32][hl * 16];
     const float* b0p = &Bs[wn * 64 + l32][hl * 16];
@@ -481,6 +488,12 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
       GS_MFMA4(z, z)
       GS_MFMA4(w, w)
 #undef GS_MFMA4
+      if (loadpos < 4 && t4 + 1 == loadpos) {
+        __builtin_amdgcn_sched_barrier(0);
+        GS_LOAD_A(min(k0 + BK, kend - BK))
+        GS_LOAD_B_F32(min(k0 + BK, kend - BK))
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
   }
 
