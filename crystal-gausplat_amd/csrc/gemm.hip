@@ -808,8 +808,12 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   // two register stages: the loads of K step k + 2 are issued at step k, so
   // they have two steps of MFMA work to land (one step of this kernel is a
   // third of the fp32 kernel's MFMA time, too short to hide them alone)
-  fx4 ra0[4], ra1[4], rb0[BSPLIT ? 1 : 4], rb1[BSPLIT ? 1 : 4], lgb0[2], lgb1[2];
-  bool aok0[4], aok1[4];
+  fx4 ra0[4] = {}, ra1[4] = {}, rb0[BSPLIT ? 1 : 4], rb1[BSPLIT ? 1 : 4], lgb0[2] = {},
+      lgb1[2] = {};
+  bool aok0[4] = {}, aok1[4] = {};
+  // A of the next step, fixed up and split into its three planes during this
+  // step's MFMAs (so only the LDS stores remain between the barriers)
+  bf16x4 sah[4], sam[4], sal[4];
   bf16x8 rbp0[BSPLIT ? 3 : 1][2], rbp1[BSPLIT ? 3 : 1][2];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
@@ -836,26 +840,31 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
       GS_LOAD_B_F32(K0)                                                          \
     }                                                                            \
   }
-  // one K step from register stage S: split into the LDS planes, then the
-  // loads of step k0 + 2 BK into the freed stage, then the MFMAs
-#define GS_X6_STEP(S)                                                            \
+  // fix-up and split of the A values in register stage S into sah/sam/sal
+#define GS_X6_PREP(S)                                                            \
   {                                                                              \
     fx4* const ra = S ? ra1 : ra0;                                               \
-    fx4* const rb = S ? rb1 : rb0;                                               \
     fx4* const lgb = S ? lgb1 : lgb0;                                            \
     bool* const aok = S ? aok1 : aok0;                                           \
     (void)lgb;                                                                   \
     (void)aok;                                                                   \
-    __syncthreads();                                                             \
     GS_FIX_A()                                                                   \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) split3(ra[i], sah[i], sam[i], sal[i]); \
+  }
+  // one K step: the A planes split during the previous step and B's planes
+  // from register stage S into LDS, then the loads of step k0 + 2 BK into the
+  // freed stage, then the MFMAs with the split of step k0 + BK beside them
+#define GS_X6_STEP(S)                                                            \
+  {                                                                              \
+    fx4* const rb = S ? rb1 : rb0;                                               \
+    __syncthreads();                                                             \
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                              \
-      bf16x4 h, m, l;                                                            \
-      split3(ra[i], h, m, l);                                                    \
       const int sa_ = GS_X6_SW(lrow + 32 * i, lc4);                              \
-      *(bf16x4*)&As[0][lrow + 32 * i][sa_] = h;                                  \
-      *(bf16x4*)&As[1][lrow + 32 * i][sa_] = m;                                  \
-      *(bf16x4*)&As[2][lrow + 32 * i][sa_] = l;                                  \
+      *(bf16x4*)&As[0][lrow + 32 * i][sa_] = sah[i];                             \
+      *(bf16x4*)&As[1][lrow + 32 * i][sa_] = sam[i];                             \
+      *(bf16x4*)&As[2][lrow + 32 * i][sa_] = sal[i];                             \
       if (!BSPLIT) {                                                             \
+        bf16x4 h, m, l;                                                          \
         split3(rb[i], h, m, l);                                                  \
         *(bf16x4*)&Bs[0][lrow + 32 * i][sa_] = h;                                \
         *(bf16x4*)&Bs[1][lrow + 32 * i][sa_] = m;                                \
@@ -870,6 +879,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
     }                                                                            \
     __syncthreads();                                                             \
     if (k0 + 2 * BK < kend) GS_X6_LOAD(k0 + 2 * BK, S)                           \
+    GS_X6_PREP(1 - S)                                                            \
     GS_X6_MMA()                                                                  \
     k0 += BK;                                                                    \
   }
@@ -900,6 +910,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   int k0 = kbeg;
   GS_X6_LOAD(kbeg, 0)
   if (kbeg + BK < kend) GS_X6_LOAD(kbeg + BK, 1)
+  GS_X6_PREP(0)
   while (true) {
     GS_X6_STEP(0)
     if (k0 >= kend) break;
@@ -909,6 +920,7 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
 #undef GS_X6
 #undef GS_X6_MMA
 #undef GS_X6_STEP
+#undef GS_X6_PREP
 #undef GS_X6_LOAD
 #undef GS_X6_SW
   if (batch.ksplit > 1)
