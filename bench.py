@@ -23,6 +23,10 @@ Secondary workloads (each its own JSON line, not the headline metric):
   cpu         the oracle's literal reference loops on the host: config 0 at 1 and
               all threads, config 1 (24 blocks, progress on stderr) at 1 and all
               threads; config 2 extrapolated by FLOPs.
+  linear-vs-library
+              the config-3 linear shapes (bias epilogue) through gs_hip_linear
+              and through torch's fp32 F.linear (the ROCm BLAS libraries) on the
+              same device tensors, alternating; TFLOP/s of each and their ratio.
 """
 import argparse
 import json
@@ -175,6 +179,75 @@ def _kernel_rates(prof, steps):
             for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"])}
 
 
+# (name, M, N, K) of the config-3 linears: encoder on 2 x 16 images of 768
+# tokens, decoder per chain on 16 x 768 tokens, descriptor MLP per head
+LIBRARY_SHAPES = [("encoder fc1", 24576, 4096, 1024), ("encoder qkv", 24576, 3072, 1024),
+                  ("encoder proj", 24576, 1024, 1024), ("encoder fc2", 24576, 1024, 4096),
+                  ("decoder fc1", 12288, 3072, 768), ("decoder fc2", 12288, 768, 3072),
+                  ("decoder proj", 12288, 768, 768), ("descriptor fc2", 12288, 6144, 7168)]
+
+
+def linear_vs_library(args):
+    """Our fp32 GEMM against the vendor library on the same shapes and tensors.
+    A reference point for the kernels, not a model measurement."""
+    import torch
+
+    import gsplat_hip as G
+    torch.backends.cuda.matmul.allow_tf32 = False
+    L = G.lib()
+    stream = torch.cuda.current_stream().cuda_stream
+    reps = max(args.steps, 5)
+
+    def timed(f):
+        for _ in range(2):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    rows, t_ours, t_lib, flops = [], 0.0, 0.0, 0.0
+    for name, M, N, K in LIBRARY_SHAPES:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a = torch.rand(M, K, device="cuda", generator=g) * 2 - 1
+        w = (torch.rand(N, K, device="cuda", generator=g) * 2 - 1) * 0.02
+        b = (torch.rand(N, device="cuda", generator=g) * 2 - 1) * 0.02
+        y = torch.empty(M, N, device="cuda")
+        ours = lambda: G.check(L.gs_hip_linear(G.ptr(a), G.ptr(w), G.ptr(b), G.ptr(y), M, K, N,
+                                               0, 0, None, stream))
+        lib = lambda: torch.nn.functional.linear(a, w, b)
+        mo, ml = [], []
+        for _ in range(2):  # alternate, keep the faster of two rounds each
+            mo.append(timed(ours))
+            ml.append(timed(lib))
+        mo, ml = min(mo), min(ml)
+        # both results against an fp64 product of the same tensors
+        ref = torch.nn.functional.linear(a.double(), w.double(), b.double())
+        ours()
+        torch.cuda.synchronize()
+        scale = ref.abs().max().item()
+        err_o = (y.double() - ref).abs().max().item() / scale
+        err_l = (lib().double() - ref).abs().max().item() / scale
+        del ref
+        fl = 2.0 * M * N * K
+        t_ours, t_lib, flops = t_ours + mo, t_lib + ml, flops + fl
+        rows.append({"shape": f"{name} M={M} N={N} K={K}", "ours_tflops": round(fl / mo / 1e9, 1),
+                     "library_tflops": round(fl / ml / 1e9, 1), "ratio": round(ml / mo, 3),
+                     "max_err_vs_fp64": {"ours": float(f"{err_o:.3g}"), "library": float(f"{err_l:.3g}")}})
+        del a, w, b, y
+    return {"metric": "fp32 linear (bias) throughput, gs_hip_linear vs torch F.linear",
+            "value": round(flops / t_ours / 1e9, 1), "unit": "TFLOP/s", "n_gpus": 1,
+            "steps": reps, "warmup": 2, "higher_is_better": True, "vs_baseline": None,
+            "dtype": "f32", "data": "synthetic",
+            "library_tflops": round(flops / t_lib / 1e9, 1),
+            "ratio_ours_over_library": round(t_lib / t_ours, 3),
+            "config": {"workload": "config-3 linear shapes, one launch each"}, "shapes": rows}
+
+
 def secondary(args):
     import torch
 
@@ -241,6 +314,8 @@ def secondary(args):
         return out
     if args.workload == "cpu":
         return cpu_table()
+    if args.workload == "linear-vs-library":
+        return linear_vs_library(args)
     if args.workload == "ref512":
         B = args.pairs or 32
         cfg = G.ref512_config()
@@ -352,7 +427,8 @@ def main():
     ap.add_argument("--per-shape", action="store_true",
                     help="also print a per-shape kernel table (stderr) from a separate step")
     ap.add_argument("--workload", default="pair",
-                    choices=["pair", "frames", "ref512", "checkpoint", "block", "encoder", "cpu"])
+                    choices=["pair", "frames", "ref512", "checkpoint", "block", "encoder", "cpu",
+                             "linear-vs-library"])
     ap.add_argument("--e2e", action="store_true",
                     help="pair workload: include the host->device image copies and the "
                          "device->host output copies (pinned host buffers) in the timed step")
