@@ -259,6 +259,7 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnBatch batch, int32_
 //     its 2 x 4 keys with two 8-byte loads.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, int32_t Bcount) {
   const int grp = blockIdx.z / Bcount;
@@ -289,16 +290,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
     for (int t = 0; t < 4; ++t) {
       const fx4 v0 = *(const fx4*)(qr + 16 * t);
       const fx4 v1 = *(const fx4*)(qr + 16 * t + 4);
-      bf16x8 h;
-      h[0] = (__bf16)(v0.x * qscale);
-      h[1] = (__bf16)(v0.y * qscale);
-      h[2] = (__bf16)(v0.z * qscale);
-      h[3] = (__bf16)(v0.w * qscale);
-      h[4] = (__bf16)(v1.x * qscale);
-      h[5] = (__bf16)(v1.y * qscale);
-      h[6] = (__bf16)(v1.z * qscale);
-      h[7] = (__bf16)(v1.w * qscale);
-      qf[t] = h;
+      const u32x4 h = {cvt_pk_bf16(v0.x * qscale, v0.y * qscale),
+                       cvt_pk_bf16(v0.z * qscale, v0.w * qscale),
+                       cvt_pk_bf16(v1.x * qscale, v1.y * qscale),
+                       cvt_pk_bf16(v1.z * qscale, v1.w * qscale)};
+      qf[t] = __builtin_bit_cast(bf16x8, h);
     }
   }
 
@@ -308,14 +304,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
   fx4 rk[4], rv[4];
   const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+  // K rows lrow + 16 i; V rows 4 lrow + i, so each thread holds four
+  // consecutive keys of V and writes its transpose with 8-byte stores
 #define GS_ATT_LOAD(KB)                                                         \
   _Pragma("unroll") for (int i = 0; i < 4; ++i) {                               \
     const int key = (KB) + lrow + 16 * i;                                       \
     const int kc = min(key, Nkv - 1);                                           \
     const fx4 kk = *(const fx4*)(kb + (int64_t)kc * p.k_sn + lc4);              \
-    const fx4 vv = *(const fx4*)(vb + (int64_t)kc * p.v_sn + lc4);              \
     rk[i] = key < Nkv ? kk : zero4;                                             \
-    rv[i] = key < Nkv ? vv : zero4;                                             \
+    const int vkey = (KB) + 4 * lrow + i;                                       \
+    const int vc = min(vkey, Nkv - 1);                                          \
+    const fx4 vv = *(const fx4*)(vb + (int64_t)vc * p.v_sn + lc4);              \
+    rv[i] = vkey < Nkv ? vv : zero4;                                            \
   }
 
   GS_ATT_LOAD(0)
@@ -323,17 +323,15 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      bf16x4 h;
-      h.x = (__bf16)rk[i].x;
-      h.y = (__bf16)rk[i].y;
-      h.z = (__bf16)rk[i].z;
-      h.w = (__bf16)rk[i].w;
-      *(bf16x4*)&Ks[lrow + 16 * i][lc4] = h;
-      const int key = lrow + 16 * i;
-      Vt[lc4 + 0][key] = (__bf16)rv[i].x;
-      Vt[lc4 + 1][key] = (__bf16)rv[i].y;
-      Vt[lc4 + 2][key] = (__bf16)rv[i].z;
-      Vt[lc4 + 3][key] = (__bf16)rv[i].w;
+      *(uint64_t*)&Ks[lrow + 16 * i][lc4] =
+          (uint64_t)cvt_pk_bf16(rk[i].x, rk[i].y) | ((uint64_t)cvt_pk_bf16(rk[i].z, rk[i].w) << 32);
+      // V^T (head-dim major): column lc4 + i of the keys 4 lrow .. 4 lrow + 3
+      const float c0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
+      const float c1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
+      const float c2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
+      const float c3[4] = {rv[3].x, rv[3].y, rv[3].z, rv[3].w};
+      *(uint64_t*)&Vt[lc4 + i][4 * lrow] =
+          (uint64_t)cvt_pk_bf16(c0[i], c1[i]) | ((uint64_t)cvt_pk_bf16(c2[i], c3[i]) << 32);
     }
     __syncthreads();
     GS_ATT_LOAD(min(kbase + KT, ((Nkv - 1) / KT) * KT))
@@ -384,9 +382,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
       l_run += ps;
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl) {
-        bf16x8 pb;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pb[i] = (__bf16)s[8 * sl + i];
+        const u32x4 pp = {cvt_pk_bf16(s[8 * sl], s[8 * sl + 1]), cvt_pk_bf16(s[8 * sl + 2], s[8 * sl + 3]),
+                          cvt_pk_bf16(s[8 * sl + 4], s[8 * sl + 5]), cvt_pk_bf16(s[8 * sl + 6], s[8 * sl + 7])};
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, pp);
         const int k0 = sub * 32 + 16 * sl + 4 * hl;
         const bf16x4 va0 = *(const bf16x4*)&Vt[l32][k0];
         const bf16x4 va1 = *(const bf16x4*)&Vt[l32][k0 + 8];
@@ -434,7 +432,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
 // >= 2^-16 (the same scheme as gemm_x6_kernel; fp32-level accuracy). Layout
 // and softmax as attn_fwd_bf16_kernel; the K / V tiles are stored as three
 // bf16 planes each (55 KB of LDS), Q's planes stay in registers.
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ void split3_8(const float* v, bf16x8& h, bf16x8& m, bf16x8& l) {
   u32x4 ph, pm, pl;
 #pragma unroll

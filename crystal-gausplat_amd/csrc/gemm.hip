@@ -717,6 +717,13 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   }
 
   constexpr int SK = BK * KC;
+  // Where the next step's loads are issued among this step's 2 KC groups of
+  // four MFMAs (0 = before the first): measured per loader at config 4
+  // (plain rows after the first group: fp32 rows 14 %, bf16 rows 1 % faster;
+  // conv after the third, concat before the first). Clamped to the last
+  // group, so every step issues its prefetch.
+  constexpr int lp_want = ALOAD == A_CONV ? 3 : (ALOAD == A_PLAIN || ALOAD == A_PLAIN_H) ? 1 : 0;
+  constexpr int loadpos = lp_want < 2 * KC ? lp_want : 2 * KC - 1;
   const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
   GS_LOAD_STEP(kbeg)
   for (int k0 = kbeg; k0 < kend; k0 += SK) {
@@ -746,11 +753,16 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
       for (int j = 0; j < 2; ++j) *(bf16x8*)&Bs[brow + 64 * j][BK * c + bc8] = rbhc[c][j];
     }
     __syncthreads();
-    GS_LOAD_STEP(min(k0 + SK, kend - SK))
+    if (loadpos == 0) GS_LOAD_STEP(min(k0 + SK, kend - SK))
 #pragma unroll
     for (int c = 0; c < KC; ++c)
 #pragma unroll
     for (int sl = 0; sl < 2; ++sl) {
+      if (loadpos > 0 && 2 * c + sl == loadpos) {
+        __builtin_amdgcn_sched_barrier(0);
+        GS_LOAD_STEP(min(k0 + SK, kend - SK))
+        __builtin_amdgcn_sched_barrier(0);
+      }
       const int kc = BK * c + sl * 16 + hl * 8;
       const bf16x8 a0 = *(const bf16x8*)&As[wm * 64 + l32][kc];
       const bf16x8 a1 = *(const bf16x8*)&As[wm * 64 + 32 + l32][kc];
