@@ -88,6 +88,13 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmArgs& p, const floatx1
     const int col = n0 + wn * 64 + bj * 32 + l32;
     bval[bj] = (flags & EPI_BIAS) ? p.bias[min(col, N - 1)] : 0.f;
   }
+  // RoPE positions: when the tokens per image and the grid width are
+  // multiples of 4, the 4 consecutive rows of a lane's row group (first row a
+  // multiple of 4) lie in one image and one grid row at consecutive columns,
+  // so the row -> (y, x) decode runs once per group
+  const bool rope_fast = ROPE && (p.tok_per_img & 3) == 0 && (p.grid_w & 3) == 0;
+  const float rtok = ROPE ? 1.0f / (float)p.tok_per_img : 0.f;
+  const float rgw = ROPE ? 1.0f / (float)p.grid_w : 0.f;
 #pragma unroll
   for (int bi = 0; bi < 2; ++bi) {
 #pragma unroll
@@ -107,12 +114,50 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmArgs& p, const floatx1
         sc_j = s - sc_i * p.sc_r;
       }
       // Half a block (8 rows) at a time: its residuals are read into
-      // registers first (x: residual 1, y: residual 2). RoPE table reads stay
-      // in the row loop: they hit in cache, and their index arithmetic would
-      // cost more registers than it saves.
+      // registers first (x: residual 1, y: residual 2), and the RoPE table
+      // entries of its rows (cos / sin at the row's position on the block's
+      // axis, frequency l32 % 16).
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
         float x[8], y[8];
+        float rcs[8], rsn[8];
+        if (rope) {
+          const int f = l32 & 15;
+          const bool xaxis = (cblk >> 5) & 1;
+          if (rope_fast) {
+#pragma unroll
+            for (int gg = 0; gg < 2; ++gg) {
+              int tok, tx;
+              divmod_small(row0 + 8 * (2 * h + gg), p.tok_per_img, rtok, tok);
+              const int ty = divmod_small(tok, p.grid_w, rgw, tx);
+              if (xaxis) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  rcs[4 * gg + e] = p.rope_cos[(tx + e) * 16 + f];
+                  rsn[4 * gg + e] = p.rope_sin[(tx + e) * 16 + f];
+                }
+              } else {
+                const float cs = p.rope_cos[ty * 16 + f], sn = p.rope_sin[ty * 16 + f];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                  rcs[4 * gg + e] = cs;
+                  rsn[4 * gg + e] = sn;
+                }
+              }
+            }
+          } else {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              const int r = 8 * h + u;
+              int tok, tx;
+              divmod_small(row0 + 8 * (r >> 2) + (r & 3), p.tok_per_img, rtok, tok);
+              const int ty = divmod_small(tok, p.grid_w, rgw, tx);
+              const int pos = xaxis ? tx : ty;
+              rcs[u] = p.rope_cos[pos * 16 + f];
+              rsn[u] = p.rope_sin[pos * 16 + f];
+            }
+          }
+        }
         if (flags & EPI_RES1) {
 #pragma unroll
           for (int u = 0; u < 8; ++u) {
@@ -136,14 +181,8 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmArgs& p, const floatx1
           float v = c[r];
           if (flags & EPI_BIAS) v = v + bval[bj];
           if (rope) {
-            int tok, tx;
-            divmod_small(row, p.tok_per_img, 1.0f / (float)p.tok_per_img, tok);
-            const int ty = divmod_small(tok, p.grid_w, 1.0f / (float)p.grid_w, tx);
-            const int pos = ((cblk >> 5) & 1) ? tx : ty;
-            const int f = l32 & 15;
-            const float cs = p.rope_cos[pos * 16 + f], sn = p.rope_sin[pos * 16 + f];
             const float partner = __shfl_xor(v, 16);
-            v = (l32 < 16) ? (v * cs - partner * sn) : (v * cs + partner * sn);
+            v = (l32 < 16) ? (v * rcs[u] - partner * rsn[u]) : (v * rcs[u] + partner * rsn[u]);
           }
           if (flags & EPI_GELU) v = gelu_tanh(v);
           if (flags & EPI_RELU) v = fmaxf(v, 0.f);
