@@ -220,6 +220,9 @@ __global__ __launch_bounds__(256) void head_out_kernel(const float* __restrict__
 }
 
 inline unsigned nblocks(int64_t total, int per) { return (unsigned)((total + per - 1) / per); }
+// A 1-D grid of `per` items per block must fit grid.x (callers check this
+// before nblocks, so negative sizes and wrapped block counts become errors).
+inline bool grid_fits(int64_t total, int per) { return total >= 0 && total / per < INT32_MAX; }
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 }  // namespace
@@ -260,9 +263,11 @@ int launch_layernorm(const LnBatch& bt, hipStream_t s) {
 
 int launch_unfold(const float* img, int32_t B, int32_t H, int32_t W, int32_t p,
                   float* out, hipStream_t s) {
-  GS_REQUIRE(p % 4 == 0 && H % p == 0 && W % p == 0, "unfold: H, W must be multiples of p, p % 4 == 0");
+  GS_REQUIRE(p > 0 && p % 4 == 0 && H % p == 0 && W % p == 0,
+             "unfold: H, W must be multiples of p, p % 4 == 0");
   GS_REQUIRE(aligned16(img) && aligned16(out), "unfold: operands must be 16-byte aligned");
   const int64_t total = (int64_t)B * (H / p) * (W / p) * (3 * p * p / 4);
+  GS_REQUIRE(B >= 0 && H >= 0 && W >= 0 && grid_fits(total, 256), "unfold: bad sizes");
   if (total == 0) return 0;
   hipEvent_t ev = prof_start(s);
   hipLaunchKernelGGL(unfold_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, img, B, H, W,
@@ -274,9 +279,10 @@ int launch_unfold(const float* img, int32_t B, int32_t H, int32_t W, int32_t p,
 
 int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C,
                       float* y, hipStream_t s) {
-  GS_REQUIRE(C % 4 == 0 && H > 0 && W > 0, "upsample2x: need C % 4 == 0");
+  GS_REQUIRE(C > 0 && C % 4 == 0 && H > 0 && W > 0 && B >= 0, "upsample2x: need C % 4 == 0");
   GS_REQUIRE(aligned16(x) && aligned16(y), "upsample2x: operands must be 16-byte aligned");
   const int64_t total = (int64_t)B * 4 * H * W * (C / 4);
+  GS_REQUIRE(grid_fits(total, 256), "upsample2x: too many elements");
   if (total == 0) return 0;
   hipEvent_t ev = prof_start(s);
   hipLaunchKernelGGL(upsample2x_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, x, B, H,
@@ -288,8 +294,10 @@ int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
 
 int launch_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld, int32_t grid_w,
                   const float* cos_t, const float* sin_t, hipStream_t s) {
-  GS_REQUIRE(ld >= (int64_t)H * 64 && grid_w > 0, "rope2d: bad layout");
+  GS_REQUIRE(t && B >= 0 && N >= 0 && H > 0 && ld >= (int64_t)H * 64 && grid_w > 0,
+             "rope2d: bad layout");
   const int64_t total = (int64_t)B * N * H * 32;
+  GS_REQUIRE(grid_fits(total, 256), "rope2d: too many elements");
   if (total == 0) return 0;
   hipLaunchKernelGGL(rope2d_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, t, B, N, H,
                      ld, grid_w, cos_t, sin_t);
@@ -302,7 +310,9 @@ int launch_rope_ref_token(const float* x, float* y, int32_t B, int32_t gh, int32
                           int32_t max_pos, hipStream_t s) {
   GS_REQUIRE(H > 0 && D % H == 0 && (D / H) % 2 == 0, "rope_ref_token: bad head split");
   GS_REQUIRE(gh <= max_pos && gw <= max_pos, "rope_ref_token: table too small");
+  GS_REQUIRE(B >= 0 && gh >= 0 && gw >= 0 && D > 0, "rope_ref_token: bad sizes");
   const int64_t total = (int64_t)B * gh * gw * D;
+  GS_REQUIRE(grid_fits(total, 256), "rope_ref_token: too many elements");
   if (total == 0) return 0;
   hipLaunchKernelGGL(rope_ref_token_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, x, y,
                      B, gh, gw, D, D / H, cos_t, sin_t);
@@ -314,6 +324,7 @@ int launch_head_out(const float* x, int64_t P, int32_t Cin, const float* w, cons
                     float* pts, float* conf, bool sigmoid, hipStream_t s) {
   GS_REQUIRE(Cin % 4 == 0 && Cin <= 4096, "head_out: need Cin % 4 == 0");
   GS_REQUIRE(aligned16(x), "head_out: input must be 16-byte aligned");
+  GS_REQUIRE(grid_fits(P, 256), "head_out: bad pixel count");
   if (P == 0) return 0;
   hipEvent_t ev = prof_start(s);
   if (sigmoid)

@@ -176,6 +176,7 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
              "conv2d: unknown flag");
   const int32_t Ho = (H + 2 * pad - k) / stride + 1, Wo = (W + 2 * pad - k) / stride + 1;
   GS_REQUIRE(Ho > 0 && Wo > 0, "conv2d: empty output");
+  GS_REQUIRE((int64_t)B * Ho * Wo <= INT32_MAX, "conv2d: too many output pixels");
   hipStream_t s = pick(stream);
   std::unique_lock<std::mutex> lk(g_ws_mu);
   const float* wk = w;
@@ -226,6 +227,8 @@ int32_t gs_hip_conv_transpose(const float* x, int32_t B, int32_t H, int32_t W, i
   if (ensure_device()) return -2;
   GS_REQUIRE(k > 0 && Cin % 32 == 0 && Cout % 32 == 0 && B >= 0 && H > 0 && W > 0,
              "conv_transpose: need Cin % 32 == 0 and Cout % 32 == 0");
+  GS_REQUIRE((int64_t)B * H * W <= INT32_MAX && (int64_t)k * k * Cout <= INT32_MAX,
+             "conv_transpose: too many pixels");
   hipStream_t s = pick(stream);
   std::unique_lock<std::mutex> lk(g_ws_mu);
   const int64_t N = (int64_t)k * k * Cout;

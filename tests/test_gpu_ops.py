@@ -208,6 +208,23 @@ def test_attention_rejects_bad_head_dim():
     assert rc != 0 and b"head_dim" in L().gs_hip_last_error()
 
 
+def test_elementwise_and_conv_reject_bad_sizes_without_launch():
+    # negative or oversized extents are errors on the host, before any grid is
+    # formed (a negative element count must not wrap into a huge grid)
+    case("elementwise / conv validation")
+    x = empty(64)
+    assert L().gs_hip_upsample2x(p(x), -1, 2, 2, 4, p(x), stream()) == -1
+    assert b"upsample2x" in L().gs_hip_last_error()
+    assert L().gs_hip_rope2d(p(x), 1, 4, 0, 64, 2, 100.0, stream()) == -1
+    assert b"rope2d" in L().gs_hip_last_error()
+    assert L().gs_hip_conv2d(p(x), 70000, 256, 256, 32, p(x), None, p(x), 32, 1, 1, 0, 1, 0, None,
+                             stream()) == -1
+    assert b"too many output pixels" in L().gs_hip_last_error()
+    assert L().gs_hip_conv_transpose(p(x), 70000, 256, 256, 32, p(x), None, p(x), 32, 2,
+                                     stream()) == -1
+    assert b"too many pixels" in L().gs_hip_last_error()
+
+
 # ---------------------------------------------------------------- rope
 
 
