@@ -187,36 +187,54 @@ __global__ void rope_ref_token_kernel(const float* __restrict__ x, float* __rest
 // DPT head tail: 1x1 conv Cin -> 4 (+bias), pts = ch 0..2, conf = 1 + exp(ch 3)
 // (the reference's split_output, src/mastr/decoder_v2.cr:619-655, with the
 // MASt3R confidence mapping) or, SIGMOID, the reference's own 1 / (1 + exp(-x)).
+constexpr int kHeadOutIter = 8;  // groups of 32 pixels per workgroup
+
 template <bool SIGMOID>
 __global__ __launch_bounds__(256) void head_out_kernel(const float* __restrict__ x, int64_t P,
                                                        int32_t Cin, const float* __restrict__ w,
                                                        const float* __restrict__ b,
                                                        float* __restrict__ pts,
                                                        float* __restrict__ conf) {
+  // Eight lanes share one pixel: lane `sub` reads the 16-byte channel chunks
+  // sub, sub + 8, ..., so each load instruction covers whole 128-byte lines of
+  // eight pixels. The four dot products are then summed over the eight lanes.
   extern __shared__ float ws[];  // [4][Cin]
   for (int i = threadIdx.x; i < 4 * Cin; i += blockDim.x) ws[i] = w[i];
   __syncthreads();
-  const int64_t px = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (px >= P) return;
-  const fx4* xr = (const fx4*)(x + px * Cin);
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  for (int c4 = 0; c4 < (Cin >> 2); ++c4) {
-    const fx4 v = xr[c4];
-    const float vv[4] = {v.x, v.y, v.z, v.w};
+  const int sub = threadIdx.x & 7;
+  const int n4 = Cin >> 2;
+  const fx4* w0 = (const fx4*)ws;
+  const fx4* w1 = w0 + n4;
+  const fx4* w2 = w1 + n4;
+  const fx4* w3 = w2 + n4;
+  for (int it = 0; it < kHeadOutIter; ++it) {
+    const int64_t px = ((int64_t)blockIdx.x * kHeadOutIter + it) * 32 + (threadIdx.x >> 3);
+    if (px >= P) break;  // uniform within each group of eight lanes
+    const fx4* xr = (const fx4*)(x + px * Cin);
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll 4
+    for (int c4 = sub; c4 < n4; c4 += 8) {
+      const fx4 v = xr[c4];
+      const fx4 q0 = w0[c4], q1 = w1[c4], q2 = w2[c4], q3 = w3[c4];
+      a0 += v.x * q0.x + v.y * q0.y + v.z * q0.z + v.w * q0.w;
+      a1 += v.x * q1.x + v.y * q1.y + v.z * q1.z + v.w * q1.w;
+      a2 += v.x * q2.x + v.y * q2.y + v.z * q2.z + v.w * q2.w;
+      a3 += v.x * q3.x + v.y * q3.y + v.z * q3.z + v.w * q3.w;
+    }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = c4 * 4 + u;
-      a0 += vv[u] * ws[c];
-      a1 += vv[u] * ws[Cin + c];
-      a2 += vv[u] * ws[2 * Cin + c];
-      a3 += vv[u] * ws[3 * Cin + c];
+    for (int o = 1; o < 8; o <<= 1) {  // xor 1, 2, 4 stay inside the group
+      a0 += __shfl_xor(a0, o);
+      a1 += __shfl_xor(a1, o);
+      a2 += __shfl_xor(a2, o);
+      a3 += __shfl_xor(a3, o);
+    }
+    if (sub < 3) {
+      pts[px * 3 + sub] = (sub == 0 ? a0 : sub == 1 ? a1 : a2) + b[sub];
+    } else if (sub == 3) {
+      const float raw = a3 + b[3];
+      conf[px] = SIGMOID ? 1.0f / (1.0f + expf(-raw)) : 1.0f + expf(raw);
     }
   }
-  pts[px * 3 + 0] = a0 + b[0];
-  pts[px * 3 + 1] = a1 + b[1];
-  pts[px * 3 + 2] = a2 + b[2];
-  const float raw = a3 + b[3];
-  conf[px] = SIGMOID ? 1.0f / (1.0f + expf(-raw)) : 1.0f + expf(raw);
 }
 
 inline unsigned nblocks(int64_t total, int per) { return (unsigned)((total + per - 1) / per); }
@@ -324,14 +342,14 @@ int launch_head_out(const float* x, int64_t P, int32_t Cin, const float* w, cons
                     float* pts, float* conf, bool sigmoid, hipStream_t s) {
   GS_REQUIRE(Cin % 4 == 0 && Cin <= 4096, "head_out: need Cin % 4 == 0");
   GS_REQUIRE(aligned16(x), "head_out: input must be 16-byte aligned");
-  GS_REQUIRE(grid_fits(P, 256), "head_out: bad pixel count");
+  GS_REQUIRE(grid_fits(P, 32 * kHeadOutIter), "head_out: bad pixel count");
   if (P == 0) return 0;
   hipEvent_t ev = prof_start(s);
   if (sigmoid)
-    hipLaunchKernelGGL(head_out_kernel<true>, dim3(nblocks(P, 256)), dim3(256),
+    hipLaunchKernelGGL(head_out_kernel<true>, dim3(nblocks(P, 32 * kHeadOutIter)), dim3(256),
                        4 * Cin * sizeof(float), s, x, P, Cin, w, b, pts, conf);
   else
-    hipLaunchKernelGGL(head_out_kernel<false>, dim3(nblocks(P, 256)), dim3(256),
+    hipLaunchKernelGGL(head_out_kernel<false>, dim3(nblocks(P, 32 * kHeadOutIter)), dim3(256),
                        4 * Cin * sizeof(float), s, x, P, Cin, w, b, pts, conf);
   GS_CHECK_HIP(hipGetLastError());
   prof_stop(s, ev, "head_out_kernel", 8.0 * (double)P * Cin, 4.0 * (double)P * (Cin + 4));
