@@ -105,19 +105,22 @@ __global__ void unfold_kernel(const float* __restrict__ img, int32_t B, int32_t 
 // No FMA contraction: a fused sh*oy - y0 moves the lerp weight by an ulp of
 // the source coordinate; this kernel is HBM-bound, so it keeps the plain
 // operation sequence of the CPU formula.
-__global__ void upsample2x_kernel(const float* __restrict__ x, int32_t B, int32_t H,
-                                  int32_t W, int32_t C, float* __restrict__ y) {
+__global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict__ x,
+                                                         int32_t H, int32_t W, int32_t C,
+                                                         int32_t blocks_per_row,
+                                                         float* __restrict__ y) {
 #pragma clang fp contract(off)
+  // One workgroup covers 256 consecutive float4s of one output row, so the
+  // row's source rows and weights are uniform and only the column is divided
+  // out per thread.
   const int Ho = 2 * H, Wo = 2 * W, C4 = C >> 2;
-  const int64_t total = (int64_t)B * Ho * Wo * C4;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= total) return;
-  const int c = (int)(t % C4) * 4;
-  int64_t r = t / C4;
-  const int ox = (int)(r % Wo);
-  r /= Wo;
-  const int oy = (int)(r % Ho);
-  const int b = (int)(r / Ho);
+  const int row = (int)(blockIdx.x / (uint32_t)blocks_per_row);  // b * Ho + oy
+  const int e = (int)(blockIdx.x - (uint32_t)row * blocks_per_row) * 256 + threadIdx.x;
+  if (e >= Wo * C4) return;
+  const int ox = e / C4;
+  const int c = (e - ox * C4) * 4;
+  const int b = row / Ho;
+  const int oy = row - b * Ho;
   const float sh = (float)(H - 1) / (float)(Ho - 1);
   const float sw = (float)(W - 1) / (float)(Wo - 1);
   const float fy = sh * (float)oy, fx = sw * (float)ox;
@@ -135,7 +138,7 @@ __global__ void upsample2x_kernel(const float* __restrict__ x, int32_t B, int32_
   o.y = hy * (hx * a.y + lx * bq.y) + ly * (hx * cq.y + lx * d.y);
   o.z = hy * (hx * a.z + lx * bq.z) + ly * (hx * cq.z + lx * d.z);
   o.w = hy * (hx * a.w + lx * bq.w) + ly * (hx * cq.w + lx * d.w);
-  *(fx4*)(y + t * 4) = o;
+  *(fx4*)(y + ((int64_t)row * Wo * C4 + e) * 4) = o;
 }
 
 // 2D RoPE in place; one thread per rotated pair (token, head, axis, j < 16).
@@ -299,12 +302,15 @@ int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
                       float* y, hipStream_t s) {
   GS_REQUIRE(C > 0 && C % 4 == 0 && H > 0 && W > 0 && B >= 0, "upsample2x: need C % 4 == 0");
   GS_REQUIRE(aligned16(x) && aligned16(y), "upsample2x: operands must be 16-byte aligned");
-  const int64_t total = (int64_t)B * 4 * H * W * (C / 4);
-  GS_REQUIRE(grid_fits(total, 256), "upsample2x: too many elements");
-  if (total == 0) return 0;
+  GS_REQUIRE((int64_t)2 * W * (C / 4) <= INT32_MAX && (int64_t)2 * B * H <= INT32_MAX,
+             "upsample2x: too many elements");
+  const int32_t blocks_per_row = (int32_t)nblocks((int64_t)2 * W * (C / 4), 256);
+  const int64_t nblk = (int64_t)2 * B * H * blocks_per_row;
+  GS_REQUIRE(nblk < INT32_MAX, "upsample2x: too many elements");
+  if (nblk == 0) return 0;
   hipEvent_t ev = prof_start(s);
-  hipLaunchKernelGGL(upsample2x_kernel, dim3(nblocks(total, 256)), dim3(256), 0, s, x, B, H,
-                     W, C, y);
+  hipLaunchKernelGGL(upsample2x_kernel, dim3((uint32_t)nblk), dim3(256), 0, s, x, H, W, C,
+                     blocks_per_row, y);
   GS_CHECK_HIP(hipGetLastError());
   prof_stop(s, ev, "upsample2x_kernel", 0.0, 4.0 * (double)B * H * W * C * 5.0);
   return 0;
