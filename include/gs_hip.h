@@ -62,8 +62,8 @@ void gs_buffer_sync(void* handle);
 void gs_buffer_copy(void* src_handle, void* dst_handle, int64_t size);
 
 /* Asynchronous host <-> device copies (no bridge counterpart: Metal's shared
- * storage needed none; SURVEY's boundary adds them for explicit device
- * memory): size bytes between host memory and the buffer at byte offset,
+ * storage needed none; discrete device memory needs explicit copies): size
+ * bytes between host memory and the buffer at byte offset,
  * enqueued on `stream` (NULL = HIP default stream). The host memory must stay
  * valid until the stream reaches the copy; pinned memory from gs_host_alloc
  * makes the copy truly asynchronous. Return 0, or -1 (bad handle / range). */
