@@ -116,3 +116,37 @@ def test_no_device_error_path():
     rc = L.gs_hip_linear(None, None, None, None, 4, 32, 32, 0, 0, None, None)
     assert rc != 0
     assert L.gs_create_buffer(16, 0) is None
+
+
+@pytest.mark.parametrize("over,msg", [
+    (dict(img_h=392), "multiple of the patch size"),
+    (dict(img_h=368), "patch grid must be even"),
+    (dict(enc_heads=15), "encoder head dim must be 64"),
+    (dict(dec_heads=13), "decoder head dim must be 64"),
+    (dict(dpt_hooks=[0, 6, 9, 11]), "hooks must be"),
+    (dict(precision=1, linear_layout=1), "precision must be"),
+    (dict(precision=3), "precision must be"),
+    (dict(rope_mode=3), "rope_mode must be"),
+    (dict(composite=2), "composite must be 0 or 1"),
+    (dict(composite=1, dpt_dims=[96, 192, 384, 512]), "dpt_dims\\[3\\] == dec_dim"),
+    (dict(enc_mlp=4004), "hidden sizes must be multiples of 32"),
+])
+def test_config_validation_before_device(over, msg):
+    """gs_hip_mastr_create validates the configuration before it touches the
+    device, so every rejection is visible without a GPU, with its reason."""
+    L = G.lib()
+    cfg = G.default_config(**over)
+    h = C.c_void_p()
+    rc = L.gs_hip_mastr_create(C.byref(cfg), 1, C.byref(h))
+    assert rc != 0 and not h.value
+    assert re.search(msg, L.gs_hip_last_error().decode()), L.gs_hip_last_error()
+
+
+def test_create_rejects_bad_arguments():
+    L = G.lib()
+    h = C.c_void_p()
+    cfg = G.default_config()
+    assert L.gs_hip_mastr_create(C.byref(cfg), 0, C.byref(h)) != 0
+    assert b"bad arguments" in L.gs_hip_last_error()
+    assert L.gs_hip_mastr_create(None, 1, C.byref(h)) != 0
+    assert L.gs_hip_mastr_create(C.byref(cfg), 1, None) != 0

@@ -381,3 +381,36 @@ def test_view_swap_symmetry_full_size():
         np.testing.assert_array_equal(a[k + "1"], b[k + "2"])
         np.testing.assert_array_equal(a[k + "2"], b[k + "1"])
     m.close()
+
+
+def test_entry_points_reject_bad_arguments(tiny_cfg):
+    """The graph entry points check batch sizes and pointers on the host and
+    return an error with its reason before any launch (batch 0, negative,
+    above the context's capacity; null images; pts without conf); the
+    context stays usable and a valid call afterwards matches the oracle."""
+    case("entry point argument checks")
+    cfg = G.default_config(**tiny_cfg)
+    w = weights_for(cfg, 0, bias_std=0.02, ln_std=0.1)
+    m = load_ctx(cfg, w, max_pairs=2)
+    H, W = cfg.img_h, cfg.img_w
+    n = 3 * H * W
+    i1 = G.seed_uniform(0, "view1", n).reshape(1, 3, H, W)
+    i2 = G.seed_uniform(0, "view2", n).reshape(1, 3, H, W)
+    d1, d2 = dev(i1), dev(i2)
+    pts, conf = empty(3, H, W, 3), empty(3, H, W, 1)
+    for B in (0, -1, 3):
+        with pytest.raises(G.GsError, match="B exceeds context capacity"):
+            m.pair(d1, d2, B, pts, conf, None, pts, conf, None, stream())
+    with pytest.raises(G.GsError, match="null image"):
+        m.pair(None, d2, 1, pts, conf, None, pts, conf, None, stream())
+    with pytest.raises(G.GsError, match="pts and conf must be given together"):
+        m.pair(d1, d2, 1, pts, None, None, None, None, None, stream())
+    N = (H // cfg.patch) * (W // cfg.patch)
+    enc = empty(5, N, cfg.enc_dim)
+    for B in (0, 5):
+        with pytest.raises(G.GsError, match="encoder: B exceeds context capacity"):
+            m.encoder(d1, B, enc, stream())
+    with pytest.raises(G.GsError, match="encoder: null argument"):
+        m.encoder(None, 1, enc, stream())
+    check_pair(run_pair(m, cfg, i1, i2, 1), O.mastr_pair(cfg.as_dict(), w, i1, i2), "after errors")
+    m.close()
