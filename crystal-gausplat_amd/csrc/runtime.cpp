@@ -7,6 +7,7 @@
 #include <hip/hip_runtime.h>
 #include <string.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
@@ -20,7 +21,9 @@ namespace {
 
 thread_local std::string t_last_error;
 std::mutex g_init_mu;
-bool g_inited = false;
+// set (release) once the device and stream are ready; read (acquire) without
+// the lock on every entry point's fast path
+std::atomic<bool> g_inited{false};
 hipStream_t g_stream = nullptr;
 int g_device = 0;
 char g_name[256] = "unavailable";
@@ -80,7 +83,7 @@ void set_error(const std::string& msg) { t_last_error = msg; }
 const char* last_error() { return t_last_error.c_str(); }
 
 int ensure_device() {
-  if (g_inited) return 0;
+  if (g_inited.load(std::memory_order_acquire)) return 0;
   return gs_init_device();
 }
 
@@ -99,7 +102,7 @@ const char* gs_hip_last_error(void) { return gs::last_error(); }
 
 int32_t gs_init_device(void) {
   std::lock_guard<std::mutex> lk(g_init_mu);
-  if (g_inited) return 0;
+  if (g_inited.load(std::memory_order_relaxed)) return 0;
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
     set_error("gs_init_device: no HIP device");
@@ -119,7 +122,7 @@ int32_t gs_init_device(void) {
     set_error("gs_init_device: stream creation failed");
     return -2;
   }
-  g_inited = true;
+  g_inited.store(true, std::memory_order_release);
   return 0;
 }
 

@@ -372,7 +372,8 @@ int32_t gs_hip_mastr_load_safetensors(void* ctx, const char* path,
  * its own stream. end synchronises those events and returns the number of
  * distinct kernels (per_shape != 0: distinct kernel + problem shape); entry i
  * gives its launches, summed event time (ms), summed algorithmic flops and
- * algorithmic HBM bytes. */
+ * algorithmic HBM bytes. The profiler state is process-wide: one thread
+ * brackets its own launches, and no other thread launches in between. */
 int32_t gs_hip_profile_begin(int32_t per_shape);
 int32_t gs_hip_profile_end(void);
 int32_t gs_hip_profile_entry(int32_t i, char* name_out, int32_t name_cap,
