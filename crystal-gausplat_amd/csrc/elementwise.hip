@@ -138,7 +138,9 @@ __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict
   o.y = hy * (hx * a.y + lx * bq.y) + ly * (hx * cq.y + lx * d.y);
   o.z = hy * (hx * a.z + lx * bq.z) + ly * (hx * cq.z + lx * d.z);
   o.w = hy * (hx * a.w + lx * bq.w) + ly * (hx * cq.w + lx * d.w);
-  *(fx4*)(y + ((int64_t)row * Wo * C4 + e) * 4) = o;
+  // the output (4x the input) is streamed out with non-temporal stores so it
+  // does not displace the source rows that neighbouring output rows re-read
+  __builtin_nontemporal_store(o, (fx4*)(y + ((int64_t)row * Wo * C4 + e) * 4));
 }
 
 // 2D RoPE in place; one thread per rotated pair (token, head, axis, j < 16).
