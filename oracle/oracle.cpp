@@ -74,8 +74,22 @@
  *                       DPT with the 365-370 residual unit, 619-655 sigmoid
  *                       confidence). Pinned: every
  *                       primitive above, view-swap symmetry with shared
- *                       decoder weights, determinism, and hand-composed
- *                       torch CPU reference of an encoder block.
+ *                       decoder weights, determinism, and compositions
+ *                       written independently from torch CPU ops: an
+ *                       encoder block, a decoder block (self-attention,
+ *                       cross-attention with norm_y on the memory and RoPE
+ *                       on its q / k, MLP), the two-chain decoder of both
+ *                       composites (memory = the other chain's previous
+ *                       state, or the own view's decoder_embed output), and
+ *                       the reference stub DPT head; float64 numpy goldens
+ *                       of the decoder block, the local-feature head and a
+ *                       full DPT head (tests/test_golden.py).
+ *   orc_set_mutation    test-only switch that plants one composition mistake
+ *                       (1 memory = the other view's decoder_embed output,
+ *                       fixed; 2 norm_y dropped; 3 no RoPE on the
+ *                       cross-attention q / k; 4 local-feature concat
+ *                       dec | enc; 5 norm2 / norm3 roles swapped) so the
+ *                       tests can show that each pin above fails on it.
  */
 #include "oracle.h"
 
@@ -330,6 +344,11 @@ extern "C" void orc_sdpa_naive(const float* q, const float* k, const float* v,
 
 static int g_naive = 0;
 extern "C" void orc_set_naive(int32_t on) { g_naive = on; }
+
+/* Planted composition mistakes, for the tests that show the decoder and
+ * local-feature pins fail on them (0 = none; see orc_set_mutation). */
+static int g_mut = 0;
+extern "C" void orc_set_mutation(int32_t m) { g_mut = m; }
 
 /* ======================================================================== */
 /* RoPE                                                                      */
@@ -670,8 +689,8 @@ void attention_core(const Ctx& c, float* qsrc, int64_t ldq, int32_t qcol,
                     float* ksrc, int64_t ldk, int32_t kcol, const float* vsrc,
                     int64_t ldv, int32_t vcol, int32_t B, int32_t Nq,
                     int32_t Nkv, int32_t H, int32_t hd, int32_t grid_w,
-                    float* out /* [B,Nq,H*hd] */) {
-  if (c.cfg->rope_mode == 1) {
+                    float* out /* [B,Nq,H*hd] */, bool rope = true) {
+  if (c.cfg->rope_mode == 1 && rope) {
     rope_cols(c, qsrc, ldq, qcol, B, Nq, H, hd, grid_w);
     rope_cols(c, ksrc, ldk, kcol, B, Nkv, H, hd, grid_w);
   }
@@ -720,6 +739,9 @@ void decoder_block(const Ctx& c, const std::string& pre, float* x,
   const int64_t M = (int64_t)B * N;
   Buf h((size_t)M * D), qkv((size_t)M * 3 * D), a((size_t)M * D), p((size_t)M * D);
   Buf ym((size_t)M * D), kk((size_t)M * D), vv((size_t)M * D), qq((size_t)M * D);
+  /* the two pre-norm names in reference roles (mutation 5 swaps them) */
+  const std::string n_cross = pre + (g_mut == 5 ? ".norm2" : ".norm3");
+  const std::string n_mlp = pre + (g_mut == 5 ? ".norm3" : ".norm2");
   /* self-attention */
   layernorm_mod(c, pre + ".norm1", x, M, D, h.data());
   linear_mod(c, pre + ".attn.qkv", h.data(), M, D, 3 * D, qkv.data(), 3);
@@ -728,17 +750,20 @@ void decoder_block(const Ctx& c, const std::string& pre, float* x,
   linear_mod(c, pre + ".attn.proj", a.data(), M, D, D, p.data());
   orc_add(x, p.data(), M * D, x);
   /* cross-attention: query norm3 (reference role naming), memory norm_y */
-  layernorm_mod(c, pre + ".norm3", x, M, D, h.data());
-  layernorm_mod(c, pre + ".norm_y", mem, M, D, ym.data());
+  layernorm_mod(c, n_cross, x, M, D, h.data());
+  if (g_mut == 2)
+    memcpy(ym.data(), mem, sizeof(float) * M * D);
+  else
+    layernorm_mod(c, pre + ".norm_y", mem, M, D, ym.data());
   linear_mod(c, pre + ".cross_attn.projq", h.data(), M, D, D, qq.data());
   linear_mod(c, pre + ".cross_attn.projk", ym.data(), M, D, D, kk.data());
   linear_mod(c, pre + ".cross_attn.projv", ym.data(), M, D, D, vv.data());
   attention_core(c, qq.data(), D, 0, kk.data(), D, 0, vv.data(), D, 0, B, N, N, H,
-                 hd, grid_w, a.data());
+                 hd, grid_w, a.data(), g_mut != 3);
   linear_mod(c, pre + ".cross_attn.proj", a.data(), M, D, D, p.data());
   orc_add(x, p.data(), M * D, x);
   /* MLP: norm2 (reference role naming) */
-  layernorm_mod(c, pre + ".norm2", x, M, D, h.data());
+  layernorm_mod(c, n_mlp, x, M, D, h.data());
   mlp_mod(c, pre + ".mlp", h.data(), M, D, cf->dec_mlp, D, p.data());
   orc_add(x, p.data(), M * D, x);
 }
@@ -900,6 +925,11 @@ void local_features(const Ctx& c, const std::string& pre, const float* enc,
   const int32_t Fo = (cf->desc_dim + 1) * r * r;
   Buf cat((size_t)M * Din), f((size_t)M * Fo);
   for (int64_t i = 0; i < M; ++i) {
+    if (g_mut == 4) { /* planted: dec | enc */
+      memcpy(&cat[i * Din], dec + i * cf->dec_dim, sizeof(float) * cf->dec_dim);
+      memcpy(&cat[i * Din + cf->dec_dim], enc + i * cf->enc_dim, sizeof(float) * cf->enc_dim);
+      continue;
+    }
     memcpy(&cat[i * Din], enc + i * cf->enc_dim, sizeof(float) * cf->enc_dim);
     memcpy(&cat[i * Din + cf->enc_dim], dec + i * cf->dec_dim, sizeof(float) * cf->dec_dim);
   }
@@ -948,8 +978,12 @@ void pair(const Ctx& c, const float* img1, const float* img2, int32_t B,
     m1 = d1;
     m2 = d2;
   }
+  if (cf->composite == 0 && g_mut == 1) { /* planted: other view, fixed */
+    m1 = d2;
+    m2 = d1;
+  }
   for (int32_t l = 0; l < cf->dec_depth; ++l) {
-    if (cf->composite == 0) {
+    if (cf->composite == 0 && g_mut != 1) {
       m1 = d2; /* each chain attends to the other view's previous state */
       m2 = d1;
     }
@@ -987,6 +1021,24 @@ extern "C" int32_t orc_encoder_block(const orc_config* cfg, const char* prefix,
                                      int32_t B, int32_t grid_h, int32_t grid_w) {
   Ctx c{cfg, wf, user};
   encoder_block(c, prefix, x, B, grid_h * grid_w, grid_w);
+  return 0;
+}
+
+extern "C" int32_t orc_decoder_block(const orc_config* cfg, const char* prefix,
+                                     orc_weight_fn wf, void* user, float* x,
+                                     const float* mem, int32_t B, int32_t grid_h,
+                                     int32_t grid_w) {
+  Ctx c{cfg, wf, user};
+  decoder_block(c, prefix, x, mem, B, grid_h * grid_w, grid_w);
+  return 0;
+}
+
+extern "C" int32_t orc_local_features(const orc_config* cfg, orc_weight_fn wf, void* user,
+                                      const char* prefix, const float* enc,
+                                      const float* dec, int32_t B, int32_t gh,
+                                      int32_t gw, float* desc) {
+  Ctx c{cfg, wf, user};
+  local_features(c, prefix, enc, dec, B, gh, gw, desc);
   return 0;
 }
 

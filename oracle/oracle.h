@@ -56,6 +56,12 @@ void orc_sdpa_naive(const float* q, const float* k, const float* v, float* o,
 /* 1: composites use the literal reference loops (orc_linear_naive,
  * orc_sdpa_naive, orc_conv2d_naive) -- the CPU-baseline configuration. */
 void orc_set_naive(int32_t on);
+/* Test-only: plant composition mistake m in the composites (0 = none):
+ * 1 cross-attention memory = the other view's decoder_embed output, fixed;
+ * 2 norm_y dropped; 3 no RoPE on the cross-attention q / k; 4 local-feature
+ * concat in dec | enc order; 5 norm2 / norm3 roles swapped. Used only to
+ * show that the composition pins fail on each. */
+void orc_set_mutation(int32_t m);
 
 /* RoPE2D tables: cos/sin[pos][j], j < hd/4, pos < max_pos. */
 void orc_rope_table(int32_t max_pos, int32_t hd, float base, float* cos_t,
@@ -137,6 +143,20 @@ typedef const float* (*orc_weight_fn)(const char* name, void* user);
 int32_t orc_encoder_block(const orc_config* cfg, const char* prefix,
                           orc_weight_fn wf, void* user, float* x, int32_t B,
                           int32_t grid_h, int32_t grid_w);
+/* One decoder block (src/mastr/decoder_v2.cr:47-63) in place on x [B,N,D];
+ * mem [B,N,D] is the cross-attention memory; prefix e.g. "dec_blocks.0". */
+int32_t orc_decoder_block(const orc_config* cfg, const char* prefix,
+                          orc_weight_fn wf, void* user, float* x,
+                          const float* mem, int32_t B, int32_t grid_h,
+                          int32_t grid_w);
+/* Local-feature head: fc2(GELU(fc1(concat(enc, dec)))) over tokens, then the
+ * pixel shuffle by `patch`, channels [0, desc_dim): enc [B,N,enc_dim],
+ * dec [B,N,dec_dim] (the dec_norm output) -> desc [B,gh*patch,gw*patch,
+ * desc_dim]; prefix e.g. "downstream_head1". */
+int32_t orc_local_features(const orc_config* cfg, orc_weight_fn wf, void* user,
+                           const char* prefix, const float* enc,
+                           const float* dec, int32_t B, int32_t gh, int32_t gw,
+                           float* desc);
 /* Full encoder: img [B,3,H,W] -> enc [B, N, enc_dim] (after enc_norm). */
 int32_t orc_encoder(const orc_config* cfg, orc_weight_fn wf, void* user,
                     const float* img, int32_t B, float* enc);

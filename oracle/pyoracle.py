@@ -78,7 +78,15 @@ _SIGS = [
                                  C.c_int32, C.c_int32, C.c_int32, vp, vp]),
     ("orc_mastr_pair_taps", C.c_int32, [C.POINTER(OrcConfig), WEIGHT_FN, vp, vp, vp, C.c_int32,
                                         vp, vp, vp, vp]),
+    ("orc_set_mutation", None, [C.c_int32]),
+    ("orc_decoder_block", C.c_int32, [C.POINTER(OrcConfig), C.c_char_p, WEIGHT_FN, vp, vp, vp,
+                                      C.c_int32, C.c_int32, C.c_int32]),
+    ("orc_local_features", C.c_int32, [C.POINTER(OrcConfig), WEIGHT_FN, vp, C.c_char_p, vp, vp,
+                                       C.c_int32, C.c_int32, C.c_int32, vp]),
 ]
+
+# Planted composition mistakes of orc_set_mutation (tests only).
+MUT_MEMORY_FIXED, MUT_NO_NORM_Y, MUT_NO_CROSS_ROPE, MUT_CONCAT_SWAP, MUT_NORM_ROLES = 1, 2, 3, 4, 5
 
 _lib = None
 
@@ -324,6 +332,47 @@ def encoder_block(cfgd, weights, prefix, x, grid_h, grid_w):
                                  grid_w)
     assert rc == 0 and not W.missing, (rc, W.missing)
     return x
+
+
+class mutation:
+    """Context manager planting composition mistake m in the oracle (tests
+    only: shows that a pin fails on that mistake)."""
+
+    def __init__(self, m):
+        self.m = m
+
+    def __enter__(self):
+        lib().orc_set_mutation(self.m)
+        return self
+
+    def __exit__(self, *exc):
+        lib().orc_set_mutation(0)
+        return False
+
+
+def decoder_block(cfgd, weights, prefix, x, mem, grid_h, grid_w):
+    cfg = config_from(cfgd)
+    W = _Weights(weights)
+    x = f32(x).copy()
+    mem = f32(mem)
+    B = x.shape[0]
+    rc = lib().orc_decoder_block(C.byref(cfg), prefix.encode(), W.cb, None, _p(x), _p(mem), B,
+                                 grid_h, grid_w)
+    assert rc == 0 and not W.missing, (rc, W.missing)
+    return x
+
+
+def local_features(cfgd, weights, prefix, enc, dec, gh, gw):
+    cfg = config_from(cfgd)
+    W = _Weights(weights)
+    enc, dec = f32(enc), f32(dec)
+    B = enc.shape[0]
+    r = cfgd["patch"]
+    desc = np.empty((B, gh * r, gw * r, cfgd["desc_dim"]), np.float32)
+    rc = lib().orc_local_features(C.byref(cfg), W.cb, None, prefix.encode(), _p(enc), _p(dec), B,
+                                  gh, gw, _p(desc))
+    assert rc == 0 and not W.missing, (rc, W.missing)
+    return desc
 
 
 def encoder(cfgd, weights, img):

@@ -181,6 +181,23 @@ int main(int argc, char** argv) {
     std::vector<float> enc(B * N * 128);
     CHECK(orc_encoder(&cfg, weight, nullptr, i1.data(), B, enc.data()) == 0);
     CHECK(finite_all(x) && finite_all(enc));
+    std::vector<float> mem(B * N * 128), desc(B * Hi * Wi * 24);
+    for (size_t i = 0; i < mem.size(); ++i) mem[i] = 0.02f * (float)(i % 89) - 0.5f;
+    CHECK(orc_decoder_block(&cfg, "dec_blocks2.2", weight, nullptr, x.data(), mem.data(), B, 4,
+                            6) == 0);
+    CHECK(orc_local_features(&cfg, weight, nullptr, "downstream_head2", enc.data(), x.data(), B,
+                             4, 6, desc.data()) == 0);
+    CHECK(finite_all(x) && finite_all(desc));
+    // every planted composition mistake runs clean too
+    for (int m = 1; m <= 5; ++m) {
+      orc_set_mutation(m);
+      std::vector<float> p1(B * Hi * Wi * 3), c1(B * Hi * Wi), d1(desc.size()), p2(p1.size()),
+          c2(c1.size()), d2(desc.size());
+      CHECK(orc_mastr_pair(&cfg, weight, nullptr, i1.data(), i2.data(), B, p1.data(), c1.data(),
+                           d1.data(), p2.data(), c2.data(), d2.data()) == 0);
+      CHECK(finite_all(d1) && finite_all(p2));
+    }
+    orc_set_mutation(0);
   }
   printf("OK\n");
   return 0;

@@ -8,8 +8,10 @@ Cases: Linear 4x8 -> 6, LayerNorm 3x16, attention 1x2x5x8, conv 1x5x7x3 -> 4
 (3x3, pad 1), RoPE2D on a 2x3 grid (one 64-dim head), GELU (tanh form), the
 linear / attention / conv cases again at shapes the device kernels take
 (K = 32, head dim 64 with 5 queries x 7 keys, Cin = 32), and
-one full DPT head on a 2x2 patch grid with the tiny test widths and seed-0
-weights of the library's generator (the generator is pinned separately by a
+one full DPT head, one decoder block (self- and cross-attention with RoPE2D,
+norm_y on the memory) and the local-feature head (concat, MLP, x16 pixel
+shuffle) on a 2x2 patch grid with the tiny test widths and seed-0 weights of
+the library's generator (the generator is pinned separately by a
 numpy restatement in tests/test_abi.py). Inputs are stored as float32 (what
 the kernels consume), expectations as float64.
 """
@@ -157,6 +159,47 @@ def dpt_head(w, pre, hooks, gh, gw, cfg):
     return out[..., :3], 1.0 + np.exp(out[..., 3:])
 
 
+def rope2d_heads(t, grid_w, H):
+    """rope2d on each 64-wide head of token-major t [N, H*64]."""
+    return np.concatenate([rope2d(t[:, 64 * h:64 * h + 64], grid_w) for h in range(H)], -1)
+
+
+def decoder_block(w, p, x, mem, H, grid_w, eps):
+    """One decoder block (src/mastr/decoder_v2.cr:47-63, reference role names)
+    with RoPE2D on q and k of the self- and the cross-attention; x, mem [N, D]
+    of one image."""
+    x, mem = f64(x), f64(mem)
+    D = x.shape[-1]
+    ln = lambda z, n: layernorm(z, w[n + ".weight"], w[n + ".bias"], eps)
+    lin = lambda z, n: linear(z, w[n + ".weight"], w[n + ".bias"])
+
+    def mha(q, k, v):
+        heads = lambda z: z.reshape(z.shape[0], H, D // H).transpose(1, 0, 2)[None]
+        o = attention(heads(rope2d_heads(q, grid_w, H)), heads(rope2d_heads(k, grid_w, H)),
+                      heads(v), (D // H) ** -0.5)
+        return o[0].transpose(1, 0, 2).reshape(-1, D)
+
+    qkv = lin(ln(x, p + ".norm1"), p + ".attn.qkv")
+    x = x + lin(mha(qkv[:, :D], qkv[:, D:2 * D], qkv[:, 2 * D:]), p + ".attn.proj")
+    hq, hm = ln(x, p + ".norm3"), ln(mem, p + ".norm_y")
+    a = mha(lin(hq, p + ".cross_attn.projq"), lin(hm, p + ".cross_attn.projk"),
+            lin(hm, p + ".cross_attn.projv"))
+    x = x + lin(a, p + ".cross_attn.proj")
+    return x + lin(gelu(lin(ln(x, p + ".norm2"), p + ".mlp.fc1")), p + ".mlp.fc2")
+
+
+def local_features(w, pre, enc, dec, gh, gw, r, C):
+    """fc2(GELU(fc1(concat(enc, dec)))) per token, pixel shuffle by r:
+    desc[r*y+i, r*x+j, c] = f[token (y, x), c*r*r + i*r + j], c < C."""
+    cat = np.concatenate([f64(enc), f64(dec)], -1)
+    h = gelu(linear(cat, w[pre + ".head_local_features.fc1.weight"],
+                    w[pre + ".head_local_features.fc1.bias"]))
+    f = linear(h, w[pre + ".head_local_features.fc2.weight"],
+               w[pre + ".head_local_features.fc2.bias"])
+    f = f[:, :C * r * r].reshape(gh, gw, C, r, r)
+    return f.transpose(0, 3, 1, 4, 2).reshape(gh * r, gw * r, C)
+
+
 def main():
     rng = np.random.default_rng(20261201)
     r32 = lambda *s: rng.standard_normal(s).astype(np.float32)
@@ -192,6 +235,13 @@ def main():
         g[f"dpt_hook{i}"] = hooks[i]
     pts, conf = dpt_head(w, "downstream_head1", hooks, gh, gw, cfg.as_dict())
     g["dpt_pts"], g["dpt_conf"] = pts, conf
+    # decoder block (both attentions with RoPE, non-trivial LayerNorm affine)
+    # and the local-feature head, on the same 2x2 grid
+    g["dec_x"], g["dec_mem"] = r32(1, gh * gw, 128), r32(1, gh * gw, 128)
+    g["dec_y"] = decoder_block(w, "dec_blocks2.1", g["dec_x"][0], g["dec_mem"][0], 2, gw, 1e-6)[None]
+    g["lf_enc"], g["lf_dec"] = r32(1, gh * gw, 128), r32(1, gh * gw, 128)
+    g["lf_desc"] = local_features(w, "downstream_head2", g["lf_enc"][0], g["lf_dec"][0], gh, gw,
+                                  16, 24)[None]
     np.savez_compressed(os.path.join(HERE, "golden.npz"), **g)
     print({k: v.shape for k, v in g.items()})
 

@@ -50,6 +50,35 @@ def test_oracle_dpt_head_2x2_grid():
     close(conf, GOLD["dpt_conf"], 1e-4, 1e-5)
 
 
+def test_oracle_decoder_block_2x2_grid():
+    """Decoder block (RoPE2D on both attentions, norm_y on the memory,
+    reference role names) against the float64 golden; each planted
+    composition mistake fails it."""
+    cfg = G.default_config(**TINY_DPT)
+    w = G.seeded_weights(cfg, 0, 0.02, 0.1)
+    d = cfg.as_dict()
+    run = lambda: O.decoder_block(d, w, "dec_blocks2.1", GOLD["dec_x"], GOLD["dec_mem"], 2, 2)
+    close(run(), GOLD["dec_y"], 1e-4, 1e-5)
+    for m in (O.MUT_NO_NORM_Y, O.MUT_NO_CROSS_ROPE, O.MUT_NORM_ROLES):
+        with O.mutation(m):
+            with pytest.raises(AssertionError):
+                close(run(), GOLD["dec_y"], 1e-4, 1e-5)
+
+
+def test_oracle_local_features_2x2_grid():
+    """Local-feature head (concat(enc, dec) -> fc1 -> GELU -> fc2 -> x16 pixel
+    shuffle -> channels 0..23) against the float64 golden; the swapped concat
+    fails it."""
+    cfg = G.default_config(**TINY_DPT)
+    w = G.seeded_weights(cfg, 0, 0.02, 0.1)
+    d = cfg.as_dict()
+    run = lambda: O.local_features(d, w, "downstream_head2", GOLD["lf_enc"], GOLD["lf_dec"], 2, 2)
+    close(run(), GOLD["lf_desc"], 1e-4, 1e-5)
+    with O.mutation(O.MUT_CONCAT_SWAP):
+        with pytest.raises(AssertionError):
+            close(run(), GOLD["lf_desc"], 1e-4, 1e-5)
+
+
 # ---- device kernels (GPU) -----------------------------------------------------
 
 @pytest.mark.gpu

@@ -284,38 +284,110 @@ def test_pixel_shuffle_and_unfold_torch():
 # ---------------------------------------------------------------- composites
 
 
-def torch_block(x, w, p, H, gw, eps):
-    """Encoder block composed from torch CPU ops (independent of the oracle)."""
+def torch_rope(z, H, gw):
+    """2D RoPE on q or k [B, N, H*64] from torch ops: per 64-wide head, dims
+    [0,32) rotate by the token's row and [32,64) by its column; pairs (j, j+16)
+    with inv_freq_j = 100^(-2j/32)."""
+    B, N, D = z.shape
+    z = z.reshape(B, N, H, 2, 2, 16).clone()
+    n = torch.arange(N)
+    pos = torch.stack([n // gw, n % gw], 1).double()  # (y, x)
+    inv = 100.0 ** (-torch.arange(16).double() * 2 / 32)
+    ang = pos[:, :, None] * inv  # N, 2, 16
+    c, s = torch.cos(ang).float(), torch.sin(ang).float()
+    a, b = z[..., 0, :], z[..., 1, :]
+    c = c[None, :, None]
+    s = s[None, :, None]
+    out = torch.stack([a * c - b * s, b * c + a * s], -2)
+    return out.reshape(B, N, D)
+
+
+def torch_mha(q, k, v, H):
+    """Heads of 64 split from token-major [B, N, H*64], SDPA, merged back."""
+    B, Nq, D = q.shape
+    sh = lambda z: z.reshape(B, z.shape[1], H, D // H).transpose(1, 2)
+    return F.scaled_dot_product_attention(sh(q), sh(k), sh(v)).transpose(1, 2).reshape(B, Nq, D)
+
+
+def _mods(w, eps):
     t = torch.from_numpy
+    ln = lambda z, n: F.layer_norm(z, (z.shape[-1],), t(w[n + ".weight"]), t(w[n + ".bias"]), eps)
+    lin = lambda z, n: F.linear(z, t(w[n + ".weight"]), t(w[n + ".bias"]))
+    return ln, lin
 
-    def rope(z):
-        B, N, D = z.shape
-        z = z.reshape(B, N, H, 2, 2, 16).clone()
-        n = torch.arange(N)
-        pos = torch.stack([n // gw, n % gw], 1).double()  # (y, x)
-        inv = 100.0 ** (-torch.arange(16).double() * 2 / 32)
-        ang = pos[:, :, None] * inv  # N, 2, 16
-        c, s = torch.cos(ang).float(), torch.sin(ang).float()
-        a, b = z[..., 0, :], z[..., 1, :]
-        c = c[None, :, None]
-        s = s[None, :, None]
-        out = torch.stack([a * c - b * s, b * c + a * s], -2)
-        return out.reshape(B, N, D)
 
+def torch_block(x, w, p, H, gw, eps):
+    """Encoder block composed from torch CPU ops (independent of the oracle),
+    src/mastr/encoder_v2.cr:38-48 with RoPE on q and k."""
+    ln, lin = _mods(w, eps)
     D = x.shape[-1]
-    xx = t(x)
-    h = F.layer_norm(xx, (D,), t(w[p + ".norm1.weight"]), t(w[p + ".norm1.bias"]), eps)
-    qkv = F.linear(h, t(w[p + ".attn.qkv.weight"]), t(w[p + ".attn.qkv.bias"]))
-    q, k, v = qkv.split(D, -1)
-    q, k = rope(q), rope(k)
-    B, N, _ = q.shape
-    sh = lambda z: z.reshape(B, N, H, 64).transpose(1, 2)
-    a = F.scaled_dot_product_attention(sh(q), sh(k), sh(v)).transpose(1, 2).reshape(B, N, D)
-    xx = xx + F.linear(a, t(w[p + ".attn.proj.weight"]), t(w[p + ".attn.proj.bias"]))
-    h = F.layer_norm(xx, (D,), t(w[p + ".norm2.weight"]), t(w[p + ".norm2.bias"]), eps)
-    m = F.gelu(F.linear(h, t(w[p + ".mlp.fc1.weight"]), t(w[p + ".mlp.fc1.bias"])),
-               approximate="tanh")
-    return (xx + F.linear(m, t(w[p + ".mlp.fc2.weight"]), t(w[p + ".mlp.fc2.bias"]))).numpy()
+    xx = torch.from_numpy(x)
+    q, k, v = lin(ln(xx, p + ".norm1"), p + ".attn.qkv").split(D, -1)
+    xx = xx + lin(torch_mha(torch_rope(q, H, gw), torch_rope(k, H, gw), v, H), p + ".attn.proj")
+    m = F.gelu(lin(ln(xx, p + ".norm2"), p + ".mlp.fc1"), approximate="tanh")
+    return (xx + lin(m, p + ".mlp.fc2")).numpy()
+
+
+def torch_decoder_block(x, mem, w, p, H, gw, eps, rope=True):
+    """One MASt3RDecoderBlock from torch CPU ops, written from
+    src/mastr/decoder_v2.cr:47-63 (reference role names: norm3 before the
+    cross-attention query, norm_y on the memory, norm2 before the MLP) with
+    RoPE2D on q and k of both attentions (the memory tokens sit on the same
+    grid). x, mem: torch [B, N, D]."""
+    ln, lin = _mods(w, eps)
+    D = x.shape[-1]
+    r = (lambda z: torch_rope(z, H, gw)) if rope else (lambda z: z)
+    q, k, v = lin(ln(x, p + ".norm1"), p + ".attn.qkv").split(D, -1)
+    x = x + lin(torch_mha(r(q), r(k), v, H), p + ".attn.proj")
+    hq, hm = ln(x, p + ".norm3"), ln(mem, p + ".norm_y")
+    q = lin(hq, p + ".cross_attn.projq")
+    k, v = lin(hm, p + ".cross_attn.projk"), lin(hm, p + ".cross_attn.projv")
+    x = x + lin(torch_mha(r(q), r(k), v, H), p + ".cross_attn.proj")
+    m = F.gelu(lin(ln(x, p + ".norm2"), p + ".mlp.fc1"), approximate="tanh")
+    return x + lin(m, p + ".mlp.fc2")
+
+
+def torch_decoder(e1, e2, w, cfg, gw):
+    """MASt3RDecoder#forward_pair (src/mastr/decoder_v2.cr:170-191) from torch
+    ops: decoder_embed, then per layer l chain 1 (dec_blocks) and chain 2
+    (dec_blocks2). composite 0: each chain's cross-attention memory is the
+    other chain's state before layer l; composite 1: its own view's
+    decoder_embed output, fixed (176-184). Returns dec_norm of both."""
+    comp = cfg.get("composite", 0)
+    eps, H = cfg["ln_eps"], cfg["dec_heads"]
+    rope = cfg["rope_mode"] == 1
+    ln, lin = _mods(w, eps)
+    d1, d2 = lin(torch.from_numpy(e1), "decoder_embed"), lin(torch.from_numpy(e2), "decoder_embed")
+    m1, m2 = d1, d2
+    for l in range(cfg["dec_depth"]):
+        if comp == 0:
+            m1, m2 = d2, d1
+        d1, d2 = (torch_decoder_block(d1, m1, w, f"dec_blocks.{l}", H, gw, eps, rope),
+                  torch_decoder_block(d2, m2, w, f"dec_blocks2.{l}", H, gw, eps, rope))
+    return ln(d1, "dec_norm").numpy(), ln(d2, "dec_norm").numpy()
+
+
+def local_features_f64(enc, dec, w, pre, gh, gw, r, C):
+    """Local-feature (descriptor) head in float64 numpy: fc2(GELU_tanh(fc1(
+    concat(enc, dec)))), then the pixel shuffle by r: desc[b, r*y+i, r*x+j, c]
+    = f[b, token (y, x), c*r*r + i*r + j], channels c < C."""
+    f64 = lambda a: np.asarray(a, np.float64)
+    W = lambda n: (f64(w[n + ".weight"]), f64(w[n + ".bias"]))
+    cat = np.concatenate([f64(enc), f64(dec)], -1)
+    w1, b1 = W(pre + ".head_local_features.fc1")
+    w2, b2 = W(pre + ".head_local_features.fc2")
+    h = cat @ w1.T + b1
+    h = 0.5 * h * (1 + np.tanh(np.sqrt(2 / np.pi) * (h + 0.044715 * h ** 3)))
+    f = h @ w2.T + b2
+    B = f.shape[0]
+    f = f[..., :C * r * r].reshape(B, gh, gw, C, r, r)
+    return f.transpose(0, 1, 4, 2, 5, 3).reshape(B, gh * r, gw * r, C)
+
+
+def max_excess(got, ref, rtol, atol):
+    """Largest |got - ref| / (atol + rtol |ref|): <= 1 means within tolerance."""
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    return float((np.abs(got - ref) / (atol + rtol * np.abs(ref))).max())
 
 
 @pytest.fixture(scope="module")
@@ -361,6 +433,95 @@ def test_oracle_thread_count_does_not_change_bits(tiny_cfg, tiny_weights):
     b = O.mastr_pair(tiny_cfg, tiny_weights, i1, i1[:, :, ::-1].copy())
     for k in a:
         np.testing.assert_array_equal(a[k], b[k])
+
+
+# Tolerances of the composition pins: oracle (fp32, serial sums) against torch
+# CPU (fp32, blocked sums) or float64 numpy, a few layers deep.
+COMP_RTOL, COMP_ATOL = 1e-4, 1e-5
+
+
+def _tiny_imgs(B=1, seed=0):
+    r = np.random.default_rng(100 + seed)
+    return (r.uniform(-1, 1, (B, 3, 64, 96)).astype(np.float32),
+            r.uniform(-1, 1, (B, 3, 64, 96)).astype(np.float32))
+
+
+@pytest.mark.parametrize("prefix", ["dec_blocks.1", "dec_blocks2.2"])
+def test_decoder_block_matches_torch_composition(tiny_cfg, tiny_weights, prefix):
+    """One decoder block of either chain (non-trivial LayerNorm affine and
+    biases) against the torch composition, with a memory unrelated to x."""
+    gh, gw, D = 4, 6, tiny_cfg["dec_dim"]
+    x, mem = rnd(2, gh * gw, D), rnd(2, gh * gw, D)
+    y = O.decoder_block(tiny_cfg, tiny_weights, prefix, x, mem, gh, gw)
+    ref = torch_decoder_block(torch.from_numpy(x), torch.from_numpy(mem), tiny_weights, prefix,
+                              tiny_cfg["dec_heads"], gw, 1e-6).numpy()
+    assert max_excess(y, ref, COMP_RTOL, COMP_ATOL) <= 1.0
+
+
+@pytest.mark.parametrize("composite", [0, 1])
+def test_decoder_pair_matches_torch_composition(tiny_cfg, tiny_weights, composite):
+    """Both decoder chains over all layers, from the oracle's own encoder taps:
+    composite 0 (memory = the other chain's previous-layer state) and
+    composite 1 (the reference's own-view decoder_embed memory)."""
+    cfg = dict(tiny_cfg) if composite == 0 else _ref_cfg(tiny_cfg)
+    i1, i2 = _tiny_imgs(2)
+    e1, e2, d1, d2 = O.mastr_pair_taps(cfg, tiny_weights, i1, i2)
+    r1, r2 = torch_decoder(e1, e2, tiny_weights, cfg, 6)
+    assert max_excess(d1, r1, COMP_RTOL, COMP_ATOL) <= 1.0
+    assert max_excess(d2, r2, COMP_RTOL, COMP_ATOL) <= 1.0
+
+
+def test_local_features_match_float64(tiny_cfg, tiny_weights):
+    """Descriptor head of the pair (concat(enc, dec_norm) -> fc1 -> GELU ->
+    fc2 -> x16 pixel shuffle -> channels 0..23) against float64 numpy, both
+    standalone and inside the full pair."""
+    i1, i2 = _tiny_imgs(1, 1)
+    e1, e2, d1, d2 = O.mastr_pair_taps(tiny_cfg, tiny_weights, i1, i2)
+    out = O.mastr_pair(tiny_cfg, tiny_weights, i1, i2, heads=False)
+    for v, e, d in ((1, e1, d1), (2, e2, d2)):
+        pre = f"downstream_head{v}"
+        ref = local_features_f64(e, d, tiny_weights, pre, 4, 6, 16, 24)
+        assert max_excess(out[f"desc{v}"], ref, COMP_RTOL, COMP_ATOL) <= 1.0
+        got = O.local_features(tiny_cfg, tiny_weights, pre, e, d, 4, 6)
+        np.testing.assert_array_equal(got, out[f"desc{v}"])
+
+
+@pytest.mark.parametrize("mut", [O.MUT_NO_NORM_Y, O.MUT_NO_CROSS_ROPE, O.MUT_NORM_ROLES])
+def test_decoder_block_pin_catches_planted_mistakes(tiny_cfg, tiny_weights, mut):
+    """The decoder-block pin fails when the oracle drops norm_y, drops RoPE on
+    the cross-attention q / k, or swaps the norm2 / norm3 roles (none of which
+    the view-swap symmetry can see)."""
+    gh, gw, D = 4, 6, tiny_cfg["dec_dim"]
+    x, mem = rnd(2, gh * gw, D), rnd(2, gh * gw, D)
+    ref = torch_decoder_block(torch.from_numpy(x), torch.from_numpy(mem), tiny_weights,
+                              "dec_blocks.1", tiny_cfg["dec_heads"], gw, 1e-6).numpy()
+    with O.mutation(mut):
+        y = O.decoder_block(tiny_cfg, tiny_weights, "dec_blocks.1", x, mem, gh, gw)
+    assert max_excess(y, ref, COMP_RTOL, COMP_ATOL) > 10.0
+    assert max_excess(O.decoder_block(tiny_cfg, tiny_weights, "dec_blocks.1", x, mem, gh, gw),
+                      ref, COMP_RTOL, COMP_ATOL) <= 1.0  # switch is off again
+
+
+def test_decoder_pair_pin_catches_fixed_memory(tiny_cfg, tiny_weights):
+    """Memory taken from the other view's decoder_embed output (fixed) instead
+    of its previous-layer state fails the two-chain pin."""
+    i1, i2 = _tiny_imgs(1, 2)
+    with O.mutation(O.MUT_MEMORY_FIXED):
+        e1, e2, d1, d2 = O.mastr_pair_taps(tiny_cfg, tiny_weights, i1, i2)
+    r1, r2 = torch_decoder(e1, e2, tiny_weights, tiny_cfg, 6)
+    assert max_excess(d1, r1, COMP_RTOL, COMP_ATOL) > 10.0
+    assert max_excess(d2, r2, COMP_RTOL, COMP_ATOL) > 10.0
+
+
+def test_local_features_pin_catches_swapped_concat(tiny_cfg, tiny_weights):
+    """concat(dec, enc) instead of concat(enc, dec) fails the descriptor pin
+    (at equal encoder and decoder widths the shapes still fit)."""
+    i1, i2 = _tiny_imgs(1, 3)
+    e1, _, d1, _ = O.mastr_pair_taps(tiny_cfg, tiny_weights, i1, i2)
+    ref = local_features_f64(e1, d1, tiny_weights, "downstream_head1", 4, 6, 16, 24)
+    with O.mutation(O.MUT_CONCAT_SWAP):
+        got = O.local_features(tiny_cfg, tiny_weights, "downstream_head1", e1, d1, 4, 6)
+    assert max_excess(got, ref, COMP_RTOL, COMP_ATOL) > 10.0
 
 
 def torch_ref_stub_head(dec, w, pre, gh, gw):
