@@ -27,6 +27,11 @@ Secondary workloads (each its own JSON line, not the headline metric):
               the config-3 linear shapes (bias epilogue) through gs_hip_linear
               and through torch's fp32 F.linear (the ROCm BLAS libraries) on the
               same device tensors, alternating; TFLOP/s of each and their ratio.
+  ref-selftest
+              the reference's own GPU micro-benchmarks (src/main.cr:860-909):
+              Linear 256x512->256, LayerNorm 256x256, MHA 2x32x64 with 4 heads
+              of 16, through the op-level C ABI; ms per iteration beside the
+              M2 Max figures the reference records (a different machine).
 """
 import argparse
 import json
@@ -94,23 +99,37 @@ def cpu_baseline():
         if n.startswith("enc_blocks.0."):
             w[n] = G.weight_values(cfg, i, int(np.prod(s))).reshape(s)
     x = G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)
-    O.set_threads(1)
     O.set_naive(True)
+    O.set_threads(0)
+    threads_all = O.lib().orc_get_threads()
     t0 = time.perf_counter()
-    O.encoder_block(cfg.as_dict(), w, "enc_blocks.0", x, 24, 32)
+    y_all = O.encoder_block(cfg.as_dict(), w, "enc_blocks.0", x, 24, 32)
+    dt_all = time.perf_counter() - t0
+    O.set_threads(1)
+    t0 = time.perf_counter()
+    y_one = O.encoder_block(cfg.as_dict(), w, "enc_blocks.0", x, 24, 32)
     dt = time.perf_counter() - t0
     O.set_naive(False)
     O.set_threads(0)
-    s_per_pair = dt * PAIR_GFLOP_384x512 / BLOCK_GFLOP
+    assert np.array_equal(y_one, y_all)  # threads split output rows only: same bits
+    ratio = PAIR_GFLOP_384x512 / BLOCK_GFLOP
+    s_per_pair = dt * ratio
     return {
         "value": 1.0 / s_per_pair,
         "unit": "pairs/s",
         "cores": 1,
         "kind": "port",
+        "value_all_cores": 1.0 / (dt_all * ratio),
+        "cores_all": threads_all,
+        "cpu": cpu_model(),
+        "logical_cpus": os.cpu_count(),
+        "extrapolation": f"measured config-0 block x {ratio:.1f} (2037.2 / 21.74 GFLOP) to one "
+                         "384x512 pair",
         "sample": (f"one config-0 ViT-L block (768 tokens, 21.74 GFLOP) through the oracle's "
-                   f"literal reference loops, 1 thread, {dt:.2f} s; extrapolated x"
-                   f"{PAIR_GFLOP_384x512 / BLOCK_GFLOP:.1f} by FLOPs to one 384x512 pair "
-                   f"({s_per_pair:.0f} s/pair); host CPU: {cpu_model()}, "
+                   f"literal reference loops: {dt:.2f} s on 1 thread, {dt_all:.3f} s on "
+                   f"{threads_all} threads (bit-identical); extrapolated x{ratio:.1f} by FLOPs "
+                   f"to one 384x512 pair ({s_per_pair:.0f} s/pair on 1 thread, "
+                   f"{dt_all * ratio:.1f} s/pair on {threads_all}); host CPU: {cpu_model()}, "
                    f"{os.cpu_count()} logical CPUs"),
     }
 
@@ -248,6 +267,102 @@ def linear_vs_library(args):
             "config": {"workload": "config-3 linear shapes, one launch each"}, "shapes": rows}
 
 
+# The reference's self-test micro-benchmarks (src/main.cr:860-909) and the
+# timings its TODO.md:111,118 records for them on an Apple M2 Max (a different
+# machine: listed beside ours, not a like-for-like comparison).
+REF_SELFTEST_M2MAX_MS = {"linear": 1.2, "layernorm": 1.3, "mha": 1.6}
+
+
+def ref_selftest(args):
+    """GPU Linear 512->256 over 256 rows, GPU LayerNorm 256 over 256 rows and
+    GPU MultiHeadAttention self-attention (2 x 32 tokens, embed 64, 4 heads of
+    16: q / k / v projections, attention, output projection) through the
+    op-level C ABI, as src/main.cr:860-909 runs them: one warm-up, then 10
+    iterations. Reported per iteration as the reference measures it (loop,
+    then one synchronisation) and with a synchronisation after every
+    iteration (the reference's Metal ops each wait for completion)."""
+    import torch
+
+    import gsplat_hip as G
+    L = G.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device="cuda").manual_seed(0)
+    rn = lambda *s: torch.randn(*s, device="cuda", generator=g)
+    P = G.ptr
+    x_lin, w_lin, b_lin = rn(256, 512), rn(256, 512) * 0.05, rn(256) * 0.05
+    y_lin = torch.empty(256, 256, device="cuda")
+    x_ln, g_ln, b_ln = rn(256, 256), torch.ones(256, device="cuda"), torch.zeros(256, device="cuda")
+    y_ln = torch.empty(256, 256, device="cuda")
+    B, N, E, H = 2, 32, 64, 4
+    x_at = rn(B, N, E)
+    Wm = {k: (rn(E, E) * 0.1, rn(E) * 0.1) for k in "qkvo"}
+    proj = {k: torch.empty(B, N, E, device="cuda") for k in "qkv"}
+    a_at, y_at = torch.empty(B, N, E, device="cuda"), torch.empty(B, N, E, device="cuda")
+    hd = E // H
+    stt = (N * E, hd, E)
+
+    def linear():
+        G.check(L.gs_hip_linear(P(x_lin), P(w_lin), P(b_lin), P(y_lin), 256, 512, 256, 0, 0, None,
+                                st))
+
+    def layernorm():
+        G.check(L.gs_hip_layernorm(P(x_ln), P(g_ln), P(b_ln), P(y_ln), 256, 256, 1e-5, st))
+
+    def mha():
+        for k in "qkv":
+            G.check(L.gs_hip_linear(P(x_at), P(Wm[k][0]), P(Wm[k][1]), P(proj[k]), B * N, E, E, 0,
+                                    0, None, st))
+        G.check(L.gs_hip_attention(P(proj["q"]), P(proj["k"]), P(proj["v"]), P(a_at), B, H, N, N,
+                                   hd, float(1.0 / hd ** 0.5), *stt, *stt, *stt, *stt, st))
+        G.check(L.gs_hip_linear(P(a_at), P(Wm["o"][0]), P(Wm["o"][1]), P(y_at), B * N, E, E, 0, 0,
+                                None, st))
+
+    iters = 10
+    res = {}
+    for name, fn, what in (("linear", linear, "Linear 256x512 -> 256 (bias)"),
+                           ("layernorm", layernorm, "LayerNorm 256 x 256"),
+                           ("mha", mha, "MultiHeadAttention self-attention 2 x 32 x 64, 4 heads "
+                                        "of 16 (3 projections, attention, output projection)")):
+        fn()  # warm-up, as the reference
+        torch.cuda.synchronize()
+        best_loop, best_sync = float("inf"), float("inf")
+        for _ in range(5):  # five repetitions of the reference's 10-iteration loop, best kept
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                fn()
+            torch.cuda.synchronize()
+            best_loop = min(best_loop, (time.perf_counter() - t0) * 1e3 / iters)
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                fn()
+                torch.cuda.synchronize()
+            best_sync = min(best_sync, (time.perf_counter() - t0) * 1e3 / iters)
+        G.profile_begin()
+        fn()
+        torch.cuda.synchronize()
+        prof = G.profile_end()
+        res[name] = {"what": what, "ms_per_iter": round(best_loop, 4),
+                     "ms_per_iter_synced": round(best_sync, 4),
+                     "kernel_ms": round(sum(v["ms"] for v in prof.values()), 4),
+                     "kernels": sorted(prof),
+                     "reference_m2max_ms_per_iter": REF_SELFTEST_M2MAX_MS[name]}
+    res["linear"]["tflops"] = round(2.0 * 256 * 512 * 256 / (res["linear"]["ms_per_iter"] * 1e-3)
+                                    / 1e12, 3)
+    return {"metric": "reference self-test GPU micro-benchmarks (src/main.cr:860-909) through "
+                      "the op-level C ABI, ms per iteration",
+            "value": round(sum(r["ms_per_iter"] for r in res.values()), 4),
+            "unit": "ms (sum of the three, per iteration)", "n_gpus": 1, "steps": iters,
+            "warmup": 1, "higher_is_better": False, "vs_baseline": None, "dtype": "f32",
+            "data": "synthetic (torch seeded normal)",
+            "config": {"workload": "ref-selftest: Linear 256x512->256, LayerNorm 256x256, MHA "
+                                   "2x32x64 with 4 heads of 16"},
+            "reference_note": "reference_m2max_ms_per_iter are the figures TODO.md:111,118 of the "
+                              "reference records on an Apple M2 Max (Metal, one synchronous "
+                              "command buffer per op): a different machine, listed beside ours "
+                              "for orientation, not a like-for-like claim",
+            "ops": res}
+
+
 def secondary(args):
     import torch
 
@@ -316,6 +431,8 @@ def secondary(args):
         return cpu_table()
     if args.workload == "linear-vs-library":
         return linear_vs_library(args)
+    if args.workload == "ref-selftest":
+        return ref_selftest(args)
     if args.workload == "ref512":
         B = args.pairs or 32
         cfg = G.ref512_config()
@@ -428,7 +545,7 @@ def main():
                     help="also print a per-shape kernel table (stderr) from a separate step")
     ap.add_argument("--workload", default="pair",
                     choices=["pair", "frames", "ref512", "checkpoint", "block", "encoder", "cpu",
-                             "linear-vs-library"])
+                             "linear-vs-library", "ref-selftest"])
     ap.add_argument("--e2e", action="store_true",
                     help="pair workload: include the host->device image copies and the "
                          "device->host output copies (pinned host buffers) in the timed step")

@@ -13,8 +13,8 @@ OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libgsplat_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "pointcloud.hip", "runtime.cpp", "seed.cpp",
-           "ops.cpp", "mastr.cpp", "safetensors.cpp"]
+SOURCES = ["gemm.hip", "attention.hip", "elementwise.hip", "pointcloud.hip", "general.hip",
+           "runtime.cpp", "seed.cpp", "ops.cpp", "mastr.cpp", "safetensors.cpp"]
 
 # Packed-fp32 VALU instructions are disabled for all device code: some of their
 # forms have given silent wrong results on the target machines.

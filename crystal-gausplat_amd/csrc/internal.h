@@ -234,6 +234,18 @@ int launch_collect_points(const float* pts, const float* conf, int64_t n, float 
                           int64_t* scratch, hipStream_t s);
 int launch_fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t s);
 
+// General-shape kernels of the op-level entry points (general.hip): attention
+// for any head_dim in [1, 128] and any strides / alignment; LayerNorm of any
+// width and alignment; a zero-padded, possibly transposing copy
+// dst[r*cp + c] = c < cols ? src[r*s_row + c*s_col] : 0; and a convolution
+// weight (OIHW layout 0 / OHWI layout 1) to OHWI with Cin padded to cp.
+int launch_attention_general(const AttnArgs& a, int32_t hd, hipStream_t s);
+int launch_layernorm_rows(const LnArgs& a, hipStream_t s);
+int launch_stage(const float* src, int64_t rows, int64_t cols, int64_t s_row, int64_t s_col,
+                 float* dst, int64_t cp, hipStream_t s);
+int launch_conv_weight_stage(const float* w, int32_t Cout, int32_t Cin, int32_t k, int32_t layout,
+                             int32_t cp, float* out, hipStream_t s);
+
 // Configuration of a MASt3R context created by gs_hip_mastr_create.
 const ::gs_mastr_config* mastr_ctx_config(void* ctx);
 

@@ -17,26 +17,29 @@ namespace {
 
 hipStream_t pick(void* stream) { return (hipStream_t)stream; }
 
-// Library-owned scratch for weight re-layouts of the op-level entry points
-// (one per process; calls that need it are serialised by the mutex).
-std::mutex g_ws_mu;
-void* g_ws = nullptr;
-size_t g_ws_size = 0;
-
-int workspace(size_t bytes, void** out) {
-  if (bytes > g_ws_size) {
-    if (g_ws) {
-      GS_CHECK_HIP(hipDeviceSynchronize());
-      GS_CHECK_HIP(hipFree(g_ws));
-      g_ws = nullptr;
-      g_ws_size = 0;
-    }
-    GS_CHECK_HIP(hipMalloc(&g_ws, bytes));
-    g_ws_size = bytes;
+// Scratch of one op-level call (weight re-layouts, zero-padded operand copies,
+// compaction block counts): allocated on the call's stream and released on it
+// after the kernels that use it (stream-ordered allocation). Calls on
+// different streams never share scratch and no call waits for the device.
+class StreamScratch {
+ public:
+  ~StreamScratch() {
+    if (p_) (void)hipFreeAsync(p_, s_);
   }
-  *out = g_ws;
-  return 0;
-}
+  int alloc(size_t bytes, hipStream_t s) {
+    s_ = s;
+    GS_CHECK_HIP(hipMallocAsync(&p_, bytes ? bytes : 16, s));
+    return 0;
+  }
+  char* get() const { return (char*)p_; }
+
+ private:
+  void* p_ = nullptr;
+  hipStream_t s_ = nullptr;
+};
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 
 // RoPE tables [512][16] per base, uploaded once.
 std::mutex g_rope_mu;
@@ -62,11 +65,6 @@ int rope_tables(float base, const float** c, const float** s) {
   return 0;
 }
 
-// Block-count scratch of gs_hip_collect_points (grown on demand).
-std::mutex g_cp_mu;
-int64_t* g_cp = nullptr;
-int64_t g_cp_n = 0;
-
 GemmArgs blank_args() {
   GemmArgs a;
   memset(&a, 0, sizeof(a));
@@ -83,6 +81,8 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   if (ensure_device()) return -2;
   GS_REQUIRE(w_layout == 0 || w_layout == 1, "linear: w_layout must be 0 or 1");
   GS_REQUIRE(M >= 0 && M <= INT32_MAX, "linear: M out of range");
+  GS_REQUIRE(K > 0 && N > 0, "linear: K and N must be positive");
+  GS_REQUIRE(x && w && y, "linear: null operand");
   GS_REQUIRE((epilogue & ~(GS_EPI_GELU | GS_EPI_RESIDUAL | GS_EPI_RELU | GS_EPI_BF16 |
                           GS_EPI_F32X6)) == 0,
              "linear: unknown epilogue flag");
@@ -92,49 +92,90 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   const bool bf16 = (epilogue & GS_EPI_BF16) != 0;
   GS_REQUIRE(!bf16 || w_layout == 0, "linear: the bf16 variant needs w_layout 0");
   GS_REQUIRE(!(epilogue & GS_EPI_RESIDUAL) || residual, "linear: residual flag without residual");
+  if (M == 0) return 0;
+  hipStream_t s = pick(stream);
+  // The MFMA GEMM takes K in steps of 32 from 16-byte aligned rows. Other
+  // shapes (the reference's linear_forward takes any width) run on
+  // zero-padded copies: x -> [M, Kp], W -> [N, Kp] (NT, either layout); the
+  // padded products are exact zeros, so the sums are those of the K terms.
+  const bool kfit = K % 32 == 0;
+  const bool stage_a = !kfit || !aligned16(x);
+  const bool stage_b = !kfit || !aligned16(w) || (w_layout == 1 && N % 4 != 0);
+  const int64_t Kp = round_up(K, 32);
+  // scratch: [staged x | staged W | bf16 copy of W], each part 256-byte aligned
+  const int64_t a_bytes = stage_a ? M * Kp * 4 : 0;
+  const int64_t b_bytes = stage_b ? (int64_t)N * Kp * 4 : 0;
+  const int64_t h_bytes = bf16 ? (int64_t)N * Kp * 2 : 0;
+  const int64_t off_b = round_up(a_bytes, 256), off_h = round_up(off_b + b_bytes, 256);
+  StreamScratch ws;
+  if (off_h + h_bytes > 0) {
+    int rc = ws.alloc((size_t)(off_h + h_bytes), s);
+    if (rc) return rc;
+  }
+  const float* A = x;
+  const float* Bw = w;
+  int64_t lda = K, ldb = w_layout == 0 ? K : N;
+  int blayout = w_layout == 0 ? B_NT : B_NN;
+  if (stage_a) {
+    float* as = (float*)ws.get();
+    int rc = launch_stage(x, M, K, K, 1, as, Kp, s);
+    if (rc) return rc;
+    A = as;
+    lda = Kp;
+  }
+  if (stage_b) {
+    float* bs = (float*)(ws.get() + off_b);
+    int rc = w_layout == 0 ? launch_stage(w, N, K, K, 1, bs, Kp, s)
+                           : launch_stage(w, N, K, 1, N, bs, Kp, s);
+    if (rc) return rc;
+    Bw = bs;
+    ldb = Kp;
+    blayout = B_NT;
+  }
   GemmArgs a = blank_args();
-  a.A = x;
-  a.lda = K;
-  a.B = w;
-  a.ldb = w_layout == 0 ? K : N;
+  a.A = A;
+  a.lda = lda;
+  a.B = Bw;
+  a.ldb = ldb;
   a.C = y;
   a.ldc = N;
   a.bias = b;
   a.M = (int32_t)M;
   a.N = N;
-  a.K = K;
+  a.K = kfit ? K : (int32_t)Kp;
   a.flags = (b ? EPI_BIAS : 0) | ((epilogue & GS_EPI_GELU) ? EPI_GELU : 0) |
             ((epilogue & GS_EPI_RELU) ? EPI_RELU : 0) |
             ((epilogue & GS_EPI_RESIDUAL) ? EPI_RES1 : 0);
   a.R1 = residual;
   a.ldr1 = N;
-  hipStream_t s = pick(stream);
-  std::unique_lock<std::mutex> lk(g_ws_mu, std::defer_lock);
   if (bf16) {
-    lk.lock();
-    void* ws = nullptr;
-    int rc = workspace((size_t)N * K * 2, &ws);
+    void* wh = ws.get() + off_h;
+    int rc = launch_f32_to_bf16(Bw, wh, (int64_t)N * a.ldb, s);
     if (rc) return rc;
-    rc = launch_f32_to_bf16(w, ws, (int64_t)N * K, s);
-    if (rc) return rc;
-    a.Bh = ws;
+    a.Bh = wh;
   }
   GemmBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
   if (x6) bt.kernel = 3;
-  int rc = launch_gemm(bt, A_PLAIN, w_layout == 0 ? B_NT : B_NN, false, s, bf16);
-  if (rc == 0 && bf16) GS_CHECK_HIP(hipStreamSynchronize(s));  // workspace reuse
-  return rc;
+  return launch_gemm(bt, A_PLAIN, blayout, false, s, bf16);
 }
 
 int32_t gs_hip_layernorm(const float* x, const float* gamma, const float* beta, float* y,
                          int64_t rows, int32_t D, float eps, void* stream) {
   if (ensure_device()) return -2;
-  LnBatch bt;
-  bt.g[0] = LnArgs{x, gamma, beta, y, rows, D, eps};
-  bt.ngroups = 1;
-  return launch_layernorm(bt, pick(stream));
+  GS_REQUIRE(D > 0 && rows >= 0, "layernorm: bad sizes");
+  const LnArgs a{x, gamma, beta, y, rows, D, eps};
+  // one wavefront per row for aligned rows of D % 4 == 0 up to 4096, one
+  // workgroup per row (any width and alignment) otherwise
+  if (D % 4 == 0 && D <= 4096 && aligned16(x) && aligned16(y) && aligned16(gamma) &&
+      aligned16(beta)) {
+    LnBatch bt;
+    bt.g[0] = a;
+    bt.ngroups = 1;
+    return launch_layernorm(bt, pick(stream));
+  }
+  return launch_layernorm_rows(a, pick(stream));
 }
 
 int32_t gs_hip_attention(const float* q, const float* k, const float* v, float* o, int32_t B,
@@ -143,10 +184,17 @@ int32_t gs_hip_attention(const float* q, const float* k, const float* v, float* 
                          int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, int64_t o_sb,
                          int64_t o_sh, int64_t o_sn, void* stream) {
   if (ensure_device()) return -2;
-  GS_REQUIRE(head_dim == 64, "attention: head_dim must be 64");
+  GS_REQUIRE(head_dim >= 1 && head_dim <= 128, "attention: head_dim must be in [1, 128]");
+  const AttnArgs a{q,    k,    v,    o,    q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb,
+                   v_sh, v_sn, o_sb, o_sh, o_sn, B,    H,    Nq,   Nkv,  scale};
+  // head_dim 64 with 16-byte aligned rows runs on the MFMA flash kernel; other
+  // head dims and layouts on the general kernel (one wavefront per query)
+  bool mfma = head_dim == 64 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  const int64_t st[12] = {q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn};
+  for (int j = 0; j < 12; ++j) mfma = mfma && st[j] % 4 == 0;
+  if (!mfma) return launch_attention_general(a, head_dim, pick(stream));
   AttnBatch bt;
-  bt.g[0] = AttnArgs{q,    k,    v,    o,    q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb,
-                     v_sh, v_sn, o_sb, o_sh, o_sn, B,    H,    Nq,   Nkv,  scale};
+  bt.g[0] = a;
   bt.ngroups = 1;
   return launch_attention(bt, pick(stream));
 }
@@ -170,38 +218,59 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
                       const float* residual, void* stream) {
   if (ensure_device()) return -2;
   GS_REQUIRE(w_layout == 0 || w_layout == 1, "conv2d: w_layout must be 0 or 1");
-  GS_REQUIRE(k > 0 && stride > 0 && pad >= 0 && B >= 0 && H > 0 && W > 0 && Cout > 0,
+  GS_REQUIRE(k > 0 && stride > 0 && pad >= 0 && B >= 0 && H > 0 && W > 0 && Cin > 0 && Cout > 0,
              "conv2d: bad geometry");
+  GS_REQUIRE(x && w && y, "conv2d: null operand");
   GS_REQUIRE((flags & ~(GS_CONV_RELU_IN | GS_CONV_RELU_OUT | GS_CONV_F32X6)) == 0,
              "conv2d: unknown flag");
   const int32_t Ho = (H + 2 * pad - k) / stride + 1, Wo = (W + 2 * pad - k) / stride + 1;
-  GS_REQUIRE(Ho > 0 && Wo > 0, "conv2d: empty output");
+  GS_REQUIRE(H + 2 * pad >= k && W + 2 * pad >= k && Ho > 0 && Wo > 0, "conv2d: empty output");
   GS_REQUIRE((int64_t)B * Ho * Wo <= INT32_MAX, "conv2d: too many output pixels");
+  GS_REQUIRE((int64_t)B * H * W <= INT32_MAX, "conv2d: too many input pixels");
+  if (B == 0) return 0;
   hipStream_t s = pick(stream);
-  std::unique_lock<std::mutex> lk(g_ws_mu);
+  // The implicit-GEMM conv reads 32 input channels per K step from 16-byte
+  // aligned NHWC rows, with the weight as OHWI. An OIHW weight is re-laid
+  // per call (the caller keeps ownership; a weight may change between calls);
+  // other channel counts run on copies zero-padded to a multiple of 32.
+  const int32_t Cp = (int32_t)round_up(Cin, 32);
+  const bool stage_x = Cp != Cin || !aligned16(x);
+  const bool stage_w = Cp != Cin || !aligned16(w) || (w_layout == 0 && k > 1);
+  const size_t x_bytes = stage_x ? (size_t)B * H * W * Cp * 4 : 0;
+  const size_t w_bytes = stage_w ? (size_t)Cout * k * k * Cp * 4 : 0;
+  StreamScratch ws;
+  if (x_bytes + w_bytes) {
+    int rc = ws.alloc(x_bytes + w_bytes + 256, s);
+    if (rc) return rc;
+  }
+  const float* xk = x;
   const float* wk = w;
-  if (w_layout == 0 && k > 1) {
-    void* ws = nullptr;
-    int rc = workspace((size_t)Cout * Cin * k * k * sizeof(float), &ws);
+  if (stage_x) {
+    float* xs = (float*)ws.get();
+    int rc = launch_stage(x, (int64_t)B * H * W, Cin, Cin, 1, xs, Cp, s);
     if (rc) return rc;
-    rc = launch_oihw_to_ohwi(w, Cout, Cin, k, (float*)ws, s);
+    xk = xs;
+  }
+  if (stage_w) {
+    float* wsb = (float*)(ws.get() + round_up((int64_t)x_bytes, 256));
+    int rc = launch_conv_weight_stage(w, Cout, Cin, k, w_layout, Cp, wsb, s);
     if (rc) return rc;
-    wk = (const float*)ws;
+    wk = wsb;
   }
   GemmArgs a = blank_args();
   const bool pointwise = (k == 1 && stride == 1 && pad == 0);
-  a.A = x;
-  a.lda = Cin;
+  a.A = xk;
+  a.lda = Cp;
   a.cH = H;
   a.cW = W;
-  a.cCin = Cin;
+  a.cCin = Cp;
   a.ck = k;
   a.cs = stride;
   a.cp = pad;
   a.cHo = Ho;
   a.cWo = Wo;
   a.B = wk;
-  a.ldb = (int64_t)k * k * Cin;
+  a.ldb = (int64_t)k * k * Cp;
   a.C = y;
   a.ldc = Cout;
   a.bias = b;
@@ -209,16 +278,14 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   a.ldr1 = Cout;
   a.M = (int32_t)((int64_t)B * Ho * Wo);
   a.N = Cout;
-  a.K = k * k * Cin;
+  a.K = k * k * Cp;
   a.flags = (b ? EPI_BIAS : 0) | ((flags & GS_CONV_RELU_OUT) ? EPI_RELU : 0) |
             (residual ? EPI_RES1 : 0);
   GemmBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
   if (flags & GS_CONV_F32X6) bt.kernel = 3;
-  int rc = launch_gemm(bt, pointwise ? A_PLAIN : A_CONV, B_NT, (flags & GS_CONV_RELU_IN) != 0, s);
-  if (rc == 0 && wk != w) GS_CHECK_HIP(hipStreamSynchronize(s));  // workspace reuse
-  return rc;
+  return launch_gemm(bt, pointwise ? A_PLAIN : A_CONV, B_NT, (flags & GS_CONV_RELU_IN) != 0, s);
 }
 
 int32_t gs_hip_conv_transpose(const float* x, int32_t B, int32_t H, int32_t W, int32_t Cin,
@@ -229,13 +296,14 @@ int32_t gs_hip_conv_transpose(const float* x, int32_t B, int32_t H, int32_t W, i
              "conv_transpose: need Cin % 32 == 0 and Cout % 32 == 0");
   GS_REQUIRE((int64_t)B * H * W <= INT32_MAX && (int64_t)k * k * Cout <= INT32_MAX,
              "conv_transpose: too many pixels");
+  GS_REQUIRE(x && w && y, "conv_transpose: null operand");
+  if (B == 0) return 0;
   hipStream_t s = pick(stream);
-  std::unique_lock<std::mutex> lk(g_ws_mu);
   const int64_t N = (int64_t)k * k * Cout;
-  void* ws = nullptr;
-  int rc = workspace((size_t)(N * Cin + N) * sizeof(float), &ws);
+  StreamScratch ws;
+  int rc = ws.alloc((size_t)(N * Cin + N) * sizeof(float), s);
   if (rc) return rc;
-  float* wt = (float*)ws;
+  float* wt = (float*)ws.get();
   float* bt_exp = wt + N * Cin;
   rc = launch_convt_relayout(w, b, Cin, Cout, k, wt, bt_exp, s);
   if (rc) return rc;
@@ -259,9 +327,7 @@ int32_t gs_hip_conv_transpose(const float* x, int32_t B, int32_t H, int32_t W, i
   GemmBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
-  rc = launch_gemm(bt, A_PLAIN, B_NT, false, s);
-  if (rc == 0) GS_CHECK_HIP(hipStreamSynchronize(s));  // workspace reuse
-  return rc;
+  return launch_gemm(bt, A_PLAIN, B_NT, false, s);
 }
 
 int32_t gs_hip_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C, float* y,
@@ -293,20 +359,14 @@ int32_t gs_hip_collect_points(const float* pts, const float* conf, int64_t n, fl
                               void* stream) {
   if (ensure_device()) return -2;
   GS_REQUIRE(n >= 0, "collect_points: n < 0");
-  std::lock_guard<std::mutex> lk(g_cp_mu);
-  const int64_t need = collect_points_scratch(n);
-  if (need > g_cp_n) {
-    if (g_cp) {
-      GS_CHECK_HIP(hipDeviceSynchronize());
-      GS_CHECK_HIP(hipFree(g_cp));
-      g_cp = nullptr;
-      g_cp_n = 0;
-    }
-    GS_CHECK_HIP(hipMalloc(&g_cp, need * sizeof(int64_t)));
-    g_cp_n = need;
-  }
-  return launch_collect_points(pts, conf, n, threshold, out_pts, out_conf, capacity, count, g_cp,
-                               pick(stream));
+  if (n == 0) return launch_collect_points(pts, conf, 0, threshold, out_pts, out_conf, capacity,
+                                           count, nullptr, pick(stream));
+  hipStream_t s = pick(stream);
+  StreamScratch ws;
+  int rc = ws.alloc((size_t)collect_points_scratch(n) * sizeof(int64_t), s);
+  if (rc) return rc;
+  return launch_collect_points(pts, conf, n, threshold, out_pts, out_conf, capacity, count,
+                               (int64_t*)ws.get(), s);
 }
 
 }  // extern "C"

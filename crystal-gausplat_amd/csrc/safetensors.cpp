@@ -292,14 +292,22 @@ struct File {
           set_error("safetensors: negative dimension in " + t.name);
           return -1;
         }
-        n *= d;
+        if (__builtin_mul_overflow(n, d, &n)) {  // a crafted shape must not wrap
+          set_error("safetensors: element count of " + t.name + " overflows");
+          return -1;
+        }
       }
       const int64_t es = elem_size(t.dtype);
       if (es == 0) {
         set_error("safetensors: unknown dtype " + t.dtype + " for " + t.name);
         return -1;
       }
-      if (t.begin < 0 || t.end < t.begin || t.end > data_size || t.end - t.begin != n * es) {
+      int64_t nbytes = 0;
+      if (__builtin_mul_overflow(n, es, &nbytes)) {
+        set_error("safetensors: byte size of " + t.name + " overflows");
+        return -1;
+      }
+      if (t.begin < 0 || t.end < t.begin || t.end > data_size || t.end - t.begin != nbytes) {
         set_error("safetensors: data offsets of " + t.name + " do not match its shape");
         return -1;
       }

@@ -123,21 +123,31 @@ void gs_seed_uniform(uint64_t seed, const char* name, float lo, float hi,
  * y[M,N] = x[M,K] . W (+ b) with the epilogue above.
  * w_layout 0: W is [N,K] (y = x W^T, the GPU path's semantics);
  * w_layout 1: W buffer read as [K,N] (the reference CPU path's literal
- * indexing, src/nn/linear.cr:194). K must be a multiple of 32. b, residual
+ * indexing, src/nn/linear.cr:194). Any M >= 0, K >= 1, N >= 1 (the reference's
+ * linear_forward takes any width; linear_forward_simple serves in or out
+ * below 64, nn.metal:84-110): K % 32 == 0 with 16-byte aligned x and W runs
+ * on them directly; other shapes on zero-padded copies of x and W in
+ * stream-ordered scratch (allocated and released on `stream`). b, residual
  * nullable. residual may alias y. */
 int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y,
                       int64_t M, int32_t K, int32_t N, int32_t w_layout,
                       int32_t epilogue, const float* residual, void* stream);
 
 /* NN::GPUOps.layernorm_forward (src/nn/gpu_ops.cr:114-138), the arithmetic of
- * LayerNorm#forward_cpu (src/nn/layernorm.cr:192-240). D <= 4096, D % 4 == 0. */
+ * LayerNorm#forward_cpu (src/nn/layernorm.cr:192-240). Any D >= 1: one
+ * wavefront per row for 16-byte aligned rows with D % 4 == 0 and D <= 4096,
+ * one workgroup per row otherwise. */
 int32_t gs_hip_layernorm(const float* x, const float* gamma, const float* beta,
                          float* y, int64_t rows, int32_t D, float eps,
                          void* stream);
 
 /* NN::GPUOps.fused_attention (src/nn/gpu_ops.cr:200-227) generalised to
  * cross-attention with Nq != Nkv (the CPU path's semantics,
- * src/nn/attention.cr:215-325). head_dim must be 64. Element (b,h,n,d) of q
+ * src/nn/attention.cr:215-325). head_dim in [1, 128] (the reference takes any;
+ * its own spec runs 16, spec/nn/attention_spec.cr:49-58): head_dim 64 with
+ * 16-byte aligned rows (pointers and strides multiples of 4 floats) runs on
+ * the MFMA flash kernel, anything else on a general kernel (one wavefront
+ * per query, K / V tiles in LDS, expf softmax). Element (b,h,n,d) of q
  * is at q[b*q_sb + h*q_sh + n*q_sn + d]; likewise for k, v, o. The
  * reference layout [B,H,N,64] is q_sb = H*N*64, q_sh = N*64, q_sn = 64;
  * token-major [B,N,H*64] is q_sb = N*H*64, q_sh = 64, q_sn = H*64. */
@@ -161,8 +171,10 @@ int32_t gs_hip_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld,
 /* NN::GPUOps.conv2d_forward (src/nn/gpu_ops.cr:478-527); the arithmetic of
  * Conv2DBlock#forward_cpu (src/mastr/decoder_v2.cr:281-344). x NHWC
  * [B,H,W,Cin], w OIHW [Cout,Cin,k,k] (w_layout 0) or OHWI [Cout,k,k,Cin]
- * (w_layout 1), y NHWC. Cin must be a multiple of 32 for k > 1 (any multiple
- * of 32 for k == 1). flags: GS_CONV_RELU_IN applies ReLU to x on load,
+ * (w_layout 1), y NHWC. Any Cin >= 1: the implicit-GEMM conv reads 32
+ * channels per step from 16-byte aligned rows, so other channel counts (and
+ * OIHW weights with k > 1, re-laid per call) run on zero-padded copies in
+ * stream-ordered scratch. flags: GS_CONV_RELU_IN applies ReLU to x on load,
  * GS_CONV_RELU_OUT after the bias, residual (nullable) is added last. */
 #define GS_CONV_RELU_IN 1
 #define GS_CONV_RELU_OUT 2
@@ -207,9 +219,9 @@ int32_t gs_hip_prepare_frames(const float* src, int32_t F, int32_t sh,
  * NaN never selected) are appended, in element order, at out_pts[*count],
  * out_conf[*count]; *count (DEVICE int64, caller-zeroed before the first
  * call) advances by the selected number, also past capacity (positions >=
- * capacity are not written), so the caller can detect overflow. Uses a
- * library-owned scratch buffer: concurrent calls on different streams must
- * not overlap. */
+ * capacity are not written), so the caller can detect overflow. Its block
+ * counts live in stream-ordered scratch (allocated and released on
+ * `stream`), so calls on different streams are independent. */
 int32_t gs_hip_collect_points(const float* pts, const float* conf, int64_t n,
                               float threshold, float* out_pts,
                               float* out_conf, int64_t capacity,

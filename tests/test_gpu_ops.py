@@ -27,6 +27,11 @@ def p(t):
     return G.ptr(t)
 
 
+def p_off(t, nbytes):
+    """Device pointer nbytes into a tensor (to break 16-byte alignment)."""
+    return C.c_void_p(t.data_ptr() + nbytes)
+
+
 # ---------------------------------------------------------------- linear
 
 LINEAR_CASES = [
@@ -75,8 +80,8 @@ def test_linear_bf16_variant(M, K, N):
     y = empty(M, N)
     G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, 0, G.EPI_BF16, None,
                               stream()))
-    rel, worst = assert_close_bf16(host(y), O.linear(x, W, b), name="linear bf16")
-    print(f"bf16 linear: rel {rel:.2e} worst {worst:.2e}")
+    rel, worst, p999 = assert_close_bf16(host(y), O.linear(x, W, b), name="linear bf16")
+    print(f"bf16 linear: rel {rel:.2e} worst {worst:.2e} p99.9 elementwise {p999:.2e}")
     assert rel > 1e-5  # it really ran in bf16
 
 
@@ -149,10 +154,65 @@ def test_linear_literal_layout(M, K, N):
 def test_linear_rejects_bad_shapes_without_launch():
     case("linear validation")
     x = empty(4, 33)
-    rc = L().gs_hip_linear(p(x), p(x), None, p(x), 4, 33, 4, 0, 0, None, stream())
-    assert rc != 0 and b"multiple of 32" in L().gs_hip_last_error()
+    rc = L().gs_hip_linear(p(x), p(x), None, p(x), 4, 0, 4, 0, 0, None, stream())
+    assert rc != 0 and b"positive" in L().gs_hip_last_error()
     rc = L().gs_hip_linear(p(x), p(x), None, p(x), 4, 32, 4, 2, 0, None, stream())
     assert rc != 0
+    rc = L().gs_hip_linear(None, p(x), None, p(x), 4, 32, 4, 0, 0, None, stream())
+    assert rc != 0 and b"null" in L().gs_hip_last_error()
+
+
+# The reference's GPUOps.linear_forward takes any in / out width
+# (src/nn/gpu_ops.cr:39-78; linear_forward_simple below 64): spec shapes
+# (spec/nn/linear_spec.cr:29-38: 64 -> 32 over 8 rows, 16 -> 8 over 2x4 rows),
+# the self-test's 512 -> 256 over 256 rows (src/main.cr:860-876) and ragged K
+# in both weight layouts.
+@pytest.mark.parametrize("M,K,N,layout", [(8, 64, 32, 0), (8, 16, 8, 0), (256, 512, 256, 0),
+                                          (37, 33, 100, 0), (5, 1000, 77, 0), (9, 7, 3, 1),
+                                          (64, 96, 30, 1), (3, 1, 1, 0)])
+def test_linear_any_width(M, K, N, layout):
+    case(f"linear any width M={M} K={K} N={N} layout={layout}")
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.1), rnd(N, scale=0.1)
+    y = empty(M, N)
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, layout, 0, None,
+                              stream()))
+    assert_close(host(y), O.linear(x, W, b, layout), name="linear any width")
+
+
+@pytest.mark.parametrize("epi", ["gelu", "residual", "bf16", "f32x6"])
+def test_linear_ragged_k_epilogues_and_variants(epi):
+    case(f"linear ragged K {epi}")
+    M, K, N = 70, 45, 130
+    x, W, b, r = rnd(M, K), rnd(N, K, scale=0.1), rnd(N, scale=0.1), rnd(M, N)
+    ref = O.linear(x, W, b)
+    flags, res = 0, None
+    if epi == "gelu":
+        flags, ref = G.EPI_GELU, O.gelu(ref)
+    elif epi == "residual":
+        flags, res, ref = G.EPI_RESIDUAL, dev(r), ref + r
+    elif epi == "bf16":
+        flags = G.EPI_BF16
+    else:
+        flags = G.EPI_F32X6
+    y = empty(M, N)
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, 0, flags,
+                              p(res) if res is not None else None, stream()))
+    if epi == "bf16":
+        assert_close_bf16(host(y), ref, name="linear ragged bf16")
+    else:
+        assert_close(host(y), ref, name=f"linear ragged {epi}")
+
+
+def test_linear_unaligned_operands():
+    # rows starting 4 bytes into an allocation (16-byte alignment broken)
+    case("linear unaligned operands")
+    M, K, N = 40, 64, 48
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.1), rnd(N, scale=0.1)
+    xb, wb = dev(np.concatenate([[0.0], x.ravel()])), dev(np.concatenate([[0.0], W.ravel()]))
+    y = empty(M * N + 1)
+    G.check(L().gs_hip_linear(p_off(xb, 4), p_off(wb, 4), p(dev(b)), p_off(y, 4), M, K, N, 0, 0,
+                              None, stream()))
+    assert_close(host(y)[1:].reshape(M, N), O.linear(x, W, b), name="linear unaligned")
 
 
 # ---------------------------------------------------------------- layernorm
@@ -165,6 +225,22 @@ def test_layernorm_parity(rows, D):
     y = empty(rows, D)
     G.check(L().gs_hip_layernorm(p(dev(x)), p(dev(g)), p(dev(b)), p(y), rows, D, 1e-6, stream()))
     assert_close(host(y), O.layernorm(x, g, b, 1e-6), name="layernorm")
+
+
+# LayerNorm of any width (GPUOps.layernorm_forward takes any feature count,
+# src/nn/gpu_ops.cr:114-138): the self-test's 256x256 (src/main.cr:878-892),
+# odd widths, widths past 4096, and unaligned rows.
+@pytest.mark.parametrize("rows,D,off", [(256, 256, 0), (5, 7, 0), (3, 4097, 0), (4, 6000, 0),
+                                        (7, 130, 1), (9, 1, 0)])
+def test_layernorm_any_width(rows, D, off):
+    case(f"layernorm any width rows={rows} D={D} off={off}")
+    x, g, b = rnd(rows, D, scale=2.0) + 0.5, rnd(D, scale=0.2) + 1, rnd(D, scale=0.2)
+    pad = lambda a: dev(np.concatenate([np.zeros(off, np.float32), a.ravel()]))
+    y = empty(rows * D + off)
+    G.check(L().gs_hip_layernorm(p_off(pad(x), 4 * off), p_off(pad(g), 4 * off),
+                                 p_off(pad(b), 4 * off), p_off(y, 4 * off), rows, D, 1e-5,
+                                 stream()))
+    assert_close(host(y)[off:].reshape(rows, D), O.layernorm(x, g, b, 1e-5), name="layernorm any")
 
 
 # ---------------------------------------------------------------- attention
@@ -204,8 +280,80 @@ def test_attention_bhnd_layout_and_large_scores():
 def test_attention_rejects_bad_head_dim():
     case("attention validation")
     x = empty(64)
-    rc = L().gs_hip_attention(p(x), p(x), p(x), p(x), 1, 1, 1, 1, 32, 0.1, *([0] * 12), stream())
-    assert rc != 0 and b"head_dim" in L().gs_hip_last_error()
+    for hd in (0, 129):
+        rc = L().gs_hip_attention(p(x), p(x), p(x), p(x), 1, 1, 1, 1, hd, 0.1, *([0] * 12),
+                                  stream())
+        assert rc != 0 and b"head_dim" in L().gs_hip_last_error()
+
+
+# GPUOps.fused_attention takes any head_dim (src/nn/gpu_ops.cr:200-227); the
+# reference's own shapes: the spec's self-attention 2x8 tokens, 4 heads of 16
+# (spec/nn/attention_spec.cr:20-25, 49-58), its cross-attention 4 queries over 6
+# keys, 2 heads of 16 (:28-37), the self-test's 2x32 tokens, 4 heads of 16
+# (src/main.cr:894-909); then other head dims, the reference [B*H, N, hd]
+# layout, and unaligned head-dim-64 rows (general kernel).
+@pytest.mark.parametrize("B,H,Nq,Nkv,hd,layout", [
+    (2, 4, 8, 8, 16, "tok"), (1, 2, 4, 6, 16, "tok"), (2, 4, 32, 32, 16, "tok"),
+    (1, 3, 100, 77, 32, "tok"), (2, 2, 70, 70, 128, "tok"), (2, 2, 33, 65, 80, "bhnd"),
+    (1, 2, 45, 200, 1, "bhnd"), (2, 3, 50, 40, 64, "odd")])
+def test_attention_any_head_dim(B, H, Nq, Nkv, hd, layout):
+    case(f"attention any head_dim B={B} H={H} Nq={Nq} Nkv={Nkv} hd={hd} {layout}")
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    q, k, v = rnd(B, H, Nq, hd, scale=2.0), rnd(B, H, Nkv, hd, scale=2.0), rnd(B, H, Nkv, hd)
+    ref = O.sdpa(q, k, v, scale)
+    if layout == "bhnd":
+        st = lambda n: (H * n * hd, n * hd, hd)
+        lay = lambda a: a
+    else:  # token-major [B, N, H*hd]; "odd" adds one padding column per row
+        extra = 1 if layout == "odd" else 0
+        D = H * hd + extra
+        st = lambda n: (n * D, hd, D)
+
+        def lay(a):
+            t = a.transpose(0, 2, 1, 3).reshape(B, a.shape[2], H * hd)
+            return np.concatenate([t, np.zeros((B, a.shape[2], extra), np.float32)], -1)
+    o = empty(B * Nq * H * hd + B * Nq * 2)
+    G.check(L().gs_hip_attention(p(dev(lay(q))), p(dev(lay(k))), p(dev(lay(v))), p(o), B, H, Nq,
+                                 Nkv, hd, scale, *st(Nq), *st(Nkv), *st(Nkv), *st(Nq), stream()))
+    got = host(o)
+    if layout == "bhnd":
+        got = got[:B * H * Nq * hd].reshape(B, H, Nq, hd)
+    else:
+        D = H * hd + (1 if layout == "odd" else 0)
+        got = got[:B * Nq * D].reshape(B, Nq, D)[..., :H * hd].reshape(B, Nq, H, hd)
+        got = got.transpose(0, 2, 1, 3)
+    assert_close(got, ref, name="attention any head_dim")
+
+
+@pytest.mark.parametrize("B,N,Nkv,E,H", [(2, 8, 8, 64, 4), (1, 4, 6, 32, 2)])
+def test_multi_head_attention_module_at_spec_shapes(B, N, Nkv, E, H):
+    """MultiHeadAttention#forward (src/nn/attention.cr:49-81) through the op
+    seam: q / k / v projections, heads of E/H split from the token-major rows,
+    SDPA, output projection; against the oracle's composition of the same."""
+    case(f"MHA module B={B} N={N} Nkv={Nkv} E={E} H={H}")
+    hd = E // H
+    xq, xkv = rnd(B, N, E), rnd(B, Nkv, E)
+    Ws = {n: (rnd(E, E, scale=0.2), rnd(E, scale=0.1)) for n in ("q", "k", "v", "o")}
+    proj = {}
+    for n, src, rows in (("q", xq, N), ("k", xkv, Nkv), ("v", xkv, Nkv)):
+        proj[n] = empty(B, rows, E)
+        G.check(L().gs_hip_linear(p(dev(src)), p(dev(Ws[n][0])), p(dev(Ws[n][1])), p(proj[n]),
+                                  B * rows, E, E, 0, 0, None, stream()))
+    a = empty(B, N, E)
+    st = lambda n: (n * E, hd, E)
+    scale = float(np.float32(1.0 / np.sqrt(hd)))
+    G.check(L().gs_hip_attention(p(proj["q"]), p(proj["k"]), p(proj["v"]), p(a), B, H, N, Nkv, hd,
+                                 scale, *st(N), *st(Nkv), *st(Nkv), *st(N), stream()))
+    out = empty(B, N, E)
+    G.check(L().gs_hip_linear(p(a), p(dev(Ws["o"][0])), p(dev(Ws["o"][1])), p(out), B * N, E, E, 0,
+                              0, None, stream()))
+    heads = lambda t, n: t.reshape(B, n, H, hd).transpose(0, 2, 1, 3)
+    rq = O.linear(xq.reshape(-1, E), *Ws["q"]).reshape(B, N, E)
+    rk = O.linear(xkv.reshape(-1, E), *Ws["k"]).reshape(B, Nkv, E)
+    rv = O.linear(xkv.reshape(-1, E), *Ws["v"]).reshape(B, Nkv, E)
+    ra = O.sdpa(heads(rq, N), heads(rk, Nkv), heads(rv, Nkv), scale)
+    ra = ra.transpose(0, 2, 1, 3).reshape(B * N, E)
+    assert_close(host(out), O.linear(ra, *Ws["o"]).reshape(B, N, E), name="MHA module")
 
 
 def test_elementwise_and_conv_reject_bad_sizes_without_launch():
@@ -309,6 +457,80 @@ def test_conv_transpose_parity(Cin, Cout, k, H, W):
     G.check(L().gs_hip_conv_transpose(p(dev(x)), B, H, W, Cin, p(dev(w)), p(dev(b)), p(y), Cout, k,
                                       stream()))
     assert_close(host(y), O.conv_transpose(x, w, b, k), name="convT")
+
+
+# GPUOps.conv2d_forward takes any channel count (src/nn/gpu_ops.cr:478-527):
+# RGB-like inputs, ragged Cin, OHWI weights, strides and fused flags.
+@pytest.mark.parametrize("B,H,W,Cin,Cout,k,s,pd,layout,flags,res", [
+    (1, 6, 7, 3, 8, 3, 1, 1, 0, 0, False),
+    (2, 5, 5, 40, 16, 1, 1, 0, 1, 0, False),
+    (1, 9, 9, 17, 32, 3, 2, 1, 1, G.CONV_RELU_IN | G.CONV_RELU_OUT, True),
+    (2, 8, 6, 50, 5, 3, 1, 0, 0, 0, True)])
+def test_conv2d_any_channels(B, H, W, Cin, Cout, k, s, pd, layout, flags, res):
+    case(f"conv2d any Cin B={B} {H}x{W} {Cin}->{Cout} k={k} s={s} p={pd} layout={layout}")
+    x, w, b = rnd(B, H, W, Cin), rnd(Cout, Cin, k, k, scale=0.1), rnd(Cout, scale=0.1)
+    Ho, Wo = (H + 2 * pd - k) // s + 1, (W + 2 * pd - k) // s + 1
+    r = rnd(B, Ho, Wo, Cout)
+    ref = O.conv2d(np.maximum(x, 0) if flags & G.CONV_RELU_IN else x, w, b, s, pd)
+    if flags & G.CONV_RELU_OUT:
+        ref = np.maximum(ref, 0)
+    if res:
+        ref = ref + r
+    wk = w if layout == 0 else np.ascontiguousarray(w.transpose(0, 2, 3, 1))
+    y = empty(B, Ho, Wo, Cout)
+    G.check(L().gs_hip_conv2d(p(dev(x)), B, H, W, Cin, p(dev(wk)), p(dev(b)), p(y), Cout, k, s, pd,
+                              layout, flags, p(dev(r)) if res else None, stream()))
+    assert_close(host(y), ref, name="conv2d any Cin")
+
+
+def test_op_scratch_is_per_stream():
+    """Op-level calls whose kernels use scratch (OIHW conv re-layout, ragged
+    linear staging, bf16 weight copies, compaction block counts), issued
+    back to back on two streams without synchronisation in between, each
+    produce their own results: scratch is stream-ordered, not shared."""
+    case("op scratch on two streams")
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    cv, ln_, cp = [], [], []
+    for i, st in enumerate(streams):
+        B, H, W, C = 1, 24, 32, 96 + 32 * i
+        x, w, b = rnd(B, H, W, C), rnd(C, C, 3, 3, scale=0.05), rnd(C, scale=0.1)
+        xl, wl = rnd(300, 45 + i), rnd(200, 45 + i, scale=0.1)
+        conf = RNG.uniform(0, 1, 50000 + 7000 * i).astype(np.float32)
+        pts = rnd(conf.size, 3)
+        cv.append((x, w, b, dev(x), dev(w), dev(b), empty(B, H, W, C)))
+        ln_.append((xl, wl, dev(xl), dev(wl), empty(300, 200), empty(300, 200)))
+        cnt = dev(np.zeros(2, np.float32)).view(torch.int64)
+        cnt.zero_()
+        cp.append((pts, conf, dev(pts), dev(conf), empty(conf.size, 3), empty(conf.size), cnt))
+    torch.cuda.synchronize()
+    for _ in range(3):  # repeated, interleaved across the streams
+        for i, st in enumerate(streams):
+            x, w, b, xd, wd, bd, y = cv[i]
+            G.check(L().gs_hip_conv2d(p(xd), 1, 24, 32, x.shape[-1], p(wd), p(bd), p(y), x.shape[-1],
+                                      3, 1, 1, 0, 0, None, st.cuda_stream))
+            xl, wl, xld, wld, yl, yh = ln_[i]
+            K = xl.shape[1]
+            G.check(L().gs_hip_linear(p(xld), p(wld), None, p(yl), 300, K, 200, 0, 0, None,
+                                      st.cuda_stream))
+            G.check(L().gs_hip_linear(p(xld), p(wld), None, p(yh), 300, K, 200, 0, G.EPI_BF16, None,
+                                      st.cuda_stream))
+    for i, st in enumerate(streams):
+        pts, conf, ptd, cfd, op, oc, cnt = cp[i]
+        G.check(L().gs_hip_collect_points(p(ptd), p(cfd), conf.size, 0.5, p(op), p(oc), conf.size,
+                                          p(cnt), st.cuda_stream))
+    torch.cuda.synchronize()
+    for i in range(2):
+        x, w, b, _, _, _, y = cv[i]
+        assert_close(host(y), O.conv2d(x, w, b, 1, 1), name=f"conv stream {i}")
+        xl, wl, _, _, yl, yh = ln_[i]
+        assert_close(host(yl), O.linear(xl, wl), name=f"linear stream {i}")
+        assert_close_bf16(host(yh), O.linear(xl, wl), name=f"linear bf16 stream {i}")
+        pts, conf, _, _, op, oc, cnt = cp[i]
+        n = int(host(cnt)[0])
+        rp, rc = O.collect_points(pts, conf, 0.5)
+        assert n == len(rc)
+        np.testing.assert_array_equal(host(op)[:n], rp)
+        np.testing.assert_array_equal(host(oc)[:n], rc)
 
 
 @pytest.mark.parametrize("B,H,W,C", [(1, 96, 128, 256), (2, 5, 7, 8)])

@@ -88,7 +88,8 @@ def test_mixed_dtypes_and_unsupported(tmp_path):
 
 @pytest.mark.parametrize("case", ["offsets_past_end", "size_vs_shape", "bad_json",
                                   "header_too_long", "unknown_dtype", "missing_field",
-                                  "short_file", "float_offset"])
+                                  "short_file", "float_offset", "bytes_overflow",
+                                  "shape_overflow"])
 def test_malformed_files_are_errors(tmp_path, case):
     p = str(tmp_path / "bad.safetensors")
     data = np.arange(4, dtype=np.float32).tobytes()
@@ -108,6 +109,12 @@ def test_malformed_files_are_errors(tmp_path, case):
         _raw_file(p, {"a": {"dtype": "F32", "shape": [4]}}, data)
     elif case == "short_file":
         open(p, "wb").write(b"\x02\x00")
+    elif case == "bytes_overflow":  # (2^62 + 4) x 4 bytes wraps to 16 in int64
+        _raw_file(p, {"a": {"dtype": "F32", "shape": [(1 << 62) + 4], "data_offsets": [0, 16]}},
+                  data)
+    elif case == "shape_overflow":  # 2^32 x 2^32 x 4 wraps the element count
+        _raw_file(p, {"a": {"dtype": "F32", "shape": [1 << 32, 1 << 32, 4],
+                            "data_offsets": [0, 16]}}, data)
     elif case == "float_offset":
         h = b'{"a": {"dtype": "F32", "shape": [4], "data_offsets": [0, 16.0]}}'
         open(p, "wb").write(struct.pack("<Q", len(h)) + h + data)
