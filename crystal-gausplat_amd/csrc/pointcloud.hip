@@ -8,6 +8,7 @@
 
 #include <mutex>
 
+#include "../../include/gs_hip.h"
 #include "internal.h"
 
 #pragma clang fp contract(off)  // fp32 sequences as the reference evaluates them
@@ -245,3 +246,59 @@ int launch_fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t s) {
 }
 
 }  // namespace gs
+
+// ---- compaction without allocation ----------------------------------------------
+// gs_hip_collect_points_noalloc keeps its block counts in `scratch`, a
+// file-scope device array: every GPU the library runs on holds its own copy
+// (256 KB) until the process ends. In host code the array's name is only a
+// stand-in; its device address on the current device comes from
+// hipGetSymbolAddress, looked up once per device and used for every launch.
+// The count pass writes every block count the scan then reads, so the array
+// needs no clearing between calls.
+namespace gs {
+namespace {
+constexpr int64_t kNoAllocMaxPoints = (int64_t)1 << 27;
+constexpr int64_t kNoAllocBlocks = kNoAllocMaxPoints / kCpTile;
+static_assert(kNoAllocMaxPoints % kCpTile == 0, "whole blocks");
+}  // namespace
+}  // namespace gs
+
+static __device__ __align__(256) int64_t scratch[gs::kNoAllocBlocks];
+
+namespace gs {
+namespace {
+constexpr int kNoAllocMaxDevices = 64;
+std::mutex g_noalloc_mu;
+int64_t* g_noalloc_ptr[kNoAllocMaxDevices] = {};
+
+int noalloc_scratch(int64_t** out) {
+  int dev = 0;
+  GS_CHECK_HIP(hipGetDevice(&dev));
+  GS_REQUIRE(dev >= 0 && dev < kNoAllocMaxDevices, "collect_points_noalloc: device out of range");
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_ptr[dev]) {
+    void* p = nullptr;
+    GS_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    GS_REQUIRE(p != nullptr, "collect_points_noalloc: no device address for the scratch array");
+    g_noalloc_ptr[dev] = (int64_t*)p;
+  }
+  *out = g_noalloc_ptr[dev];
+  return 0;
+}
+}  // namespace
+}  // namespace gs
+
+extern "C" int32_t gs_hip_collect_points_noalloc(const float* pts, const float* conf, int64_t n,
+                                                 float threshold, float* out_pts,
+                                                 float* out_conf, int64_t capacity,
+                                                 int64_t* count, void* stream) {
+  GS_REQUIRE(n >= 0 && n <= gs::kNoAllocMaxPoints,
+             "collect_points_noalloc: n must be in [0, 2^27] (134217728 points)");
+  int64_t* sc = nullptr;
+  if (n > 0) {
+    const int rc = gs::noalloc_scratch(&sc);
+    if (rc) return rc;
+  }
+  return gs::launch_collect_points(pts, conf, n, threshold, out_pts, out_conf, capacity, count, sc,
+                                   (hipStream_t)stream);
+}

@@ -89,6 +89,8 @@ _SIGS = [
                                           C.c_int32, vp, vp]),
     ("gs_hip_collect_points", C.c_int32, [vp, vp, C.c_int64, C.c_float, vp, vp, C.c_int64, vp,
                                           vp]),
+    ("gs_hip_collect_points_noalloc", C.c_int32, [vp, vp, C.c_int64, C.c_float, vp, vp,
+                                                  C.c_int64, vp, vp]),
     ("gs_mastr_default_config", None, [C.POINTER(MastrConfig)]),
     ("gs_mastr_weight_count", C.c_int32, [C.POINTER(MastrConfig)]),
     ("gs_mastr_weight_info", C.c_int32, [C.POINTER(MastrConfig), C.c_int32, C.c_char_p, C.c_int32,

@@ -227,6 +227,22 @@ int32_t gs_hip_collect_points(const float* pts, const float* conf, int64_t n,
                               float* out_conf, int64_t capacity,
                               int64_t* count, void* stream);
 
+/* gs_hip_collect_points without allocation. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory at call time (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). Same arguments, behaviour and results as gs_hip_collect_points;
+ * the block counts live in a static 256 KB device array of the library (one
+ * per GPU, held until the process ends), so n is at most 2^27 (134217728)
+ * points, and a larger n is an error before any launch. Calls share that
+ * array per GPU: calls that overlap in time on one GPU (on different streams
+ * or threads) race and must be ordered by the caller. */
+#define GS_COLLECT_POINTS_NOALLOC_MAX ((int64_t)1 << 27)
+int32_t gs_hip_collect_points_noalloc(const float* pts, const float* conf,
+                                      int64_t n, float threshold,
+                                      float* out_pts, float* out_conf,
+                                      int64_t capacity, int64_t* count,
+                                      void* stream);
+
 /* ------------------------------------------------------------------------ */
 /* 3. Graph-level entry points (MASt3R)                                      */
 /* ------------------------------------------------------------------------ */
