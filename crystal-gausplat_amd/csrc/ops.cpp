@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <vector>
@@ -40,6 +41,16 @@ class StreamScratch {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
+
+// Split-K / key-split partials of an op-level call whose launch would leave
+// most CUs idle (fewer than ~432 workgroups): up to 16 partial tiles per
+// output, capped at 64 MB (the launchers pick a smaller split that fits).
+constexpr int64_t kOpSplitCapBytes = (int64_t)64 << 20;
+int64_t gemm_split_bytes(int64_t M, int64_t N, int ngroups = 1) {
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128) * ngroups;
+  if (tiles >= 432) return 0;
+  return std::min<int64_t>(16 * M * N * 4 * ngroups, kOpSplitCapBytes);
+}
 
 // RoPE tables [512][16] per base, uploaded once.
 std::mutex g_rope_mu;
@@ -107,9 +118,10 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   const int64_t b_bytes = stage_b ? (int64_t)N * Kp * 4 : 0;
   const int64_t h_bytes = bf16 ? (int64_t)N * Kp * 2 : 0;
   const int64_t off_b = round_up(a_bytes, 256), off_h = round_up(off_b + b_bytes, 256);
+  const int64_t off_p = round_up(off_h + h_bytes, 256), p_bytes = gemm_split_bytes(M, N);
   StreamScratch ws;
-  if (off_h + h_bytes > 0) {
-    int rc = ws.alloc((size_t)(off_h + h_bytes), s);
+  if (off_p + p_bytes > 0) {
+    int rc = ws.alloc((size_t)(off_p + p_bytes), s);
     if (rc) return rc;
   }
   const float* A = x;
@@ -158,6 +170,10 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   bt.g[0] = a;
   bt.ngroups = 1;
   if (x6) bt.kernel = 3;
+  if (p_bytes) {
+    bt.part_ws = (float*)(ws.get() + off_p);
+    bt.part_ws_elems = p_bytes / 4;
+  }
   return launch_gemm(bt, A_PLAIN, blayout, false, s, bf16);
 }
 
@@ -196,6 +212,19 @@ int32_t gs_hip_attention(const float* q, const float* k, const float* v, float* 
   AttnBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
+  // launches of fewer than ~432 workgroups split the keys into ranges merged
+  // in order; their partial states (64 outputs + max + sum per query and
+  // range) live in stream-ordered scratch
+  const int64_t units = (int64_t)B * H, qtiles = (Nq + 127) / 128;
+  StreamScratch ws;
+  if (units * qtiles < 432 && Nkv >= 128 && B > 0 && H > 0 && Nq > 0) {
+    const int64_t ranges = std::min<int64_t>((Nkv + 63) / 64, (432 + units * qtiles - 1) / (units * qtiles));
+    const int64_t elems = std::min<int64_t>(units * Nq * ranges * 66, kOpSplitCapBytes / 4) / 4 * 4;
+    int rc = ws.alloc((size_t)elems * 4, pick(stream));
+    if (rc) return rc;
+    bt.part_ws = (float*)ws.get();
+    bt.part_ws_elems = elems;
+  }
   return launch_attention(bt, pick(stream));
 }
 
@@ -236,11 +265,13 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   const int32_t Cp = (int32_t)round_up(Cin, 32);
   const bool stage_x = Cp != Cin || !aligned16(x);
   const bool stage_w = Cp != Cin || !aligned16(w) || (w_layout == 0 && k > 1);
-  const size_t x_bytes = stage_x ? (size_t)B * H * W * Cp * 4 : 0;
-  const size_t w_bytes = stage_w ? (size_t)Cout * k * k * Cp * 4 : 0;
+  const int64_t x_bytes = stage_x ? (int64_t)B * H * W * Cp * 4 : 0;
+  const int64_t w_bytes = stage_w ? (int64_t)Cout * k * k * Cp * 4 : 0;
+  const int64_t off_w = round_up(x_bytes, 256), off_p = round_up(off_w + w_bytes, 256);
+  const int64_t p_bytes = gemm_split_bytes((int64_t)B * Ho * Wo, Cout);
   StreamScratch ws;
-  if (x_bytes + w_bytes) {
-    int rc = ws.alloc(x_bytes + w_bytes + 256, s);
+  if (off_p + p_bytes > 0) {
+    int rc = ws.alloc((size_t)(off_p + p_bytes), s);
     if (rc) return rc;
   }
   const float* xk = x;
@@ -252,7 +283,7 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
     xk = xs;
   }
   if (stage_w) {
-    float* wsb = (float*)(ws.get() + round_up((int64_t)x_bytes, 256));
+    float* wsb = (float*)(ws.get() + off_w);
     int rc = launch_conv_weight_stage(w, Cout, Cin, k, w_layout, Cp, wsb, s);
     if (rc) return rc;
     wk = wsb;
@@ -285,6 +316,10 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   bt.g[0] = a;
   bt.ngroups = 1;
   if (flags & GS_CONV_F32X6) bt.kernel = 3;
+  if (p_bytes) {
+    bt.part_ws = (float*)(ws.get() + off_p);
+    bt.part_ws_elems = p_bytes / 4;
+  }
   return launch_gemm(bt, pointwise ? A_PLAIN : A_CONV, B_NT, (flags & GS_CONV_RELU_IN) != 0, s);
 }
 
