@@ -41,6 +41,9 @@ LINEAR_CASES = [
     (768, 768, 2304), (768, 3072, 768), (768, 1024, 768), (300, 1792, 7168),
     # ragged
     (1, 32, 32), (37, 64, 100), (129, 96, 130),
+    # at least one 128 x 256 tile per CU (the one-wave-per-SIMD kernel) with
+    # ragged rows and columns
+    (5000, 96, 3000), (4099, 1024, 2304),
 ]
 
 
@@ -54,10 +57,11 @@ def test_linear_parity(M, K, N):
     assert_close(host(y), O.linear(x, W, b), name="linear")
 
 
+@pytest.mark.parametrize("M", [200, 8200])
 @pytest.mark.parametrize("epi", ["gelu", "residual", "relu", "nobias"])
-def test_linear_epilogues(epi):
-    case(f"linear epilogue {epi}")
-    M, K, N = 200, 256, 384
+def test_linear_epilogues(epi, M):
+    case(f"linear epilogue {epi} M={M}")
+    K, N = 256, 4096 if M > 1000 else 384
     x, W, b, r = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1), rnd(M, N)
     ref = O.linear(x, W, None if epi == "nobias" else b)
     flags = 0
