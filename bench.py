@@ -27,6 +27,9 @@ Secondary workloads (each its own JSON line, not the headline metric):
               the config-3 linear shapes (bias epilogue) through gs_hip_linear
               and through torch's fp32 F.linear (the ROCm BLAS libraries) on the
               same device tensors, alternating; TFLOP/s of each and their ratio.
+  library-bf16
+              the vendor library's bf16 GEMM (torch F.linear on bf16 tensors) on
+              the config-4 linear shapes; TFLOP/s per shape (reference point).
   ref-selftest
               the reference's own GPU micro-benchmarks (src/main.cr:860-909):
               Linear 256x512->256, LayerNorm 256x256, MHA 2x32x64 with 4 heads
@@ -363,6 +366,49 @@ def ref_selftest(args):
             "ops": res}
 
 
+# (name, M, N, K) of the config-4 linears (32 pairs at 512x512: encoder on
+# 2 x 32 images of 1024 tokens, decoder per chain on 32 x 1024 tokens)
+LIBRARY_SHAPES_C4 = [("encoder fc1", 65536, 4096, 1024), ("encoder qkv", 65536, 3072, 1024),
+                     ("encoder proj", 65536, 1024, 1024), ("encoder fc2", 65536, 1024, 4096),
+                     ("decoder fc1", 32768, 3072, 768), ("decoder qkv", 32768, 2304, 768),
+                     ("decoder proj", 32768, 768, 768), ("decoder fc2", 32768, 768, 3072)]
+
+
+def library_bf16(args):
+    """The vendor library's bf16 GEMM (torch F.linear on bf16 tensors, bias
+    epilogue) on the config-4 linear shapes: the reference point for the bf16
+    kernels, whose per-shape rates in the model come from --precision bf16
+    --per-shape."""
+    import torch
+    reps = max(args.steps, 5)
+    rows, t_lib, flops = [], 0.0, 0.0
+    for name, M, N, K in LIBRARY_SHAPES_C4:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        a = (torch.rand(M, K, device="cuda", generator=g) * 2 - 1).bfloat16()
+        w = ((torch.rand(N, K, device="cuda", generator=g) * 2 - 1) * 0.02).bfloat16()
+        b = ((torch.rand(N, device="cuda", generator=g) * 2 - 1) * 0.02).bfloat16()
+        f = lambda: torch.nn.functional.linear(a, w, b)
+        for _ in range(2):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        fl = 2.0 * M * N * K
+        t_lib, flops = t_lib + ms, flops + fl
+        rows.append({"shape": f"{name} M={M} N={N} K={K}", "library_tflops": round(fl / ms / 1e9, 1)})
+        del a, w, b
+    return {"metric": "vendor bf16 linear (torch F.linear, bias) throughput on the config-4 shapes",
+            "value": round(flops / t_lib / 1e9, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps,
+            "warmup": 2, "higher_is_better": True, "vs_baseline": None, "dtype": "bf16",
+            "data": "synthetic", "config": {"workload": "config-4 linear shapes, one launch each"},
+            "shapes": rows}
+
+
 def secondary(args):
     import torch
 
@@ -433,6 +479,8 @@ def secondary(args):
         return linear_vs_library(args)
     if args.workload == "ref-selftest":
         return ref_selftest(args)
+    if args.workload == "library-bf16":
+        return library_bf16(args)
     if args.workload == "ref512":
         B = args.pairs or 32
         cfg = G.ref512_config()
@@ -545,7 +593,7 @@ def main():
                     help="also print a per-shape kernel table (stderr) from a separate step")
     ap.add_argument("--workload", default="pair",
                     choices=["pair", "frames", "ref512", "checkpoint", "block", "encoder", "cpu",
-                             "linear-vs-library", "ref-selftest"])
+                             "linear-vs-library", "ref-selftest", "library-bf16"])
     ap.add_argument("--e2e", action="store_true",
                     help="pair workload: include the host->device image copies and the "
                          "device->host output copies (pinned host buffers) in the timed step")
