@@ -34,17 +34,38 @@ constexpr int QT = 128;  // queries per workgroup
 constexpr int KT = 64;   // keys per LDS tile
 constexpr int HD = 64;
 
-// SPLIT: workgroup (query tile, key range) = (blockIdx.x / kv_split,
-// blockIdx.x % kv_split) processes keys [range * kv_chunk, + kv_chunk) and
+// Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
+// own L2. The logical (query tile, head, image) of a workgroup is therefore
+// taken from a remapped id that gives every XCD one contiguous range of the
+// x-fastest order: the query tiles of one (image, head) run on one XCD at
+// about the same time and read its K / V through one L2, instead of every
+// XCD fetching them. XCD c (of 8) runs logical ids
+// [c*q + min(c, r), ... + q + (c < r)), q = total / 8, r = total % 8.
+struct AttnTile {
+  int x, y, z;
+};
+__device__ __forceinline__ AttnTile attn_tile() {
+  const int64_t gx = gridDim.x, gy = gridDim.y;
+  const int64_t total = gx * gy * (int64_t)gridDim.z;
+  const int64_t L = blockIdx.x + gx * (blockIdx.y + gy * (int64_t)blockIdx.z);
+  const int64_t q = total >> 3, r = total & 7, c = L & 7;
+  const int64_t w = c * q + (c < r ? c : r) + (L >> 3);
+  const int64_t yz = w / gx;
+  return AttnTile{(int)(w - yz * gx), (int)(yz % gy), (int)(yz / gy)};
+}
+
+// SPLIT: workgroup (query tile, key range) = (x / kv_split, x % kv_split) of
+// its remapped tile processes keys [range * kv_chunk, + kv_chunk) and
 // writes its unnormalised output with the running max and sum to the
 // scratch; attn_merge_kernel combines the ranges.
 template <bool SPLIT>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32_t Bcount) {
   constexpr int NW = 4, KTT = KT, KP = KTT / (4 * NW);  // K/V fx4 loads per thread per tile
-  const int grp = blockIdx.z / Bcount;
-  const int b = blockIdx.z - grp * Bcount;
+  const AttnTile tile = attn_tile();
+  const int grp = tile.z / Bcount;
+  const int b = tile.z - grp * Bcount;
   const AttnArgs& p = batch.g[grp];
-  const int head = blockIdx.y;
+  const int head = tile.y;
   const int Nq = p.Nq, Nkv = p.Nkv;
 
   __shared__ __attribute__((aligned(16))) float Ks[KTT][HD + 4];
@@ -60,8 +81,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
   float* ob = p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh;
 
   const int ns = SPLIT ? batch.kv_split : 1;
-  const int qtile = SPLIT ? blockIdx.x / ns : blockIdx.x;
-  const int krange = SPLIT ? blockIdx.x - qtile * ns : 0;
+  const int qtile = SPLIT ? tile.x / ns : tile.x;
+  const int krange = SPLIT ? tile.x - qtile * ns : 0;
   const int kbeg = SPLIT ? krange * batch.kv_chunk : 0;
   const int kend = SPLIT ? min(kbeg + batch.kv_chunk, Nkv) : Nkv;
   const int q0 = qtile * (32 * NW) + wave * 32;
@@ -255,32 +276,53 @@ __global__ __launch_bounds__(256) void attn_merge_kernel(AttnBatch batch, int32_
 //   O^T += V^T . P^T: slice s of a 32-key block takes, for lane half h, keys
 //     {16s + 4h + 0..3, 16s + 8 + 4h + 0..3} -- exactly the keys the lane
 //     holds in S^T accumulator registers 8s .. 8s+7 -- so P is converted in
-//     registers; V is staged transposed in LDS (Vt[hd][key]) so a lane reads
+//     registers; V is staged transposed in LDS (hd-major) so a lane reads
 //     its 2 x 4 keys with two 8-byte loads.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+// Transposed V tile of the bf16 kernel: hd row h holds its 64 keys as 16
+// groups of 4 (8 bytes each) in unpadded 128-byte rows, key group G in slot
+// G ^ vt_swz(h). On gfx950 LDS writes resolve 32 banks (16 lanes of 8 bytes
+// per cycle) and reads 64 banks (32 lanes of 8 bytes per cycle); with this
+// slot order the transposing writes (16 lanes: rows 4c + j, c < 16, one key
+// group) and the MFMA operand reads (32 lanes: rows l, l < 32, one key group)
+// each touch distinct banks. The rows of 72 keys used before cost 8 cycles
+// per write cycle (an 8-way conflict) and 2 per read.
+__device__ __forceinline__ int vt_swz(int h) { return ((h >> 2) ^ (((h >> 1) & 1) << 3)) & 15; }
+
 __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, int32_t Bcount) {
-  const int grp = blockIdx.z / Bcount;
-  const int b = blockIdx.z - grp * Bcount;
+  const AttnTile tile = attn_tile();
+  const int grp = tile.z / Bcount;
+  const int b = tile.z - grp * Bcount;
   const AttnArgs& p = batch.g[grp];
-  const int head = blockIdx.y;
+  const int head = tile.y;
   const int Nq = p.Nq, Nkv = p.Nkv;
 
   __shared__ __attribute__((aligned(16))) __bf16 Ks[KT][HD + 8];
-  __shared__ __attribute__((aligned(16))) __bf16 Vt[HD][KT + 8];
+  __shared__ __attribute__((aligned(16))) __bf16 Vt[HD * KT];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hl = lane >> 5;
+  // element offsets of the lane's V^T operand reads, [row half e][sub][sl][u]
+  // for hd row 32 e + l32 and key group 8 sub + 4 sl + 2 u + hl
+  int vto[2][8];
+#pragma unroll
+  for (int e = 0; e < 2; ++e)
+#pragma unroll
+    for (int ix = 0; ix < 8; ++ix) {
+      const int h = 32 * e + l32, G = 2 * ix + hl;
+      vto[e][ix] = h * KT + 4 * (G ^ vt_swz(h));
+    }
 
   const float* qb = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh;
   const float* kb = p.k + (int64_t)b * p.k_sb + (int64_t)head * p.k_sh;
   const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)head * p.v_sh;
   float* ob = p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh;
 
-  const int q0 = blockIdx.x * QT + wave * 32;
+  const int q0 = tile.x * QT + wave * 32;
   const float qscale = p.scale * 1.4426950408889634f;
   bf16x8 qf[4];
   {
@@ -303,19 +345,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
 
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
   fx4 rk[4], rv[4];
-  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
   // K rows lrow + 16 i; V rows 4 lrow + i, so each thread holds four
-  // consecutive keys of V and writes its transpose with 8-byte stores
-#define GS_ATT_LOAD(KB)                                                         \
-  _Pragma("unroll") for (int i = 0; i < 4; ++i) {                               \
-    const int key = (KB) + lrow + 16 * i;                                       \
-    const int kc = min(key, Nkv - 1);                                           \
-    const fx4 kk = *(const fx4*)(kb + (int64_t)kc * p.k_sn + lc4);              \
-    rk[i] = key < Nkv ? kk : zero4;                                             \
-    const int vkey = (KB) + 4 * lrow + i;                                       \
-    const int vc = min(vkey, Nkv - 1);                                          \
-    const fx4 vv = *(const fx4*)(vb + (int64_t)vc * p.v_sn + lc4);              \
-    rv[i] = vkey < Nkv ? vv : zero4;                                            \
+  // consecutive keys of V and writes its transpose with 8-byte stores.
+  // The loads go through buffer resources whose base is the tile's first key
+  // row (scalar registers) and whose size ends at the last key's 64 values:
+  // the lane offsets stay fixed across tiles, and rows at or past Nkv are out
+  // of range and read as zero (rows are at least HD apart, checked on the
+  // host). The whole (image, head) span is below 2^31 bytes (host check).
+  uint32_t kvo[4], vvo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kvo[i] = (uint32_t)(((int64_t)(lrow + 16 * i) * p.k_sn + lc4) * 4);
+    vvo[i] = (uint32_t)(((int64_t)(4 * lrow + i) * p.v_sn + lc4) * 4);
+  }
+  const int64_t kspan = ((int64_t)(Nkv - 1) * p.k_sn + HD) * 4;
+  const int64_t vspan = ((int64_t)(Nkv - 1) * p.v_sn + HD) * 4;
+#define GS_ATT_LOAD(KB)                                                                      \
+  {                                                                                          \
+    const int64_t ko = (int64_t)(KB) * p.k_sn, vo = (int64_t)(KB) * p.v_sn;                  \
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(                    \
+        (void*)(kb + ko), (short)0, (int)(kspan - 4 * ko), 0x00020000);                      \
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(                    \
+        (void*)(vb + vo), (short)0, (int)(vspan - 4 * vo), 0x00020000);                      \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                          \
+      rk[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo[i], 0, 0)); \
+      rv[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vvo[i], 0, 0)); \
+    }                                                                                        \
   }
 
   GS_ATT_LOAD(0)
@@ -330,7 +385,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
       const float c1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
       const float c2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
       const float c3[4] = {rv[3].x, rv[3].y, rv[3].z, rv[3].w};
-      *(uint64_t*)&Vt[lc4 + i][4 * lrow] =
+      *(uint64_t*)&Vt[(lc4 + i) * KT + 4 * (lrow ^ vt_swz(lc4 + i))] =
           (uint64_t)cvt_pk_bf16(c0[i], c1[i]) | ((uint64_t)cvt_pk_bf16(c2[i], c3[i]) << 32);
     }
     __syncthreads();
@@ -385,11 +440,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
         const u32x4 pp = {cvt_pk_bf16(s[8 * sl], s[8 * sl + 1]), cvt_pk_bf16(s[8 * sl + 2], s[8 * sl + 3]),
                           cvt_pk_bf16(s[8 * sl + 4], s[8 * sl + 5]), cvt_pk_bf16(s[8 * sl + 6], s[8 * sl + 7])};
         const bf16x8 pb = __builtin_bit_cast(bf16x8, pp);
-        const int k0 = sub * 32 + 16 * sl + 4 * hl;
-        const bf16x4 va0 = *(const bf16x4*)&Vt[l32][k0];
-        const bf16x4 va1 = *(const bf16x4*)&Vt[l32][k0 + 8];
-        const bf16x4 vb0 = *(const bf16x4*)&Vt[32 + l32][k0];
-        const bf16x4 vb1 = *(const bf16x4*)&Vt[32 + l32][k0 + 8];
+        // keys sub*32 + 16 sl + 4 hl + {0..3, 8..11}: key groups 8 sub + 4 sl + hl (+2)
+        const int ix = 4 * sub + 2 * sl;
+        const bf16x4 va0 = *(const bf16x4*)&Vt[vto[0][ix]];
+        const bf16x4 va1 = *(const bf16x4*)&Vt[vto[0][ix + 1]];
+        const bf16x4 vb0 = *(const bf16x4*)&Vt[vto[1][ix]];
+        const bf16x4 vb1 = *(const bf16x4*)&Vt[vto[1][ix + 1]];
         const bf16x8 v0 = {va0.x, va0.y, va0.z, va0.w, va1.x, va1.y, va1.z, va1.w};
         const bf16x8 v1 = {vb0.x, vb0.y, vb0.z, vb0.w, vb1.x, vb1.y, vb1.z, vb1.w};
         o0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v0, pb, o0, 0, 0, 0);
@@ -448,10 +504,11 @@ __device__ __forceinline__ void split3_8(const float* v, bf16x8& h, bf16x8& m, b
 }
 
 __global__ __launch_bounds__(256, 2) void attn_fwd_x6_kernel(AttnBatch batch, int32_t Bcount) {
-  const int grp = blockIdx.z / Bcount;
-  const int b = blockIdx.z - grp * Bcount;
+  const AttnTile tile = attn_tile();
+  const int grp = tile.z / Bcount;
+  const int b = tile.z - grp * Bcount;
   const AttnArgs& p = batch.g[grp];
-  const int head = blockIdx.y;
+  const int head = tile.y;
   const int Nq = p.Nq, Nkv = p.Nkv;
 
   __shared__ __attribute__((aligned(16))) __bf16 Ks[3][KT][HD + 8];
@@ -466,7 +523,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_x6_kernel(AttnBatch batch, in
   const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)head * p.v_sh;
   float* ob = p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh;
 
-  const int q0 = blockIdx.x * QT + wave * 32;
+  const int q0 = tile.x * QT + wave * 32;
   const float qscale = p.scale * 1.4426950408889634f;
   bf16x8 qf[3][4];  // [term][16-wide head-dim slice], scaled as the fp32 kernel
   {
@@ -641,6 +698,11 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, int prec) {
                             a.v_sb, a.v_sh, a.v_sn, a.o_sb, a.o_sh, a.o_sn};
     for (int j = 0; j < 12; ++j)
       GS_REQUIRE(st[j] % 4 == 0 && st[j] >= 0, "attention: strides must be multiples of 4");
+    if (bf16) {  // the bf16 kernel's buffer-resource loads (see the kernel)
+      GS_REQUIRE(a.k_sn >= HD && a.v_sn >= HD, "attention: bf16 kernel needs key rows >= 64 apart");
+      GS_REQUIRE(((int64_t)(a.Nkv - 1) * std::max(a.k_sn, a.v_sn) + HD) * 4 < ((int64_t)1 << 31),
+                 "attention: bf16 kernel needs each (image, head) K / V span below 2 GiB");
+    }
   }
   GS_REQUIRE(a0.B > 0 && a0.H > 0 && a0.Nq > 0 && a0.Nkv > 0, "attention: bad sizes");
   GS_REQUIRE((int64_t)a0.B * bt.ngroups <= 65535 && a0.H <= 65535, "attention: grid too large");

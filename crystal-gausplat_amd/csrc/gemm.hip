@@ -547,10 +547,13 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
 // global_load_lds_dwordx4 streams each K step straight into one of two LDS
 // buffers (no VGPR staging, no ds_write), so the next step's tiles are in
 // flight while the MFMAs consume the current one. LDS rows are 32 floats with
-// the 16-byte chunks XOR-swizzled by row (chunk c of row r at slot c ^ (r&7)):
-// a wave's load instruction writes 8 contiguous rows (lane -> row lane>>3,
-// slot lane&7), and the MFMA reads of 8 consecutive rows at one chunk hit 8
-// distinct slots (conflict-free). Same per-element MFMA sequence as
+// the 16-byte chunks XOR-swizzled by row (chunk c of row r at slot
+// c ^ ((r >> 1) & 7)): a wave's load instruction writes 8 contiguous rows
+// (lane -> row lane>>3, slot lane&7). gfx950 LDS reads serve 16 lanes of
+// 16 bytes per cycle from 64 banks, i.e. two 128-byte rows of banks; the MFMA
+// reads of 16 consecutive rows at one chunk then hit 16 distinct bank groups
+// (slot ^ (r & 7) left rows r and r + 8 on one group: 2-way conflicts,
+// measured). Same per-element MFMA sequence as
 // gemm_f32_kernel, so results are bit-identical to it. Synchronisation is
 // explicit: s_waitcnt vmcnt leaves the next step's 8 loads in flight, and
 // the barriers are bare s_barrier (a __syncthreads fence would also wait for
@@ -589,14 +592,16 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dl_kernel(GemmBatch batch) {
   const int wm = wave >> 1, wn = wave & 1;
   const int l32 = lane & 31, hl = lane >> 5;
 
-  // loader: wave w, instruction i fills tile rows 32w + 8i .. +7
-  const int rin = lane >> 3, chunk = (lane & 7) ^ rin;
+  // loader: wave w, instruction i fills tile rows 32w + 8i .. +7; the lane's
+  // slot lane & 7 of row r holds chunk (lane & 7) ^ ((r >> 1) & 7)
+  const int rin = lane >> 3;
   const float* ag[4];
   const float* ag2[4];
   const float* bg[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int row = 32 * wave + 8 * i + rin;
+    const int chunk = (lane & 7) ^ ((row >> 1) & 7);
     const int64_t m = min(m0 + row, M - 1), n = min(n0 + row, N - 1);
     ag[i] = p.A + m * p.lda + 4 * chunk;
     ag2[i] = ALOAD == A_CONCAT ? p.A2 + m * p.lda2 + 4 * chunk - p.K1 : nullptr;
@@ -611,9 +616,9 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dl_kernel(GemmBatch batch) {
     _Pragma("unroll") for (int i = 0; i < 4; ++i)                                       \
       lds_dma16(bg[i] + k_, b_lds[BUF] + (32 * wave + 8 * i) * BK * 4);                 \
   }
-  // per-lane LDS byte offsets of the MFMA operand rows; chunk c of row r sits
-  // at slot c ^ (r & 7) and r & 7 == l32 & 7 for every operand row
-  const int swz = l32 & 7;
+  // per-lane LDS offsets of the MFMA operand rows; chunk c of row r sits at
+  // slot c ^ ((r >> 1) & 7), the same for every operand row of the lane
+  const int swz = (l32 >> 1) & 7;
   const int fa0 = (wm * 64 + l32) * BK, fa1 = fa0 + 32 * BK;
   const int fb0 = (wn * 64 + l32) * BK, fb1 = fb0 + 32 * BK;
   const uint32_t a_lds[2] = {lds_addr(As0), lds_addr(As1)};
@@ -680,10 +685,21 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dl_kernel(GemmBatch batch) {
 // bf16 (round-to-nearest-even) on its way into LDS, B is a bf16 copy of the
 // weights ([N, K], NT layout). Within one K step of 32, MFMA slice s (0..1)
 // feeds lane l (half h = l/32) with k = 16s + 8h .. 16s + 8h + 7, one
-// ds_read_b128 per operand block. LDS rows are 40 bf16 (80 B).
+// ds_read_b128 per operand block. LDS rows hold 64 bf16 in swizzled order
+// (bsw) for 64-deep steps, else 32 bf16 + 8 of padding.
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 constexpr int LDSH = BK + 8;
+
+// LDS rows of 64 bf16 (two 32-wide K chunks, 128 bytes, unpadded): the 8-byte
+// chunk q of row r is stored at chunk q ^ bsw(r). On gfx950, LDS reads resolve
+// 64 banks (16 lanes of 16 bytes per cycle) and writes 32 banks (16 lanes of
+// 8 bytes, or 8 lanes of 16 bytes, per cycle). With this order, the fragment
+// reads (16 rows, one 16-byte chunk each) and the staging writes (two rows per
+// cycle) touch distinct banks. Padded rows of 72 conflicted 2-way on both
+// operand writes.
+__device__ __forceinline__ int bsw(int r) { return (((r >> 1) & 7) << 1) ^ ((r & 1) << 3); }
+__device__ __forceinline__ int bsw_col(int col, int h) { return (((col >> 2) ^ h) << 2) | (col & 3); }
 
 // KC: 32-wide K chunks per LDS step (2 where it divides the K range, else
 // 1): one barrier pair then covers 8 KC MFMAs per wave. Each chunk is
@@ -694,7 +710,9 @@ constexpr int LDSH = BK + 8;
 template <int ALOAD, bool A_RELU, int KC>
 __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   constexpr int BLAYOUT = B_NT;
-  constexpr int LH = BK * KC + 8;  // LDS row: KC chunks + 8 bf16 of padding
+  // LDS row: two chunks swizzled (bsw), or one chunk + 8 bf16 of padding
+  constexpr int LH = KC == 2 ? 2 * BK : BK + 8;
+  static_assert(KC == 1 || KC == 2, "K chunks per step");
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
   int m0, n0;
@@ -713,6 +731,10 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   // B (bf16): rows tid/4 + 64*j (j < 2), 8 bf16 at column 8*(tid%4)
   const __bf16* Bh = (const __bf16*)p.Bh;
   const int brow = tid >> 2, bc8 = (tid & 3) * 8;
+  // swizzle of the rows this thread writes (A: lrow + 32 i, B: brow + 64 j)
+  // and reads (l32 + multiples of 32); 0 with padded single-chunk rows
+  const int hA = KC == 2 ? bsw(lrow) : 0, hB = KC == 2 ? bsw(brow) : 0;
+  const int hR = KC == 2 ? bsw(l32) : 0;
   int bo[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
@@ -786,10 +808,10 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
           h.z = (__bf16)ra[i].z;
           h.w = (__bf16)ra[i].w;
         }
-        *(bf16x4*)&As[lrow + 32 * i][BK * c + lc4] = h;
+        *(bf16x4*)&As[lrow + 32 * i][bsw_col(BK * c + lc4, hA)] = h;
       }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) *(bf16x8*)&Bs[brow + 64 * j][BK * c + bc8] = rbhc[c][j];
+      for (int j = 0; j < 2; ++j) *(bf16x8*)&Bs[brow + 64 * j][bsw_col(BK * c + bc8, hB)] = rbhc[c][j];
     }
     __syncthreads();
     if (loadpos == 0) GS_LOAD_STEP(min(k0 + SK, kend - SK))
@@ -802,7 +824,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
         GS_LOAD_STEP(min(k0 + SK, kend - SK))
         __builtin_amdgcn_sched_barrier(0);
       }
-      const int kc = BK * c + sl * 16 + hl * 8;
+      const int kc = bsw_col(BK * c + sl * 16 + hl * 8, hR);
       const bf16x8 a0 = *(const bf16x8*)&As[wm * 64 + l32][kc];
       const bf16x8 a1 = *(const bf16x8*)&As[wm * 64 + 32 + l32][kc];
       const bf16x8 b0 = *(const bf16x8*)&Bs[wn * 64 + l32][kc];
@@ -1003,8 +1025,10 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_w1_kernel(GemmBatch batch) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int l32 = lane & 31, hl = lane >> 5;
-  // loader: wave w, instruction i fills tile rows 32i + 8w .. +7
-  const int rin = lane >> 3, chunk = (lane & 7) ^ rin;
+  // loader: wave w, instruction i fills tile rows 32i + 8w .. +7; chunk c of
+  // row r sits at slot c ^ ((r >> 1) & 7) (as in gemm_f32_dl_kernel), and
+  // (r >> 1) & 7 is the same for every i
+  const int rin = lane >> 3, chunk = (lane & 7) ^ ((4 * (wave & 1) + (rin >> 1)) & 7);
   const __bf16* Ah = (const __bf16*)p.A;
   const __bf16* Bh = (const __bf16*)p.Bh;
   const __bf16* ag[HBM_ / 32];
@@ -1029,7 +1053,7 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_w1_kernel(GemmBatch batch) {
       lds_dma16((const float*)(bg[i] + (K0)),                                                \
                 lds0 + ((BUF) * H1_STAGE + (HBM_ + 32 * i + 8 * wave) * HBK) * 2);           \
   }
-  const int swz = l32 & 7;
+  const int swz = (l32 >> 1) & 7;
   const int ra0 = (wm * 128 + l32) * HBK, rb0 = (wn * 128 + l32) * HBK;
   floatx16 c00 = {}, c01 = {}, c02 = {}, c03 = {}, c10 = {}, c11 = {}, c12 = {}, c13 = {}, c20 = {}, c21 = {}, c22 = {}, c23 = {}, c30 = {}, c31 = {}, c32 = {}, c33 = {};
 #define GS_H1_RD(AS, BS, S)                                                                  \
