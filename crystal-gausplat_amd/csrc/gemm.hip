@@ -1138,6 +1138,244 @@ __global__ __launch_bounds__(256, 1) void gemm_bf16_w1_kernel(GemmBatch batch) {
   w1_epi_row_any(p, c30, c31, c32, c33, mw + 96, nw, stage, l32, hl);
 }
 
+// bf16-input / fp32-accumulate kernel for large launches with bf16 activations
+// (A_PLAIN_H) and NT bf16 weights: workgroup tile 256 x 128 of 2 x 2 waves at
+// 128 x 64 (4 x 2 MFMA 32x32x16 blocks, 128 accumulators per lane), 32-deep K
+// steps streamed straight into one of two LDS stages (global_load_lds_dwordx4,
+// 48 KB in all), two or three workgroups per CU. Each wave reads 6 fragments
+// per 8 MFMAs (the 128 x 128 kernel: 4 per 4), and with more than one
+// workgroup per CU one workgroup's epilogue runs under the others' MFMAs,
+// which the 256 x 256 one-workgroup-per-CU kernel cannot do.
+// LDS rows are 32 bf16 (64 bytes, four 16-byte chunks); a load instruction
+// fills 16 rows (lane -> row lane >> 2, slot lane & 3), and chunk c of row r
+// sits at slot c ^ ((r >> 2) & 3): four rows share a 256-byte bank line, so
+// the fragment reads of 16 consecutive rows at one chunk hit 16 distinct bank
+// groups. Lane l (half h) feeds slice s with k = 16s + 8h .. +7: the
+// per-element MFMA sequence of gemm_bf16_kernel. The accumulators go out
+// through w2_epi_row, one 32-row block row at a time.
+constexpr int W2M = 256, W2N = 128, W2K = 32;
+constexpr int W2_STAGE = (W2M + W2N) * W2K;  // bf16 per LDS stage
+constexpr int W2_SS = 68;                    // epilogue stage row stride (floats)
+static_assert(4 * 32 * W2_SS * 4 <= 2 * W2_STAGE * 2, "w2 epilogue stages fit the LDS stages");
+
+// Epilogue of one 32 x 64 block row of a gemm_bf16_w2_kernel wave (q0: columns
+// col0 .. +31, q1: col0 + 32 .. +63): bias, RoPE, GELU / ReLU on the
+// accumulators, then through the wave's LDS stage (32 rows of W2_SS floats) so
+// that residuals are read and outputs written as 16-byte row segments (16
+// lanes per 64-column row). Same per-element operations and order as
+// gemm_epilogue_t; no scatter form (checked on the host). Measured in the
+// model: the per-element form of the shared epilogue (64-bit addresses, 4-byte
+// accesses) took this kernel from ~1100 TFLOP/s (main loop) to 360-565.
+template <bool ROPE>
+__device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0,
+                                           const floatx16& q1, int row0, int col0, float* stage,
+                                           int lane, int l32, int hl) {
+  const int M = p.M, N = p.N;
+  const int flags = ROPE ? p.flags & ~(EPI_RES1 | EPI_RES2) : p.flags & ~EPI_ROPE;
+  const float rtok = ROPE ? 1.0f / (float)p.tok_per_img : 0.f;
+  const float rgw = ROPE ? 1.0f / (float)p.grid_w : 0.f;
+  // col0 is a multiple of 64, so q0 is the y-axis half and q1 the x-axis
+  // half of one head's RoPE columns
+  const float bv0 = (flags & EPI_BIAS) ? p.bias[min(col0 + l32, N - 1)] : 0.f;
+  const float bv1 = (flags & EPI_BIAS) ? p.bias[min(col0 + 32 + l32, N - 1)] : 0.f;
+  const bool rope = ROPE && col0 < p.rope_ncols;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float v0 = q0[r], v1 = q1[r];
+    if (flags & EPI_BIAS) {
+      v0 = v0 + bv0;
+      v1 = v1 + bv1;
+    }
+    if (rope) {
+      // the row's grid position, frequency l32 % 16
+      const int row = min(row0 + 8 * (r >> 2) + 4 * hl + (r & 3), M - 1);
+      int tok, tx;
+      divmod_small(row, p.tok_per_img, rtok, tok);
+      const int ty = divmod_small(tok, p.grid_w, rgw, tx);
+      const int iy = ty * 16 + (l32 & 15), ix = tx * 16 + (l32 & 15);
+      const float cy = p.rope_cos[iy], sy = p.rope_sin[iy];
+      const float cx = p.rope_cos[ix], sx = p.rope_sin[ix];
+      const float p0 = __shfl_xor(v0, 16), p1 = __shfl_xor(v1, 16);
+      v0 = (l32 < 16) ? (v0 * cy - p0 * sy) : (v0 * cy + p0 * sy);
+      v1 = (l32 < 16) ? (v1 * cx - p1 * sx) : (v1 * cx + p1 * sx);
+    }
+    if (flags & EPI_GELU) {
+      v0 = gelu_tanh(v0);
+      v1 = gelu_tanh(v1);
+    }
+    if (flags & EPI_RELU) {
+      v0 = fmaxf(v0, 0.f);
+      v1 = fmaxf(v1, 0.f);
+    }
+    float* srow = stage + (8 * (r >> 2) + 4 * hl + (r & 3)) * W2_SS + l32;
+    srow[0] = v0;
+    srow[32] = v1;
+  }
+  // the stage belongs to this wave: LDS accesses of one wave complete in
+  // order, so a wave-level fence orders the writes above and the reads below
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int rin = lane >> 4, c4 = (lane & 15) * 4;
+  const int col = col0 + c4;
+  const int colc = min(col, N - 4);
+  // two halves of 16 rows, the residuals of a half read before its stores
+#pragma unroll
+  for (int hq = 0; hq < 2; ++hq) {
+  fx4 x1[4], x2[4];
+  if (flags & EPI_RES1) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = min(row0 + 16 * hq + 4 * u + rin, M - 1);
+      x1[u] = *(const fx4*)(p.R1 + (int64_t)row * p.ldr1 + colc);
+    }
+  }
+  if (flags & EPI_RES2) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int row = min(row0 + 16 * hq + 4 * u + rin, M - 1);
+      x2[u] = *(const fx4*)(p.R2 + (int64_t)row * p.ldr2 + colc);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int q = 4 * hq + u;
+    const int row = row0 + 4 * q + rin;
+    fx4 v = *(const fx4*)(stage + (4 * q + rin) * W2_SS + c4);
+    if (flags & EPI_RES1) v = v + x1[u];
+    if (flags & EPI_RES2) v = x2[u] + v;
+    if (row < M && col < N) {
+      if (flags & EPI_BF16OUT) {
+        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+        bf16x4_t h;
+        h.x = (__bf16)v.x;
+        h.y = (__bf16)v.y;
+        h.z = (__bf16)v.z;
+        h.w = (__bf16)v.w;
+        *(bf16x4_t*)((__bf16*)p.C + (int64_t)row * p.ldc + col) = h;
+      } else {
+        *(fx4*)(p.C + (int64_t)row * p.ldc + col) = v;
+        if (flags & EPI_DUAL) *(fx4*)(p.C2 + (int64_t)row * p.ldc + col) = v;
+      }
+    }
+  }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ bool w2_tile(const GemmArgs& p, int& m0, int& n0) {
+  const int tiles_m = (p.M + W2M - 1) / W2M, tiles_n = (p.N + W2N - 1) / W2N;
+  const int ntiles = tiles_m * tiles_n;
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  if (bid >= ntiles) return false;
+  const int per_group = GROUP_M * tiles_n;
+  const int gid = bid / per_group;
+  const int first_m = gid * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  m0 = (first_m + (bid % per_group) % gsz) * W2M;
+  n0 = ((bid % per_group) / gsz) * W2N;
+  return true;
+}
+
+__global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int M = p.M, N = p.N, K = p.K;
+  int m0, n0;
+  if (!w2_tile(p, m0, n0)) return;
+  __shared__ __attribute__((aligned(16))) __bf16 lds[2 * W2_STAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+  // loader: wave w, instruction i fills tile rows 16 (4i + w) .. +15; the
+  // slot swizzle (r >> 2) & 3 of those rows is (rin >> 2) & 3 for every i
+  const int rin = lane >> 2, chunk = (lane & 3) ^ ((rin >> 2) & 3);
+  const __bf16* Ah = (const __bf16*)p.A;
+  const __bf16* Bh = (const __bf16*)p.Bh;
+  const __bf16* ag[W2M / 64];
+  const __bf16* bg[W2N / 64];
+#pragma unroll
+  for (int i = 0; i < W2M / 64; ++i) {
+    const int64_t m = min(m0 + 16 * (4 * i + wave) + rin, M - 1);
+    ag[i] = Ah + m * p.lda + 8 * chunk;
+  }
+#pragma unroll
+  for (int i = 0; i < W2N / 64; ++i) {
+    const int64_t n = min(n0 + 16 * (4 * i + wave) + rin, N - 1);
+    bg[i] = Bh + n * p.ldb + 8 * chunk;
+  }
+  const uint32_t lds0 = lds_addr((const float*)lds);
+#define GS_W2_ISSUE(BUF, K0)                                                                 \
+  {                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < W2M / 64; ++i)                                     \
+      lds_dma16((const float*)(ag[i] + (K0)),                                                \
+                lds0 + ((BUF) * W2_STAGE + 16 * (4 * i + wave) * W2K) * 2);                  \
+    _Pragma("unroll") for (int i = 0; i < W2N / 64; ++i)                                     \
+      lds_dma16((const float*)(bg[i] + (K0)),                                                \
+                lds0 + ((BUF) * W2_STAGE + (W2M + 16 * (4 * i + wave)) * W2K) * 2);          \
+  }
+  const int swz = (l32 >> 2) & 3;
+  const int ra0 = (wm * 128 + l32) * W2K, rb0 = (wn * 64 + l32) * W2K;
+  floatx16 c00 = {}, c01 = {}, c10 = {}, c11 = {}, c20 = {}, c21 = {}, c30 = {}, c31 = {};
+  int buf = 0;
+  GS_W2_ISSUE(0, 0)
+  for (int k0 = 0; k0 < K; k0 += W2K) {
+    // step k0 in stage buf, step k0 + W2K streaming into the other stage:
+    // each wave waits for its own 6 loads of step k0, the barrier makes all
+    // of them visible; the fragment reads drain before the barrier that lets
+    // the stage be refilled
+    if (k0 + W2K < K) {
+      GS_W2_ISSUE(buf ^ 1, k0 + W2K)
+      asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    const __bf16* as = lds + buf * W2_STAGE;
+    const __bf16* bs = as + W2M * W2K;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int co = ((2 * s + hl) ^ swz) << 3;
+      const bf16x8 a0 = *(const bf16x8*)(as + ra0 + co);
+      const bf16x8 a1 = *(const bf16x8*)(as + ra0 + 32 * W2K + co);
+      const bf16x8 a2 = *(const bf16x8*)(as + ra0 + 64 * W2K + co);
+      const bf16x8 a3 = *(const bf16x8*)(as + ra0 + 96 * W2K + co);
+      const bf16x8 b0 = *(const bf16x8*)(bs + rb0 + co);
+      const bf16x8 b1 = *(const bf16x8*)(bs + rb0 + 32 * W2K + co);
+      c00 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, c00, 0, 0, 0);
+      c01 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, c01, 0, 0, 0);
+      c10 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, c10, 0, 0, 0);
+      c11 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, c11, 0, 0, 0);
+      c20 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b0, c20, 0, 0, 0);
+      c21 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b1, c21, 0, 0, 0);
+      c30 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b0, c30, 0, 0, 0);
+      c31 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b1, c31, 0, 0, 0);
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    buf ^= 1;
+  }
+#undef GS_W2_ISSUE
+  // four 32-row block rows per wave through the staged epilogue (the wave's
+  // 32 x 68-float stage; the LDS stages are free after the last barrier)
+  const int mw = m0 + wm * 128, nw = n0 + wn * 64;
+  float* stage = (float*)lds + wave * 32 * W2_SS;
+  if (p.flags & EPI_ROPE) {
+    w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
+    w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
+    w2_epi_row<true>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
+    w2_epi_row<true>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
+  } else {
+    w2_epi_row<false>(p, c00, c01, mw, nw, stage, lane, l32, hl);
+    w2_epi_row<false>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
+    w2_epi_row<false>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
+    w2_epi_row<false>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
+  }
+}
+
 template <int ALOAD, bool A_RELU, bool BSPLIT>
 __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   constexpr int BLAYOUT = B_NT;
@@ -1506,6 +1744,28 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
       hipLaunchKernelGGL(gemm_bf16_w1_kernel, dim3(ht, 1, b.ngroups), dim3(256), 0, s, b);
       GS_CHECK_HIP(hipGetLastError());
       if (ev) prof_stop(s, ev, gemm_prof_name("gemm_bf16_w1_kernel<A_PLAIN_H>", b).c_str(), flops,
+                        bytes);
+      return 0;
+    }
+  }
+  // other large unsplit launches with bf16 activations: the 256 x 128 kernel
+  // (at least two of its tiles per CU)
+  if (bf16 && aload == A_PLAIN_H && !a_relu && b.ksplit == 1) {
+    int wt = 0, wtot = 0;
+    bool ok = true;
+    for (int i = 0; i < b.ngroups; ++i) {
+      const GemmArgs& g = b.g[i];
+      const int t = ((g.M + W2M - 1) / W2M) * ((g.N + W2N - 1) / W2N);
+      wt = std::max(wt, t);
+      wtot += t;
+      ok = ok && g.K % W2K == 0 && g.lda % 8 == 0 && aligned16(g.A) && g.ldb % 8 == 0 &&
+           aligned16(g.Bh) && w1_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+    }
+    if (ok && wtot >= 512) {
+      hipEvent_t ev = prof_start(s);
+      hipLaunchKernelGGL(gemm_bf16_w2_kernel, dim3(wt, 1, b.ngroups), dim3(256), 0, s, b);
+      GS_CHECK_HIP(hipGetLastError());
+      if (ev) prof_stop(s, ev, gemm_prof_name("gemm_bf16_w2_kernel<A_PLAIN_H>", b).c_str(), flops,
                         bytes);
       return 0;
     }

@@ -113,12 +113,17 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   const bool stage_a = !kfit || !aligned16(x);
   const bool stage_b = !kfit || !aligned16(w) || (w_layout == 1 && N % 4 != 0);
   const int64_t Kp = round_up(K, 32);
-  // scratch: [staged x | staged W | bf16 copy of W], each part 256-byte aligned
+  // scratch: [staged x | staged W | bf16 copy of W | bf16 copy of x], each
+  // part 256-byte aligned. The bf16 variant reads bf16 activations (the
+  // A_PLAIN_H loader): x is rounded once here, with the round-to-nearest-even
+  // the fp32-row loader applies, so the products are the same.
   const int64_t a_bytes = stage_a ? M * Kp * 4 : 0;
   const int64_t b_bytes = stage_b ? (int64_t)N * Kp * 4 : 0;
   const int64_t h_bytes = bf16 ? (int64_t)N * Kp * 2 : 0;
+  const int64_t xh_bytes = bf16 ? M * Kp * 2 : 0;
   const int64_t off_b = round_up(a_bytes, 256), off_h = round_up(off_b + b_bytes, 256);
-  const int64_t off_p = round_up(off_h + h_bytes, 256), p_bytes = gemm_split_bytes(M, N);
+  const int64_t off_xh = round_up(off_h + h_bytes, 256);
+  const int64_t off_p = round_up(off_xh + xh_bytes, 256), p_bytes = gemm_split_bytes(M, N);
   StreamScratch ws;
   if (off_p + p_bytes > 0) {
     int rc = ws.alloc((size_t)(off_p + p_bytes), s);
@@ -165,6 +170,10 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
     int rc = launch_f32_to_bf16(Bw, wh, (int64_t)N * a.ldb, s);
     if (rc) return rc;
     a.Bh = wh;
+    void* xh = ws.get() + off_xh;
+    rc = launch_f32_to_bf16(A, xh, M * lda, s);
+    if (rc) return rc;
+    a.A = (const float*)xh;  // bf16 rows, lda elements apart
   }
   GemmBatch bt;
   bt.g[0] = a;
@@ -174,7 +183,7 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
     bt.part_ws = (float*)(ws.get() + off_p);
     bt.part_ws_elems = p_bytes / 4;
   }
-  return launch_gemm(bt, A_PLAIN, blayout, false, s, bf16);
+  return launch_gemm(bt, bf16 ? A_PLAIN_H : A_PLAIN, blayout, false, s, bf16);
 }
 
 int32_t gs_hip_layernorm(const float* x, const float* gamma, const float* beta, float* y,

@@ -89,6 +89,34 @@ def test_linear_bf16_variant(M, K, N):
     assert rel > 1e-5  # it really ran in bf16
 
 
+@pytest.mark.parametrize("M,K,N,epi", [(8200, 1024, 3000, "gelu"), (8200, 1024, 3000, "residual"),
+                                       (8192, 768, 2304, "nobias"), (16384, 2048, 1024, "residual"),
+                                       (16400, 3072, 1000, "gelu")])
+def test_linear_bf16_large_launches(M, K, N, epi):
+    """The bf16 variant on launches large enough for the 256 x 128 and 256 x 256
+    kernels (ragged M and N, the three epilogues), against an fp64 product of
+    the bf16-rounded operands: the kernels round x and W to bf16 and
+    accumulate in fp32, so the error bound is the fp32 accumulation's."""
+    case(f"linear bf16 large M={M} K={K} N={N} {epi}")
+    x, W, b, r = rnd(M, K), rnd(N, K, scale=0.02), rnd(N, scale=0.1), rnd(M, N)
+    xb = torch.from_numpy(x).to(torch.bfloat16).double().numpy()
+    Wb = torch.from_numpy(W).to(torch.bfloat16).double().numpy()
+    ref = xb @ Wb.T + (0 if epi == "nobias" else b.astype(np.float64))
+    flags = G.EPI_BF16
+    if epi == "gelu":
+        flags |= G.EPI_GELU
+        ref = 0.5 * ref * (1 + np.tanh(0.7978845608028654 * (ref + 0.044715 * ref ** 3)))
+    elif epi == "residual":
+        flags |= G.EPI_RESIDUAL
+        ref = ref + r
+    y = dev(r) if epi == "residual" else empty(M, N)  # residual in place
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), None if epi == "nobias" else p(dev(b)), p(y),
+                              M, K, N, 0, flags, p(y) if epi == "residual" else None, stream()))
+    got = host(y)
+    # fp32 accumulation of K bf16 products: a few ulp of the partial sums
+    assert_close(got, ref, rtol=1e-4, atol=2e-5 * np.sqrt(K / 1024), name=f"bf16 large {epi}")
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 1024, 256), (256, 4096, 256), (300, 1792, 7168),
                                    (129, 96, 130)])
 def test_linear_f32x6_accuracy_vs_fp64(M, K, N):
