@@ -869,283 +869,13 @@ __device__ __forceinline__ void split3(const fx4& v, bf16x4& h, bf16x4& m, bf16x
 }
 
 // bf16-input / fp32-accumulate kernel for large launches with bf16 activations
-// (A_PLAIN_H) and NT bf16 weights: workgroup tile 256 x 256 of 2 x 2 waves at
-// 128 x 128 (4 x 4 MFMA 32x32x16 blocks, 256 accumulators per lane in AGPRs),
-// one workgroup per CU. bf16 MFMAs read their operands from LDS at twice the
-// rate of fp32 per flop; at 128 x 128 per wave the fragment reads need half the
-// LDS bandwidth of 64 x 64 waves. Each 64-deep K step streams into one of two
-// LDS stages with global_load_lds_dwordx4 (rows of 64 bf16 = 128 bytes, the
-// 16-byte chunks swizzled by row as in gemm_f32_dl_kernel); the fragments of
-// the next 16-deep slice are read while the current slice's 16 MFMAs run.
-// Lane l (half h) feeds slice s with k = 16s + 8h .. +7: the per-element
-// MFMA sequence of gemm_bf16_kernel.
-// Epilogue of the one-wave-per-SIMD kernels: one 32-row block row of a wave's
-// tile (four 32 x 32 blocks across 128 columns) at a time, staged through the
-// wave's own LDS region. With one workgroup per CU nothing hides the epilogue,
-// so its memory accesses are issued in bulk and row-contiguous:
-//   phase 1 (accumulator layout): bias, RoPE (every cos / sin entry of the
-//   block row's 16 rows per lane loaded up front), GELU, ReLU, written to the
-//   stage;
-//   phase 2 (row layout, lane = 4 consecutive columns): all residual loads of
-//   the block row issued first (16-byte loads), then the adds, the store and
-//   the dual store (16-byte stores; 8-byte for bf16 output).
-// The per-element operation order is gemm_epilogue_t's (bias, RoPE, GELU,
-// ReLU, residual 1, residual 2, store); the compiler may contract the
-// expressions differently, so results agree to fp32 rounding.
-// Needs N % 4 == 0, 16-byte aligned C / C2 / residuals with ld % 4 == 0 and
-// no scatter (checked by w1_epi_ok on the host).
-constexpr int W1_SS = 132;  // stage row stride in floats
-
-template <bool ROPE>
-__device__ __forceinline__ void w1_epi_row(const GemmArgs& p, const floatx16& q0,
-                                           const floatx16& q1, const floatx16& q2,
-                                           const floatx16& q3, int row0, int col0, float* stage,
-                                           int l32, int hl) {
-  const int M = p.M, N = p.N;
-  const int flags = ROPE ? p.flags & ~(EPI_RES1 | EPI_RES2) : p.flags & ~EPI_ROPE;
-  float bv[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j)
-    bv[j] = (flags & EPI_BIAS) ? p.bias[min(col0 + 32 * j + l32, N - 1)] : 0.f;
-  float cy[16], sy[16], cx[16], sx[16];
-  if (ROPE) {
-    const float rtok = 1.0f / (float)p.tok_per_img, rgw = 1.0f / (float)p.grid_w;
-    const int f = l32 & 15;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int row = min(row0 + 8 * (r >> 2) + 4 * hl + (r & 3), M - 1);
-      int tok, tx;
-      divmod_small(row, p.tok_per_img, rtok, tok);
-      const int ty = divmod_small(tok, p.grid_w, rgw, tx);
-      cy[r] = p.rope_cos[ty * 16 + f];
-      sy[r] = p.rope_sin[ty * 16 + f];
-      cx[r] = p.rope_cos[tx * 16 + f];
-      sx[r] = p.rope_sin[tx * 16 + f];
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const floatx16& c = j == 0 ? q0 : j == 1 ? q1 : j == 2 ? q2 : q3;
-    const int cblk = col0 + 32 * j;
-    const bool rope = ROPE && cblk < p.rope_ncols;
-    const bool xaxis = (cblk >> 5) & 1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v = c[r];
-      if (flags & EPI_BIAS) v = v + bv[j];
-      if (rope) {
-        const float partner = __shfl_xor(v, 16);
-        const float cs = xaxis ? cx[r] : cy[r], sn = xaxis ? sx[r] : sy[r];
-        v = (l32 < 16) ? (v * cs - partner * sn) : (v * cs + partner * sn);
-      }
-      if (flags & EPI_GELU) v = gelu_tanh(v);
-      if (flags & EPI_RELU) v = fmaxf(v, 0.f);
-      stage[(8 * (r >> 2) + 4 * hl + (r & 3)) * W1_SS + 32 * j + l32] = v;
-    }
-  }
-  __syncthreads();
-  const int col = col0 + 4 * l32;
-  const int colc = min(col, N - 4);
-  fx4 x1[16], x2[16];
-  if (flags & EPI_RES1) {
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int row = min(row0 + 2 * q + hl, M - 1);
-      x1[q] = *(const fx4*)(p.R1 + (int64_t)row * p.ldr1 + colc);
-    }
-  }
-  if (flags & EPI_RES2) {
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int row = min(row0 + 2 * q + hl, M - 1);
-      x2[q] = *(const fx4*)(p.R2 + (int64_t)row * p.ldr2 + colc);
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < 16; ++q) {
-    const int row = row0 + 2 * q + hl;
-    fx4 v = *(const fx4*)(stage + (2 * q + hl) * W1_SS + 4 * l32);
-    if (flags & EPI_RES1) v = v + x1[q];
-    if (flags & EPI_RES2) v = x2[q] + v;
-    if (row < M && col < N) {
-      if (flags & EPI_BF16OUT) {
-        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-        bf16x4_t h;
-        h.x = (__bf16)v.x;
-        h.y = (__bf16)v.y;
-        h.z = (__bf16)v.z;
-        h.w = (__bf16)v.w;
-        *(bf16x4_t*)((__bf16*)p.C + (int64_t)row * p.ldc + col) = h;
-      } else {
-        *(fx4*)(p.C + (int64_t)row * p.ldc + col) = v;
-        if (flags & EPI_DUAL) *(fx4*)(p.C2 + (int64_t)row * p.ldc + col) = v;
-      }
-    }
-  }
-  __syncthreads();
-}
-
-__device__ __forceinline__ void w1_epi_row_any(const GemmArgs& p, const floatx16& q0,
-                                               const floatx16& q1, const floatx16& q2,
-                                               const floatx16& q3, int row0, int col0,
-                                               float* stage, int l32, int hl) {
-  if (p.flags & EPI_ROPE)
-    w1_epi_row<true>(p, q0, q1, q2, q3, row0, col0, stage, l32, hl);
-  else
-    w1_epi_row<false>(p, q0, q1, q2, q3, row0, col0, stage, l32, hl);
-}
-
-constexpr int HBM_ = 256, HBN_ = 256, HBK = 64;
-constexpr int H1_STAGE = (HBM_ + HBN_) * HBK;  // bf16 per LDS stage
-
-__device__ __forceinline__ bool h1_tile(const GemmArgs& p, int& m0, int& n0) {
-  const int tiles_m = (p.M + HBM_ - 1) / HBM_, tiles_n = (p.N + HBN_ - 1) / HBN_;
-  const int ntiles = tiles_m * tiles_n;
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-  if (bid >= ntiles) return false;
-  const int per_group = GROUP_M * tiles_n;
-  const int gid = bid / per_group;
-  const int first_m = gid * GROUP_M;
-  const int gsz = min(tiles_m - first_m, GROUP_M);
-  m0 = (first_m + (bid % per_group) % gsz) * HBM_;
-  n0 = ((bid % per_group) / gsz) * HBN_;
-  return true;
-}
-
-__global__ __launch_bounds__(256, 1) void gemm_bf16_w1_kernel(GemmBatch batch) {
-  const GemmArgs& p = batch.g[blockIdx.z];
-  const int M = p.M, N = p.N, K = p.K;
-  int m0, n0;
-  if (!h1_tile(p, m0, n0)) return;
-  __shared__ __attribute__((aligned(16))) __bf16 lds[2 * H1_STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, hl = lane >> 5;
-  // loader: wave w, instruction i fills tile rows 32i + 8w .. +7; chunk c of
-  // row r sits at slot c ^ ((r >> 1) & 7) (as in gemm_f32_dl_kernel), and
-  // (r >> 1) & 7 is the same for every i
-  const int rin = lane >> 3, chunk = (lane & 7) ^ ((4 * (wave & 1) + (rin >> 1)) & 7);
-  const __bf16* Ah = (const __bf16*)p.A;
-  const __bf16* Bh = (const __bf16*)p.Bh;
-  const __bf16* ag[HBM_ / 32];
-  const __bf16* bg[HBN_ / 32];
-#pragma unroll
-  for (int i = 0; i < HBM_ / 32; ++i) {
-    const int64_t m = min(m0 + 32 * i + 8 * wave + rin, M - 1);
-    ag[i] = Ah + m * p.lda + 8 * chunk;
-  }
-#pragma unroll
-  for (int i = 0; i < HBN_ / 32; ++i) {
-    const int64_t n = min(n0 + 32 * i + 8 * wave + rin, N - 1);
-    bg[i] = Bh + n * p.ldb + 8 * chunk;
-  }
-  const uint32_t lds0 = lds_addr((const float*)lds);
-#define GS_H1_ISSUE(BUF, K0)                                                                 \
-  {                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < HBM_ / 32; ++i)                                    \
-      lds_dma16((const float*)(ag[i] + (K0)),                                                \
-                lds0 + ((BUF) * H1_STAGE + (32 * i + 8 * wave) * HBK) * 2);                  \
-    _Pragma("unroll") for (int i = 0; i < HBN_ / 32; ++i)                                    \
-      lds_dma16((const float*)(bg[i] + (K0)),                                                \
-                lds0 + ((BUF) * H1_STAGE + (HBM_ + 32 * i + 8 * wave) * HBK) * 2);           \
-  }
-  const int swz = (l32 >> 1) & 7;
-  const int ra0 = (wm * 128 + l32) * HBK, rb0 = (wn * 128 + l32) * HBK;
-  floatx16 c00 = {}, c01 = {}, c02 = {}, c03 = {}, c10 = {}, c11 = {}, c12 = {}, c13 = {}, c20 = {}, c21 = {}, c22 = {}, c23 = {}, c30 = {}, c31 = {}, c32 = {}, c33 = {};
-#define GS_H1_RD(AS, BS, S)                                                                  \
-  {                                                                                          \
-    const int co = ((2 * (S) + hl) ^ swz) << 3;                                              \
-    a0 = *(const bf16x8*)((AS) + ra0 + co);                                                  \
-    a1 = *(const bf16x8*)((AS) + ra0 + 32 * HBK + co);                                       \
-    a2 = *(const bf16x8*)((AS) + ra0 + 64 * HBK + co);                                       \
-    a3 = *(const bf16x8*)((AS) + ra0 + 96 * HBK + co);                                       \
-    b0 = *(const bf16x8*)((BS) + rb0 + co);                                                  \
-    b1 = *(const bf16x8*)((BS) + rb0 + 32 * HBK + co);                                       \
-    b2 = *(const bf16x8*)((BS) + rb0 + 64 * HBK + co);                                       \
-    b3 = *(const bf16x8*)((BS) + rb0 + 96 * HBK + co);                                       \
-  }
-#define GS_H1_MM()                                                                           \
-  {                                                                                          \
-      c00 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, c00, 0, 0, 0);      \
-      c01 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, c01, 0, 0, 0);      \
-      c02 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b2, c02, 0, 0, 0);      \
-      c03 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b3, c03, 0, 0, 0);      \
-      c10 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, c10, 0, 0, 0);      \
-      c11 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, c11, 0, 0, 0);      \
-      c12 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b2, c12, 0, 0, 0);      \
-      c13 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b3, c13, 0, 0, 0);      \
-      c20 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b0, c20, 0, 0, 0);      \
-      c21 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b1, c21, 0, 0, 0);      \
-      c22 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b2, c22, 0, 0, 0);      \
-      c23 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b3, c23, 0, 0, 0);      \
-      c30 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b0, c30, 0, 0, 0);      \
-      c31 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b1, c31, 0, 0, 0);      \
-      c32 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b2, c32, 0, 0, 0);      \
-      c33 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b3, c33, 0, 0, 0);      \
-  }
-  int buf = 0;
-  GS_H1_ISSUE(0, 0)
-  for (int k0 = 0; k0 < K; k0 += HBK) {
-    // step k0 in stage buf, step k0 + HBK streaming into the other stage:
-    // each wave waits for its own 16 loads of step k0, the barrier makes all
-    // of them visible; the fragment reads drain before the barrier that lets
-    // the stage be refilled
-    if (k0 + HBK < K) {
-      GS_H1_ISSUE(buf ^ 1, k0 + HBK)
-      asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    }
-    const __bf16* as = lds + buf * H1_STAGE;
-    const __bf16* bs = as + HBM_ * HBK;
-    bf16x8 a0, a1, a2, a3, b0, b1, b2, b3;
-    bf16x8 na0, na1, na2, na3, nb0, nb1, nb2, nb3;
-    GS_H1_RD(as, bs, 0)
-#pragma unroll
-    for (int sl = 0; sl < 4; ++sl) {
-      if (sl < 3) {
-        {
-          bf16x8 t0 = a0, t1 = a1, t2 = a2, t3 = a3, u0 = b0, u1 = b1, u2 = b2, u3 = b3;
-          GS_H1_RD(as, bs, sl + 1)
-          na0 = a0; na1 = a1; na2 = a2; na3 = a3; nb0 = b0; nb1 = b1; nb2 = b2; nb3 = b3;
-          a0 = t0; a1 = t1; a2 = t2; a3 = t3; b0 = u0; b1 = u1; b2 = u2; b3 = u3;
-        }
-        __builtin_amdgcn_sched_barrier(0);  // the next slice's reads go out first
-      }
-      GS_H1_MM()
-      if (sl < 3) {
-        a0 = na0; a1 = na1; a2 = na2; a3 = na3; b0 = nb0; b1 = nb1; b2 = nb2; b3 = nb3;
-      }
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    buf ^= 1;
-  }
-#undef GS_H1_MM
-#undef GS_H1_RD
-#undef GS_H1_ISSUE
-  // four 32-row block rows per wave through the staged epilogue (the wave's
-  // 32 x 132-float stage sits in the first 67.6 KB of the LDS stages, free
-  // after the last step's barrier)
-  const int mw = m0 + wm * 128, nw = n0 + wn * 128;
-  float* stage = (float*)lds + wave * 32 * W1_SS;
-  w1_epi_row_any(p, c00, c01, c02, c03, mw, nw, stage, l32, hl);
-  w1_epi_row_any(p, c10, c11, c12, c13, mw + 32, nw, stage, l32, hl);
-  w1_epi_row_any(p, c20, c21, c22, c23, mw + 64, nw, stage, l32, hl);
-  w1_epi_row_any(p, c30, c31, c32, c33, mw + 96, nw, stage, l32, hl);
-}
-
-// bf16-input / fp32-accumulate kernel for large launches with bf16 activations
 // (A_PLAIN_H) and NT bf16 weights: workgroup tile 256 x 128 of 2 x 2 waves at
 // 128 x 64 (4 x 2 MFMA 32x32x16 blocks, 128 accumulators per lane), 32-deep K
 // steps streamed straight into one of two LDS stages (global_load_lds_dwordx4,
 // 48 KB in all), two or three workgroups per CU. Each wave reads 6 fragments
 // per 8 MFMAs (the 128 x 128 kernel: 4 per 4), and with more than one
 // workgroup per CU one workgroup's epilogue runs under the others' MFMAs,
-// which the 256 x 256 one-workgroup-per-CU kernel cannot do.
+// which a 256 x 256 tile at one workgroup per CU cannot do.
 // LDS rows are 32 bf16 (64 bytes, four 16-byte chunks); a load instruction
 // fills 16 rows (lane -> row lane >> 2, slot lane & 3), and chunk c of row r
 // sits at slot c ^ ((r >> 2) & 3): four rows share a 256-byte bank line, so
@@ -1542,7 +1272,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 // The staged epilogue of the one-wave-per-SIMD kernels stores 4 columns per
 // lane with vector accesses.
-bool w1_epi_ok(const GemmArgs& g) {
+bool row_epi_ok(const GemmArgs& g) {
   if (g.flags & EPI_SCATTER) return false;
   if (g.N % 4 || g.ldc % 4 || !aligned16(g.C)) return false;
   if ((g.flags & EPI_RES1) && (g.ldr1 % 4 || !aligned16(g.R1))) return false;
@@ -1723,33 +1453,11 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
                       flops, bytes);                                          \
     return 0;                                                                 \
   }
-  // large unsplit launches with bf16 activations and long K: the 256 x 256
-  // one-wave-per-SIMD kernel. Its main loop runs at ~1100 TFLOP/s, but with one
-  // workgroup per CU nothing hides its epilogue; measured at config 4 it is
-  // faster than gemm_bf16_kernel from K = 3072 (encoder fc2 866 against 764
-  // TFLOP/s, decoder fc2 782 against 711) and slower at K <= 1024 with GELU or
-  // RoPE epilogues (fc1 602 against 660, qkv 472 against 568)
-  if (bf16 && aload == A_PLAIN_H && !a_relu && b.ksplit == 1) {
-    int ht = 0, htot = 0;
-    bool kok = true;
-    for (int i = 0; i < b.ngroups; ++i) {
-      const int t = ((b.g[i].M + HBM_ - 1) / HBM_) * ((b.g[i].N + HBN_ - 1) / HBN_);
-      ht = std::max(ht, t);
-      htot += t;
-      kok = kok && b.g[i].K % HBK == 0 && b.g[i].K >= 2048 && b.g[i].lda % 8 == 0 &&
-            aligned16(b.g[i].A) && w1_epi_ok(b.g[i]);
-    }
-    if (kok && htot >= 256) {
-      hipEvent_t ev = prof_start(s);
-      hipLaunchKernelGGL(gemm_bf16_w1_kernel, dim3(ht, 1, b.ngroups), dim3(256), 0, s, b);
-      GS_CHECK_HIP(hipGetLastError());
-      if (ev) prof_stop(s, ev, gemm_prof_name("gemm_bf16_w1_kernel<A_PLAIN_H>", b).c_str(), flops,
-                        bytes);
-      return 0;
-    }
-  }
-  // other large unsplit launches with bf16 activations: the 256 x 128 kernel
-  // (at least two of its tiles per CU)
+  // large unsplit launches with bf16 activations: the 256 x 128 kernel (at
+  // least two of its tiles per CU). Measured at config 4 against the 128 x 128
+  // kernel: encoder fc1 873 against 648 TFLOP/s, qkv 742 against 562, fc2 846
+  // against 764; a 256 x 256 kernel at one workgroup per CU, which it replaced,
+  // ran fc2 at 812 and lost at K <= 1024 (its epilogue is exposed)
   if (bf16 && aload == A_PLAIN_H && !a_relu && b.ksplit == 1) {
     int wt = 0, wtot = 0;
     bool ok = true;
@@ -1759,7 +1467,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
       wt = std::max(wt, t);
       wtot += t;
       ok = ok && g.K % W2K == 0 && g.lda % 8 == 0 && aligned16(g.A) && g.ldb % 8 == 0 &&
-           aligned16(g.Bh) && w1_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+           aligned16(g.Bh) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
     }
     if (ok && wtot >= 512) {
       hipEvent_t ev = prof_start(s);
