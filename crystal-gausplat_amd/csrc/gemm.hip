@@ -886,6 +886,10 @@ __device__ __forceinline__ void split3(const fx4& v, bf16x4& h, bf16x4& m, bf16x
 constexpr int W2M = 256, W2N = 128, W2K = 32;
 constexpr int W2_STAGE = (W2M + W2N) * W2K;  // bf16 per LDS stage
 constexpr int W2_SS = 68;                    // epilogue stage row stride (floats)
+// fp32 256 x 128 kernel dispatch: at least this many tiles, one full round at
+// three workgroups per CU (measured at config 3: the 576-tile decoder launches
+// run 105 TFLOP/s on it against 120 on the 128 x 128 kernels)
+constexpr int kF2MinTiles = 768;
 static_assert(4 * 32 * W2_SS * 4 <= 2 * W2_STAGE * 2, "w2 epilogue stages fit the LDS stages");
 
 // Epilogue of one 32 x 64 block row of a gemm_bf16_w2_kernel wave (q0: columns
@@ -1093,6 +1097,103 @@ __global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
   // 32 x 68-float stage; the LDS stages are free after the last barrier)
   const int mw = m0 + wm * 128, nw = n0 + wn * 64;
   float* stage = (float*)lds + wave * 32 * W2_SS;
+  if (p.flags & EPI_ROPE) {
+    w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
+    w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
+    w2_epi_row<true>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
+    w2_epi_row<true>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
+  } else {
+    w2_epi_row<false>(p, c00, c01, mw, nw, stage, lane, l32, hl);
+    w2_epi_row<false>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
+    w2_epi_row<false>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
+    w2_epi_row<false>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
+  }
+}
+
+// fp32 kernel of the same structure for large launches with plain rows:
+// workgroup tile 256 x 128 of 2 x 2 waves at 128 x 64 (4 x 2 blocks of
+// v_mfma_f32_32x32x2_f32), 16-deep K steps (64-byte rows: the bf16 kernel's
+// LDS geometry, loader and slot swizzle) streamed into two LDS stages
+// (48 KB), three workgroups per CU, epilogue through w2_epi_row. Lane l
+// (half h) feeds MFMA step t of a K step with k = 8h + t.
+__global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
+  constexpr int FK = 16;                     // floats per K step
+  constexpr int FSTAGE = (W2M + W2N) * FK;   // floats per LDS stage
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int M = p.M, N = p.N, K = p.K;
+  int m0, n0;
+  if (!w2_tile(p, m0, n0)) return;
+  __shared__ __attribute__((aligned(16))) float lds[2 * FSTAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const int rin = lane >> 2, chunk = (lane & 3) ^ ((rin >> 2) & 3);
+  const float* ag[W2M / 64];
+  const float* bg[W2N / 64];
+#pragma unroll
+  for (int i = 0; i < W2M / 64; ++i) {
+    const int64_t m = min(m0 + 16 * (4 * i + wave) + rin, M - 1);
+    ag[i] = p.A + m * p.lda + 4 * chunk;
+  }
+#pragma unroll
+  for (int i = 0; i < W2N / 64; ++i) {
+    const int64_t n = min(n0 + 16 * (4 * i + wave) + rin, N - 1);
+    bg[i] = p.B + n * p.ldb + 4 * chunk;
+  }
+  const uint32_t lds0 = lds_addr(lds);
+#define GS_F2_ISSUE(BUF, K0)                                                                 \
+  {                                                                                          \
+    _Pragma("unroll") for (int i = 0; i < W2M / 64; ++i)                                     \
+      lds_dma16(ag[i] + (K0), lds0 + ((BUF) * FSTAGE + 16 * (4 * i + wave) * FK) * 4);       \
+    _Pragma("unroll") for (int i = 0; i < W2N / 64; ++i)                                     \
+      lds_dma16(bg[i] + (K0), lds0 + ((BUF) * FSTAGE + (W2M + 16 * (4 * i + wave)) * FK) * 4); \
+  }
+  const int swz = (l32 >> 2) & 3;
+  const int ra0 = (wm * 128 + l32) * FK, rb0 = (wn * 64 + l32) * FK;
+  floatx16 c00 = {}, c01 = {}, c10 = {}, c11 = {}, c20 = {}, c21 = {}, c30 = {}, c31 = {};
+  int buf = 0;
+  GS_F2_ISSUE(0, 0)
+  for (int k0 = 0; k0 < K; k0 += FK) {
+    if (k0 + FK < K) {
+      GS_F2_ISSUE(buf ^ 1, k0 + FK)
+      asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    const float* as = lds + buf * FSTAGE;
+    const float* bs = as + W2M * FK;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int co = ((2 * hl + u) ^ swz) << 2;
+      const fx4 a0 = *(const fx4*)(as + ra0 + co);
+      const fx4 a1 = *(const fx4*)(as + ra0 + 32 * FK + co);
+      const fx4 a2 = *(const fx4*)(as + ra0 + 64 * FK + co);
+      const fx4 a3 = *(const fx4*)(as + ra0 + 96 * FK + co);
+      const fx4 b0 = *(const fx4*)(bs + rb0 + co);
+      const fx4 b1 = *(const fx4*)(bs + rb0 + 32 * FK + co);
+#define GS_F2_MM(X)                                                                          \
+  c00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.X, b0.X, c00, 0, 0, 0);                      \
+  c01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.X, b1.X, c01, 0, 0, 0);                      \
+  c10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b0.X, c10, 0, 0, 0);                      \
+  c11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b1.X, c11, 0, 0, 0);                      \
+  c20 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2.X, b0.X, c20, 0, 0, 0);                      \
+  c21 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2.X, b1.X, c21, 0, 0, 0);                      \
+  c30 = __builtin_amdgcn_mfma_f32_32x32x2f32(a3.X, b0.X, c30, 0, 0, 0);                      \
+  c31 = __builtin_amdgcn_mfma_f32_32x32x2f32(a3.X, b1.X, c31, 0, 0, 0);
+      GS_F2_MM(x)
+      GS_F2_MM(y)
+      GS_F2_MM(z)
+      GS_F2_MM(w)
+#undef GS_F2_MM
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    buf ^= 1;
+  }
+#undef GS_F2_ISSUE
+  const int mw = m0 + wm * 128, nw = n0 + wn * 64;
+  float* stage = lds + wave * 32 * W2_SS;
   if (p.flags & EPI_ROPE) {
     w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
     w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
@@ -1526,6 +1627,28 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   int kern = b.kernel;
   if (kern == 0) {
     kern = dl_ok && long_k ? 2 : 1;
+    // large unsplit launches with plain rows: the 256 x 128 kernel, when its
+    // tiles fill the CUs at least once
+    if (!bf16 && blayout == B_NT && !a_relu && b.ksplit == 1 && aload == A_PLAIN) {
+      int ft = 0, ftot = 0;
+      bool ok = true;
+      for (int i = 0; i < b.ngroups; ++i) {
+        const GemmArgs& g = b.g[i];
+        const int t = ((g.M + W2M - 1) / W2M) * ((g.N + W2N - 1) / W2N);
+        ft = std::max(ft, t);
+        ftot += t;
+        ok = ok && g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
+             aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+      }
+      if (ok && ftot >= kF2MinTiles) {
+        hipEvent_t ev = prof_start(s);
+        hipLaunchKernelGGL(gemm_f32_w2_kernel, dim3(ft, 1, b.ngroups), dim3(256), 0, s, b);
+        GS_CHECK_HIP(hipGetLastError());
+        if (ev)
+          prof_stop(s, ev, gemm_prof_name("gemm_f32_w2_kernel<A_PLAIN>", b).c_str(), flops, bytes);
+        return 0;
+      }
+    }
   } else {
     GS_REQUIRE(kern >= 1 && kern <= 3 && !bf16, "gemm: unknown fp32 kernel request");
     GS_REQUIRE(kern != 3 || blayout == B_NT, "gemm: the bf16x6 kernel takes NT B");
