@@ -1111,18 +1111,42 @@ __global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
 }
 
 // fp32 kernel of the same structure for large launches with plain rows:
-// workgroup tile 256 x 128 of 2 x 2 waves at 128 x 64 (4 x 2 blocks of
-// v_mfma_f32_32x32x2_f32), 16-deep K steps (64-byte rows: the bf16 kernel's
-// LDS geometry, loader and slot swizzle) streamed into two LDS stages
-// (48 KB), three workgroups per CU, epilogue through w2_epi_row. Lane l
-// (half h) feeds MFMA step t of a K step with k = 8h + t.
+// workgroup tile BM x 128 (BM = 256 or 192) of 2 x 2 waves at (BM / 2) x 64
+// (BM / 64 x 2 blocks of v_mfma_f32_32x32x2_f32), 16-deep K steps (64-byte
+// rows: the bf16 kernel's LDS geometry, loader and slot swizzle) streamed into
+// two LDS stages (48 / 40 KB), three workgroups per CU, epilogue through
+// w2_epi_row. Lane l (half h) feeds MFMA step t of a K step with k = 8h + t.
+// BM = 192 serves launches whose 256-row tiles would leave part of the last
+// round of workgroup slots empty (the decoder's N = 768 linears: 576 tiles of
+// 256 rows on 768 slots, exactly 768 of 192 rows).
+template <int BM>
+__device__ __forceinline__ bool f2_tile(const GemmArgs& p, int& m0, int& n0) {
+  const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + W2N - 1) / W2N;
+  const int ntiles = tiles_m * tiles_n;
+  int bid = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  if (bid >= ntiles) return false;
+  const int per_group = GROUP_M * tiles_n;
+  const int gid = bid / per_group;
+  const int first_m = gid * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  m0 = (first_m + (bid % per_group) % gsz) * BM;
+  n0 = ((bid % per_group) / gsz) * W2N;
+  return true;
+}
+
+template <int BM>
 __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   constexpr int FK = 16;                     // floats per K step
-  constexpr int FSTAGE = (W2M + W2N) * FK;   // floats per LDS stage
+  constexpr int WTM = BM / 64;               // 32-row blocks per wave
+  constexpr int FSTAGE = (BM + W2N) * FK;    // floats per LDS stage
+  static_assert(BM == 256 || BM == 192, "tile rows");
+  static_assert(4 * 32 * W2_SS <= 2 * FSTAGE, "epilogue stages fit the LDS stages");
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
   int m0, n0;
-  if (!w2_tile(p, m0, n0)) return;
+  if (!f2_tile<BM>(p, m0, n0)) return;
   __shared__ __attribute__((aligned(16))) float lds[2 * FSTAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1130,10 +1154,10 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   const int wm = wave >> 1, wn = wave & 1;
   const int l32 = lane & 31, hl = lane >> 5;
   const int rin = lane >> 2, chunk = (lane & 3) ^ ((rin >> 2) & 3);
-  const float* ag[W2M / 64];
+  const float* ag[BM / 64];
   const float* bg[W2N / 64];
 #pragma unroll
-  for (int i = 0; i < W2M / 64; ++i) {
+  for (int i = 0; i < BM / 64; ++i) {
     const int64_t m = min(m0 + 16 * (4 * i + wave) + rin, M - 1);
     ag[i] = p.A + m * p.lda + 4 * chunk;
   }
@@ -1145,32 +1169,37 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   const uint32_t lds0 = lds_addr(lds);
 #define GS_F2_ISSUE(BUF, K0)                                                                 \
   {                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < W2M / 64; ++i)                                     \
+    _Pragma("unroll") for (int i = 0; i < BM / 64; ++i)                                      \
       lds_dma16(ag[i] + (K0), lds0 + ((BUF) * FSTAGE + 16 * (4 * i + wave) * FK) * 4);       \
     _Pragma("unroll") for (int i = 0; i < W2N / 64; ++i)                                     \
-      lds_dma16(bg[i] + (K0), lds0 + ((BUF) * FSTAGE + (W2M + 16 * (4 * i + wave)) * FK) * 4); \
+      lds_dma16(bg[i] + (K0), lds0 + ((BUF) * FSTAGE + (BM + 16 * (4 * i + wave)) * FK) * 4); \
   }
   const int swz = (l32 >> 2) & 3;
-  const int ra0 = (wm * 128 + l32) * FK, rb0 = (wn * 64 + l32) * FK;
+  const int ra0 = (wm * 32 * WTM + l32) * FK, rb0 = (wn * 64 + l32) * FK;
   floatx16 c00 = {}, c01 = {}, c10 = {}, c11 = {}, c20 = {}, c21 = {}, c30 = {}, c31 = {};
   int buf = 0;
   GS_F2_ISSUE(0, 0)
   for (int k0 = 0; k0 < K; k0 += FK) {
+    // each wave waits for its own BM / 64 + 2 loads of step k0
     if (k0 + FK < K) {
       GS_F2_ISSUE(buf ^ 1, k0 + FK)
-      asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+      if constexpr (BM == 256)
+        asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory");
     } else {
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     }
     const float* as = lds + buf * FSTAGE;
-    const float* bs = as + W2M * FK;
+    const float* bs = as + BM * FK;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int co = ((2 * hl + u) ^ swz) << 2;
       const fx4 a0 = *(const fx4*)(as + ra0 + co);
       const fx4 a1 = *(const fx4*)(as + ra0 + 32 * FK + co);
       const fx4 a2 = *(const fx4*)(as + ra0 + 64 * FK + co);
-      const fx4 a3 = *(const fx4*)(as + ra0 + 96 * FK + co);
+      fx4 a3 = {};
+      if constexpr (WTM == 4) a3 = *(const fx4*)(as + ra0 + 96 * FK + co);
       const fx4 b0 = *(const fx4*)(bs + rb0 + co);
       const fx4 b1 = *(const fx4*)(bs + rb0 + 32 * FK + co);
 #define GS_F2_MM(X)                                                                          \
@@ -1180,8 +1209,10 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   c11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b1.X, c11, 0, 0, 0);                      \
   c20 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2.X, b0.X, c20, 0, 0, 0);                      \
   c21 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2.X, b1.X, c21, 0, 0, 0);                      \
-  c30 = __builtin_amdgcn_mfma_f32_32x32x2f32(a3.X, b0.X, c30, 0, 0, 0);                      \
-  c31 = __builtin_amdgcn_mfma_f32_32x32x2f32(a3.X, b1.X, c31, 0, 0, 0);
+  if constexpr (WTM == 4) {                                                                  \
+    c30 = __builtin_amdgcn_mfma_f32_32x32x2f32(a3.X, b0.X, c30, 0, 0, 0);                    \
+    c31 = __builtin_amdgcn_mfma_f32_32x32x2f32(a3.X, b1.X, c31, 0, 0, 0);                    \
+  }
       GS_F2_MM(x)
       GS_F2_MM(y)
       GS_F2_MM(z)
@@ -1192,18 +1223,18 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
     buf ^= 1;
   }
 #undef GS_F2_ISSUE
-  const int mw = m0 + wm * 128, nw = n0 + wn * 64;
+  const int mw = m0 + wm * 32 * WTM, nw = n0 + wn * 64;
   float* stage = lds + wave * 32 * W2_SS;
   if (p.flags & EPI_ROPE) {
     w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
     w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
     w2_epi_row<true>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
-    w2_epi_row<true>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
+    if constexpr (WTM == 4) w2_epi_row<true>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
   } else {
     w2_epi_row<false>(p, c00, c01, mw, nw, stage, lane, l32, hl);
     w2_epi_row<false>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
     w2_epi_row<false>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
-    w2_epi_row<false>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
+    if constexpr (WTM == 4) w2_epi_row<false>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
   }
 }
 
@@ -1630,22 +1661,33 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     // large unsplit launches with plain rows: the 256 x 128 kernel, when its
     // tiles fill the CUs at least once
     if (!bf16 && blayout == B_NT && !a_relu && b.ksplit == 1 && aload == A_PLAIN) {
-      int ft = 0, ftot = 0;
+      // 256-row tiles, else 192-row tiles, if they fill the CUs at least once
+      int t256 = 0, tot256 = 0, t192 = 0, tot192 = 0;
       bool ok = true;
       for (int i = 0; i < b.ngroups; ++i) {
         const GemmArgs& g = b.g[i];
-        const int t = ((g.M + W2M - 1) / W2M) * ((g.N + W2N - 1) / W2N);
-        ft = std::max(ft, t);
-        ftot += t;
+        const int tn = (g.N + W2N - 1) / W2N;
+        const int ta = ((g.M + 255) / 256) * tn, tb = ((g.M + 191) / 192) * tn;
+        t256 = std::max(t256, ta);
+        tot256 += ta;
+        t192 = std::max(t192, tb);
+        tot192 += tb;
         ok = ok && g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
              aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
       }
-      if (ok && ftot >= kF2MinTiles) {
+      const int bm = !ok ? 0 : tot256 >= kF2MinTiles ? 256 : tot192 >= kF2MinTiles ? 192 : 0;
+      if (bm) {
         hipEvent_t ev = prof_start(s);
-        hipLaunchKernelGGL(gemm_f32_w2_kernel, dim3(ft, 1, b.ngroups), dim3(256), 0, s, b);
+        if (bm == 256)
+          hipLaunchKernelGGL(gemm_f32_w2_kernel<256>, dim3(t256, 1, b.ngroups), dim3(256), 0, s, b);
+        else
+          hipLaunchKernelGGL(gemm_f32_w2_kernel<192>, dim3(t192, 1, b.ngroups), dim3(256), 0, s, b);
         GS_CHECK_HIP(hipGetLastError());
         if (ev)
-          prof_stop(s, ev, gemm_prof_name("gemm_f32_w2_kernel<A_PLAIN>", b).c_str(), flops, bytes);
+          prof_stop(s, ev,
+                    gemm_prof_name(bm == 256 ? "gemm_f32_w2_kernel<256>" : "gemm_f32_w2_kernel<192>",
+                                   b).c_str(),
+                    flops, bytes);
         return 0;
       }
     }
