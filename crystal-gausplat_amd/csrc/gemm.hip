@@ -1525,6 +1525,12 @@ int plan_ksplit(const GemmBatch& b, int max_tiles) {
 
 }  // namespace
 
+bool gemm_f32_w2_takes(int64_t M, int N, int ngroups) {
+  const int64_t tn = (N + W2N - 1) / W2N;
+  return ((M + 255) / 256) * tn * ngroups >= kF2MinTiles ||
+         ((M + 191) / 192) * tn * ngroups >= kF2MinTiles;
+}
+
 int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
                 hipStream_t s, bool bf16) {
   GS_REQUIRE(b_in.ngroups >= 1 && b_in.ngroups <= kMaxGroups, "gemm: bad group count");
@@ -1675,7 +1681,16 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
         ok = ok && g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
              aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
       }
-      const int bm = !ok ? 0 : tot256 >= kF2MinTiles ? 256 : tot192 >= kF2MinTiles ? 192 : 0;
+      // the tile height whose tiles fill the last round of workgroup slots
+      // best (decoder qkv / kv: 2.25 / 1.5 rounds of 256-row tiles, 3 / 2 of
+      // 192-row tiles); ties go to 256 rows
+      auto fill = [](int t) {
+        const int rounds = (t + kF2MinTiles - 1) / kF2MinTiles;
+        return (double)t / ((double)rounds * kF2MinTiles);
+      };
+      int bm = 0;
+      if (ok && tot256 >= kF2MinTiles) bm = 256;
+      if (ok && tot192 >= kF2MinTiles && (bm == 0 || fill(tot192) > fill(tot256))) bm = 192;
       if (bm) {
         hipEvent_t ev = prof_start(s);
         if (bm == 256)

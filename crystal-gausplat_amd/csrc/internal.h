@@ -137,6 +137,11 @@ struct GemmBatch {
 int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
                 hipStream_t s, bool bf16 = false);
 int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16 = false);
+// True when an fp32 plain-row launch of ngroups problems of M x N (aligned,
+// NT weights, no scatter) runs the 256 x 128 (or 192-row) direct-to-LDS
+// kernel. The model materialises a LayerNorm for such launches instead of
+// applying it in the GEMM's A load.
+bool gemm_f32_w2_takes(int64_t M, int N, int ngroups);
 
 // ---- attention -----------------------------------------------------------------
 struct AttnArgs {

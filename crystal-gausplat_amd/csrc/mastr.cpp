@@ -384,8 +384,14 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   const bool hb = f.precision == 1;
   const int aH = hb ? A_PLAIN_H : A_PLAIN;
   // fp32 products (precisions 0 and 2): the norm1 / norm2 apply steps run in
-  // the qkv / fc1 A loads, after a statistics-only LayerNorm pass
-  const bool fuse = f.precision != 1 && f.linear_layout == 0;
+  // the qkv / fc1 A loads, after a statistics-only LayerNorm pass, except
+  // where the plain-row launch runs the 256 x 128 fp32 kernel: there the
+  // normalised rows are written once and that kernel reads them (measured at
+  // config 3: encoder fc1 125 -> 136 TFLOP/s, qkv 122 -> 134, with the
+  // LayerNorm pass 25 us longer)
+  const bool fuse0 = f.precision != 1 && f.linear_layout == 0;
+  const bool fuse = fuse0 && !(f.precision == 0 && gemm_f32_w2_takes(M, 3 * D, 1));
+  const bool fuse_mlp = fuse0 && !(f.precision == 0 && gemm_f32_w2_takes(M, f.enc_mlp, 1));
   const LnFuse ln1{c.lnst, W(c, p + ".norm1.weight"), W(c, p + ".norm1.bias")};
   const LnFuse ln2{c.lnst, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias")};
   if (fuse) {
@@ -403,7 +409,7 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   ab.ngroups = 1;
   RC(attention(c, ab, s));
   RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s, 1, 0, aH));
-  if (fuse) {
+  if (fuse_mlp) {
     RC(layernorm1(x, ln2.g, ln2.b, nullptr, M, D, f.ln_eps, s, false, c.lnst));
     RC(linear_mode(c, p + ".mlp.fc1", x, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D, EPI_GELU, s, 1, 0,
                    A_LN, ln2));
@@ -463,13 +469,17 @@ int decoder(Ctx& c, int B, hipStream_t s) {
     float* mc[2] = {c.mlp, c.mlp + Mv * f.dec_mlp};
     // LayerNorm of src per chain. fp32 products (precisions 0 and 2): a
     // statistics-only pass, the apply step runs in the next GEMM's A load
-    // (A_LN) on src; otherwise the normalised rows are written to dst. Sets
-    // the next GEMM's A sources (asrc) and loader (al).
-    const bool fuse = f.precision != 1 && f.linear_layout == 0;
+    // (A_LN) on src; otherwise, and where the next GEMM (n_next columns per
+    // chain) is a plain-row launch of the 256 x 128 fp32 kernel, the
+    // normalised rows are written to dst. Sets the next GEMM's A sources
+    // (asrc) and loader (al).
+    const bool fuse0 = f.precision != 1 && f.linear_layout == 0;
+    bool fuse = fuse0;
     const float* asrc[2];
     int al = aH;
     const char* lnm = "";
-    auto ln2 = [&](const char* nm, float* const* src, float* const* dst) {
+    auto ln2 = [&](const char* nm, float* const* src, float* const* dst, int n_next) {
+      fuse = fuse0 && !(f.precision == 0 && gemm_f32_w2_takes(Mv, n_next, 2));
       LnBatch bt;
       for (int k = 0; k < 2; ++k) {
         bt.g[k] = LnArgs{src[k], W(c, p[k] + nm + ".weight"), W(c, p[k] + nm + ".bias"),
@@ -495,7 +505,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       other[0] = c.dmem;
       other[1] = c.dmem + Mv * D;
     }
-    RC(ln2(".norm_y", other, yc));
+    RC(ln2(".norm_y", other, yc, 2 * D));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
@@ -507,7 +517,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       RC(run2(c, a[0], a[1], al, s));
     }
     // self-attention
-    RC(ln2(".norm1", dc, hc));
+    RC(ln2(".norm1", dc, hc, 3 * D));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
@@ -534,7 +544,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       RC(run2(c, a[0], a[1], aH, s));
     }
     // cross-attention (query norm3, reference role naming)
-    RC(ln2(".norm3", dc, hc));
+    RC(ln2(".norm3", dc, hc, D));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
@@ -560,7 +570,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       RC(run2(c, a[0], a[1], aH, s));
     }
     // MLP (norm2, reference role naming)
-    RC(ln2(".norm2", dc, hc));
+    RC(ln2(".norm2", dc, hc, f.dec_mlp));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
