@@ -33,6 +33,7 @@ namespace {
 constexpr int QT = 128;  // queries per workgroup
 constexpr int KT = 64;   // keys per LDS tile
 constexpr int HD = 64;
+constexpr int kAttnCUs = 256;  // MI355X compute units
 
 // Workgroups go to the 8 XCDs round-robin by linear id, and each XCD has its
 // own L2. The logical (query tile, head, image) of a workgroup is therefore
@@ -706,24 +707,43 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, int prec) {
   }
   GS_REQUIRE(a0.B > 0 && a0.H > 0 && a0.Nq > 0 && a0.Nkv > 0, "attention: bad sizes");
   GS_REQUIRE((int64_t)a0.B * bt.ngroups <= 65535 && a0.H <= 65535, "attention: grid too large");
-  // fp32 launches that would leave CUs idle split the keys into ranges of a
-  // multiple of 64 keys, enough ranges for ~432 workgroups (the GEMM split
-  // target; measured gains here are 10-35 % at one image / one pair).
+  // fp32 launches with fewer workgroups than three per CU may split the keys
+  // into ranges of a multiple of 64 keys. The split minimises
+  //   ceil(workgroups / CUs) * (64-key tiles per range) + 0.25 ns units Nq / 16384
+  // (a CU's key tiles, plus the merge pass's round trip of the ranges' partial
+  // outputs), which picks the fastest measured split of the one-image /
+  // one-pair launches: 16 heads x 1 image 2 ranges (40.8 us; 4 ranges 42.6),
+  // 16 heads x 2 images 4 (57.8; 3 ranges 70.2), 12 heads x 2 chains 3
+  // (49.5; 4 ranges 57.2); unsplit they take 63.9, 64.7 and 63.5 us.
   AttnBatch b = bt;
   const int64_t units = (int64_t)a0.H * a0.B * bt.ngroups;
   const int qtiles = (a0.Nq + QT - 1) / QT;
   const int requested = bt.kv_split;
   b.kv_split = 1;
-  if (!bf16 && b.part_ws && a0.Nkv >= 2 * KT &&
-      (requested > 1 || (requested == 0 && units * qtiles < 432))) {
-    int want = requested > 1 ? requested : (int)((432 + units * qtiles - 1) / (units * qtiles));
-    for (; want >= 2; --want) {
+  auto fits = [&](int ns) { return units * a0.Nq * ns * 66 <= b.part_ws_elems; };
+  if (!bf16 && b.part_ws && a0.Nkv >= 2 * KT && requested > 1) {
+    for (int want = requested; want >= 2; --want) {
       const int chunk = ((a0.Nkv + want - 1) / want + KT - 1) / KT * KT;
       const int ns = (a0.Nkv + chunk - 1) / chunk;
-      if (ns >= 2 && units * a0.Nq * ns * 66 <= b.part_ws_elems) {
+      if (ns >= 2 && fits(ns)) {
         b.kv_split = ns;
         b.kv_chunk = chunk;
         break;
+      }
+    }
+  } else if (!bf16 && b.part_ws && a0.Nkv >= 2 * KT && requested == 0 &&
+             units * qtiles < 3 * kAttnCUs) {
+    const int ktiles = (a0.Nkv + KT - 1) / KT;
+    double best = (double)((units * qtiles + kAttnCUs - 1) / kAttnCUs) * ktiles;
+    for (int per = ktiles - 1; per >= 1; --per) {  // key tiles per range
+      const int ns = (ktiles + per - 1) / per;
+      if (ns < 2 || !fits(ns)) continue;
+      const double cost = (double)((units * qtiles * ns + kAttnCUs - 1) / kAttnCUs) * per +
+                          0.25 * ns * (double)units * a0.Nq / 16384.0;
+      if (cost < best) {
+        best = cost;
+        b.kv_split = ns;
+        b.kv_chunk = per * KT;
       }
     }
   }

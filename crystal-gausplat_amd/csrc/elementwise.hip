@@ -7,11 +7,6 @@
 namespace gs {
 namespace {
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
-  return v;
-}
 
 // LayerNorm#forward_cpu (src/nn/layernorm.cr:192-240): two-pass mean /
 // variance, inv_std = 1/sqrt(var + eps), y = (x - mean)*inv_std*gamma + beta.

@@ -222,6 +222,15 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16&
     gemm_epilogue_t<false>(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
 }
 
+// Split-K range of workgroup row blockIdx.y: the K steps (of `unit` elements)
+// are cut at floor(y * steps / S), so ranges differ by at most one step and S
+// need not divide the step count (the host keeps every range non-empty).
+__device__ __forceinline__ void split_range(int K, int S, int unit, int& kbeg, int& kend) {
+  const int steps = K / unit, y = blockIdx.y;
+  kbeg = (int)((int64_t)y * steps / S) * unit;
+  kend = (int)((int64_t)(y + 1) * steps / S) * unit;
+}
+
 // Split-K: the raw accumulators of K range blockIdx.y go to
 // part[blockIdx.y][row][col]; gemm_splitk_reduce applies the epilogue.
 __device__ __forceinline__ void store_partial(const GemmArgs& p, const floatx16& acc00,
@@ -298,6 +307,67 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
   }
   *(fx4*)(p.C + (int64_t)row * p.ldc + c0) = v;
   if (flags & EPI_DUAL) *(fx4*)(p.C2 + (int64_t)row * p.ldc + c0) = v;
+}
+
+// gemm_splitk_reduce for launches with EPI_LNOUT: one wavefront per output row
+// (columns 4 * (lane + 64 i)) sums the partials in split order and applies
+// the bias / residual epilogue in gemm_splitk_reduce's order, stores the row,
+// then writes its LayerNorm with layernorm_kernel's per-lane sums, wavefront
+// reduction and expression, so both outputs are bit-identical to the reduce
+// pass followed by the LayerNorm kernel. N <= 256 * NV, N % 4 == 0.
+template <int NV>
+__global__ __launch_bounds__(256) void gemm_splitk_reduce_ln(GemmBatch batch) {
+  const GemmArgs& p = batch.g[blockIdx.y];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  if (row >= p.M) return;
+  const int N = p.N, nv = N >> 2, S = batch.ksplit, flags = p.flags;
+  fx4 v[NV];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < nv) {
+      const int c0 = 4 * idx;
+      fx4 x = splitk_sum(p, S, row * N + c0);
+      if (flags & EPI_BIAS) x = x + *(const fx4*)(p.bias + c0);
+      if (flags & EPI_RES1) x = x + *(const fx4*)(p.R1 + row * p.ldr1 + c0);
+      if (flags & EPI_RES2) x = *(const fx4*)(p.R2 + row * p.ldr2 + c0) + x;
+      *(fx4*)(p.C + row * p.ldc + c0) = x;
+      v[i] = x;
+      s += x.x + x.y + x.z + x.w;
+    } else {
+      v[i] = mk4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+  const float mean = wave_sum(s) / (float)N;
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < nv) {
+      const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+      q += a * a + b * b + c * c + d * d;
+    }
+  }
+  const float var = wave_sum(q) / (float)N;
+  const float inv = 1.0f / sqrtf(var + p.lnout_eps);
+  const fx4* g4 = (const fx4*)p.lnout_g;
+  const fx4* b4 = (const fx4*)p.lnout_b;
+  fx4* yr = (fx4*)(p.lnout + row * N);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int idx = lane + 64 * i;
+    if (idx < nv) {
+      const fx4 g = g4[idx], bb = b4[idx];
+      fx4 o;
+      o.x = (v[i].x - mean) * inv * g.x + bb.x;
+      o.y = (v[i].y - mean) * inv * g.y + bb.y;
+      o.z = (v[i].z - mean) * inv * g.z + bb.z;
+      o.w = (v[i].w - mean) * inv * g.w + bb.w;
+      yr[idx] = o;
+    }
+  }
 }
 
 // Global loads of one K step into registers (macros rather than lambdas so the
@@ -478,7 +548,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_kernel(GemmBatch batch) {
   // the end; concat and LayerNorm best at the compiler's placement).
   constexpr int loadpos = ALOAD == A_CONV ? 3 : ALOAD == A_PLAIN ? 1 : 4;
   // split-K: this workgroup's contiguous K range (the whole K when ksplit == 1)
-  const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
+  int kbeg, kend;
+  split_range(K, batch.ksplit, BK, kbeg, kend);
   GS_LOAD_A(kbeg)
   if (fix_at_load) GS_FIX_A()
   GS_LOAD_B_F32(kbeg)
@@ -642,7 +713,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_dl_kernel(GemmBatch batch) {
   }
 
   floatx16 acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};
-  const int Kc = p.K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
+  int kbeg, kend;
+  split_range(p.K, batch.ksplit, BK, kbeg, kend);
   int k0 = kbeg;
   GS_DL_ISSUE(0, k0)
   while (true) {
@@ -785,7 +857,8 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   // group, so every step issues its prefetch.
   constexpr int lp_want = ALOAD == A_CONV ? 3 : (ALOAD == A_PLAIN || ALOAD == A_PLAIN_H) ? 1 : 0;
   constexpr int loadpos = lp_want < 2 * KC ? lp_want : 2 * KC - 1;
-  const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
+  int kbeg, kend;
+  split_range(K, batch.ksplit, SK, kbeg, kend);
   GS_LOAD_STEP(kbeg)
   for (int k0 = kbeg; k0 < kend; k0 += SK) {
     __syncthreads();
@@ -1377,7 +1450,8 @@ __global__ __launch_bounds__(256, 2) void gemm_x6_kernel(GemmBatch batch) {
   acc10 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[TA], b0[TB], acc10, 0, 0, 0);   \
   acc11 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1[TA], b1[TB], acc11, 0, 0, 0);
 
-  const int Kc = K / batch.ksplit, kbeg = blockIdx.y * Kc, kend = kbeg + Kc;
+  int kbeg, kend;
+  split_range(K, batch.ksplit, BK, kbeg, kend);
   int k0 = kbeg;
   GS_X6_LOAD(kbeg, 0)
   if (kbeg + BK < kend) GS_X6_LOAD(kbeg + BK, 1)
@@ -1472,6 +1546,15 @@ int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16) {
   if (a.flags & EPI_BF16OUT)
     GS_REQUIRE(!(a.flags & (EPI_SCATTER | EPI_DUAL)) && a.ldc % 4 == 0,
                "gemm: bf16 output excludes scatter / dual stores");
+  if (a.flags & EPI_LNOUT)
+    GS_REQUIRE(!(a.flags & ~(EPI_BIAS | EPI_RES1 | EPI_RES2 | EPI_LNOUT)) && a.N % 4 == 0 &&
+                   a.N <= 4096 && a.ldc == a.N && a.lnout && a.lnout_g && a.lnout_b &&
+                   aligned16(a.lnout) && aligned16(a.lnout_g) && aligned16(a.lnout_b) &&
+                   aligned16(a.C) && (!(a.flags & EPI_BIAS) || aligned16(a.bias)) &&
+                   (!(a.flags & EPI_RES1) || (a.ldr1 % 4 == 0 && aligned16(a.R1))) &&
+                   (!(a.flags & EPI_RES2) || (a.ldr2 % 4 == 0 && aligned16(a.R2))),
+               "gemm: the LayerNorm output takes bias / residual epilogues, N % 4 == 0, "
+               "N <= 4096, ldc == N and 16-byte aligned operands");
   if (a.flags & EPI_SCATTER)
     GS_REQUIRE(a.sc_r > 0 && a.sc_C > 0 && a.N == a.sc_r * a.sc_r * a.sc_C &&
                    a.sc_Cout <= a.sc_C && a.sc_gh > 0 && a.sc_gw > 0 &&
@@ -1492,6 +1575,7 @@ namespace {
 // one-image / one-pair encoder and decoder shapes (M 768..1536, N 768..4096,
 // K 768..4096) the fastest split was the smallest giving >= 432 workgroups.
 constexpr int kSplitTarget = 432;
+constexpr int kNumCUs = 256;  // MI355X compute units
 bool splitk_eligible(const GemmBatch& b) {
   if (!b.part_ws || !aligned16(b.part_ws)) return false;
   const GemmArgs& g0 = b.g[0];
@@ -1523,13 +1607,63 @@ int plan_ksplit(const GemmBatch& b, int max_tiles) {
   return best;
 }
 
-}  // namespace
-
-bool gemm_f32_w2_takes(int64_t M, int N, int ngroups) {
-  const int64_t tn = (N + W2N - 1) / W2N;
-  return ((M + 255) / 256) * tn * ngroups >= kF2MinTiles ||
-         ((M + 191) / 192) * tn * ngroups >= kF2MinTiles;
+// Split factor of a direct-to-LDS launch with fewer tiles than one round of
+// the 256 x 128 kernel. That kernel keeps the matrix cores busy at one
+// workgroup per CU (its double buffer hides the loads), so a CU's time is its
+// workgroup count times the K steps of each, and a split costs its partial
+// tiles' round trip through the scratch. Cost in units of one workgroup K
+// step (1.88 us), fitted to 95 timed launches of the one-image / one-pair
+// encoder and decoder shapes (M 768..1536, N 768..4096, K 768..4096, S 1..16):
+//   ceil(S * tiles / CUs) * ceil(steps / S) + [S > 1] (0.627 S M N g / 1e6 - 6.1)
+// The S it minimises is the fastest measured one on 13 of the 14 shapes and
+// within 2 % on the last; the 432-workgroup rule of plan_ksplit was up to
+// 22 % slower on six of them. Ranges keep at least 4 K steps.
+int plan_ksplit_dl(const GemmBatch& b, int max_tiles) {
+  if (!splitk_eligible(b)) return 1;
+  const GemmArgs& g0 = b.g[0];
+  const int tiles = max_tiles * b.ngroups, steps = g0.K / BK;
+  const double mn = (double)g0.M * g0.N * b.ngroups;
+  int best = 1;
+  double best_cost = 0.0;
+  for (int S = 1; S <= 16; ++S) {
+    if (S > 1 && (steps / S < 4 || (int64_t)S * g0.M * g0.N * b.ngroups > b.part_ws_elems))
+      break;
+    const double per_cu = (double)((tiles * S + kNumCUs - 1) / kNumCUs);
+    const double cost = per_cu * ((steps + S - 1) / S) + (S > 1 ? 0.627 * S * mn / 1e6 - 6.1 : 0.0);
+    if (S == 1 || cost < best_cost) {
+      best = S;
+      best_cost = cost;
+    }
+  }
+  return best;
 }
+
+// The split-K reduce pass of a launch (with the row LayerNorm for EPI_LNOUT).
+void launch_reduce(const GemmBatch& b, dim3 rgrid, hipStream_t s) {
+  if (b.g[0].flags & EPI_LNOUT) {
+    const dim3 g((unsigned)((b.g[0].M + 3) / 4), b.ngroups);
+    if (b.g[0].N <= 1024)
+      hipLaunchKernelGGL(gemm_splitk_reduce_ln<4>, g, dim3(256), 0, s, b);
+    else
+      hipLaunchKernelGGL(gemm_splitk_reduce_ln<16>, g, dim3(256), 0, s, b);
+  } else {
+    hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);
+  }
+}
+
+// EPI_LNOUT of an unsplit launch: the LayerNorm kernel over the finished C.
+int post_layernorm(const GemmBatch& b, hipStream_t s) {
+  if (b.ksplit > 1 || !(b.g[0].flags & EPI_LNOUT)) return 0;
+  LnBatch lb;
+  lb.ngroups = b.ngroups;
+  for (int i = 0; i < b.ngroups; ++i) {
+    const GemmArgs& g = b.g[i];
+    lb.g[i] = LnArgs{g.C, g.lnout_g, g.lnout_b, g.lnout, g.M, g.N, g.lnout_eps};
+  }
+  return launch_layernorm(lb, s);
+}
+
+}  // namespace
 
 int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
                 hipStream_t s, bool bf16) {
@@ -1545,14 +1679,24 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     const int t = ((b.g[i].M + BM - 1) / BM) * ((b.g[i].N + BN - 1) / BN);
     max_tiles = t > max_tiles ? t : max_tiles;
   }
+  for (int i = 1; i < b.ngroups; ++i)
+    GS_REQUIRE((b.g[i].flags & EPI_LNOUT) == (b.g[0].flags & EPI_LNOUT) &&
+                   (!(b.g[0].flags & EPI_LNOUT) || b.g[i].M == b.g[0].M),
+               "gemm: the LayerNorm output needs the same setting and M in every group");
   if (max_tiles == 0) return 0;
+  // fp32 plain / concat rows with NT weights below one round of 256 x 128
+  // tiles take the direct-to-LDS kernel, split by its own cost model
+  // (measured at one image / one pair: faster than the register-staged
+  // kernel at every split factor of those shapes)
+  const bool dl_ok = !bf16 && blayout == B_NT && !a_relu && (aload == A_PLAIN || aload == A_CONCAT);
+  const bool dl_small = dl_ok && (b.kernel == 2 || (b.kernel == 0 && max_tiles * b.ngroups < kF2MinTiles));
   if (b.ksplit > 1) {  // requested split
     GS_REQUIRE(splitk_eligible(b), "gemm: this launch cannot split K");
-    GS_REQUIRE((b.g[0].K / BK) % b.ksplit == 0 &&
+    GS_REQUIRE(b.g[0].K / BK >= b.ksplit &&
                    (int64_t)b.ksplit * b.g[0].M * b.g[0].N * b.ngroups <= b.part_ws_elems,
-               "gemm: requested split-K must divide the K steps and fit the scratch");
+               "gemm: requested split-K needs a K step per range and must fit the scratch");
   } else {
-    b.ksplit = plan_ksplit(b, max_tiles);
+    b.ksplit = dl_small ? plan_ksplit_dl(b, max_tiles) : plan_ksplit(b, max_tiles);
   }
   int64_t reduce_items = 0;
   if (b.ksplit > 1) {
@@ -1573,10 +1717,10 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
                    ec = (g.flags & EPI_BF16OUT) ? 2.0 : 4.0;
       bytes += ea * g.M * (double)g.K + eb * g.N * (double)g.K + ec * g.M * (double)g.N;
     }
-  // bf16 K step: 64 where it divides every K range, else 32
+  // bf16 K step: 64 where it divides K and every range keeps a whole step
   int bkc = 2;
   for (int i = 0; i < b.ngroups; ++i)
-    if ((b.g[i].K / b.ksplit) % (BK * 2)) bkc = 1;
+    if (b.g[i].K % (BK * 2) || b.g[i].K / (BK * 2) < b.ksplit) bkc = 1;
 #define GS_GEMM_BF16_CASE(AL, RL)                                             \
   if (bf16 && aload == AL && a_relu == RL) {                                  \
     hipEvent_t ev = prof_start(s);                                            \
@@ -1585,11 +1729,11 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     else                                                                      \
       hipLaunchKernelGGL((gemm_bf16_kernel<AL, RL, 1>), grid, block, 0, s, b); \
     if (b.ksplit > 1)                                                         \
-      hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
+      launch_reduce(b, rgrid, s);                                              \
     GS_CHECK_HIP(hipGetLastError());                                          \
     if (ev) prof_stop(s, ev, gemm_prof_name("gemm_bf16_kernel<" #AL "," #RL ">", b).c_str(), \
                       flops, bytes);                                          \
-    return 0;                                                                 \
+    return post_layernorm(b, s);                                              \
   }
   // large unsplit launches with bf16 activations: the 256 x 128 kernel (at
   // least two of its tiles per CU). Measured at config 4 against the 128 x 128
@@ -1613,7 +1757,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
       GS_CHECK_HIP(hipGetLastError());
       if (ev) prof_stop(s, ev, gemm_prof_name("gemm_bf16_w2_kernel<A_PLAIN_H>", b).c_str(), flops,
                         bytes);
-      return 0;
+      return post_layernorm(b, s);
     }
   }
   GS_GEMM_BF16_CASE(A_PLAIN, false)
@@ -1637,33 +1781,33 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     else                                                                      \
       hipLaunchKernelGGL((gemm_x6_kernel<AL, RL, false>), grid, block, 0, s, b); \
     if (b.ksplit > 1)                                                         \
-      hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
+      launch_reduce(b, rgrid, s);                                              \
     GS_CHECK_HIP(hipGetLastError());                                          \
     if (ev) prof_stop(s, ev, gemm_prof_name("gemm_x6_kernel<" NM ">", b).c_str(), \
                       flops, bytes);                                          \
-    return 0;                                                                 \
+    return post_layernorm(b, s);                                              \
   }
 #define GS_GEMM_CASE(AL, BL, RL)                                              \
   if (!bf16 && aload == AL && blayout == BL && a_relu == RL) {                \
     hipEvent_t ev = prof_start(s);                                            \
     hipLaunchKernelGGL((gemm_f32_kernel<AL, BL, RL>), grid, block, 0, s, b);  \
     if (b.ksplit > 1)                                                         \
-      hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
+      launch_reduce(b, rgrid, s);                                              \
     GS_CHECK_HIP(hipGetLastError());                                          \
     if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_kernel<" #AL "," #BL "," #RL ">", b).c_str(), \
                       flops, bytes);                                          \
-    return 0;                                                                 \
+    return post_layernorm(b, s);                                              \
   }
   // fp32 kernel choice. long-K launches take the direct-to-LDS kernel: its
-  // double buffer (64 KB of LDS, two workgroups per CU) pays off from ~2048 K,
-  // while shorter K runs faster on the register-staged kernel at three
-  // workgroups per CU (measured per shape at config 3)
+  // double buffer (64 KB of LDS, two workgroups per CU) pays off from ~2048 K
+  // per workgroup, while shorter K (also a long K cut into split ranges) runs
+  // faster on the register-staged kernel at three workgroups per CU (measured
+  // per shape at config 3 and at one image)
   bool long_k = true;
-  for (int i = 0; i < b.ngroups; ++i) long_k = long_k && b.g[i].K >= 2048;
-  const bool dl_ok = !bf16 && blayout == B_NT && !a_relu && (aload == A_PLAIN || aload == A_CONCAT);
+  for (int i = 0; i < b.ngroups; ++i) long_k = long_k && b.g[i].K / b.ksplit >= 2048;
   int kern = b.kernel;
   if (kern == 0) {
-    kern = dl_ok && long_k ? 2 : 1;
+    kern = dl_ok && (long_k || dl_small) ? 2 : 1;
     // large unsplit launches with plain rows: the 256 x 128 kernel, when its
     // tiles fill the CUs at least once
     if (!bf16 && blayout == B_NT && !a_relu && b.ksplit == 1 && aload == A_PLAIN) {
@@ -1703,7 +1847,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
                     gemm_prof_name(bm == 256 ? "gemm_f32_w2_kernel<256>" : "gemm_f32_w2_kernel<192>",
                                    b).c_str(),
                     flops, bytes);
-        return 0;
+        return post_layernorm(b, s);
       }
     }
   } else {
@@ -1716,11 +1860,11 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     hipEvent_t ev = prof_start(s);                                            \
     hipLaunchKernelGGL((gemm_f32_dl_kernel<AL>), grid, block, 0, s, b);       \
     if (b.ksplit > 1)                                                         \
-      hipLaunchKernelGGL(gemm_splitk_reduce, rgrid, dim3(256), 0, s, b);      \
+      launch_reduce(b, rgrid, s);                                              \
     GS_CHECK_HIP(hipGetLastError());                                          \
     if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_dl_kernel<" #AL ">", b).c_str(), \
                       flops, bytes);                                          \
-    return 0;                                                                 \
+    return post_layernorm(b, s);                                              \
   }
   GS_GEMM_DL_CASE(A_PLAIN)
   GS_GEMM_DL_CASE(A_CONCAT)

@@ -50,6 +50,13 @@ hipEvent_t prof_start(hipStream_t s);
 void prof_stop(hipStream_t s, hipEvent_t start, const char* kernel, double flops,
                double bytes);
 
+// Sum over the 64 lanes of a wavefront (butterfly; every lane gets the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
 // ---- GEMM ------------------------------------------------------------------
 // C[M,N] = A[M,K] . B (+ epilogue). One GEMM problem of a (possibly grouped)
 // launch. All pointers are device pointers.
@@ -71,6 +78,7 @@ enum EpiFlags : int {
   EPI_SCATTER = 64,  // sub-pixel scatter store (ConvT / pixel shuffle)
   EPI_DUAL = 128,    // also store the result to C2 (same ldc)
   EPI_BF16OUT = 256, // C holds bf16 (ldc in elements); not with SCATTER / DUAL
+  EPI_LNOUT = 512,   // also the LayerNorm of every output row into lnout (see GemmArgs)
 };
 
 struct GemmArgs {
@@ -114,6 +122,15 @@ struct GemmArgs {
   int32_t sc_r, sc_C, sc_gh, sc_gw, sc_Cout;
   // split-K partials [ksplit][M][N] of this group (set by launch_gemm)
   float* part;
+  // EPI_LNOUT: once a row of C is final, its LayerNorm over the N columns,
+  // lnout = (c - mean) * inv_std * lnout_g + lnout_b (same arithmetic and
+  // order as the LayerNorm kernel), rows of N floats. Split launches do it in
+  // the reduce pass; otherwise launch_gemm runs the LayerNorm kernel after
+  // the GEMM. Bias / residual epilogues only, N % 4 == 0, N <= 4096, ldc == N.
+  float* lnout;
+  const float* lnout_g;
+  const float* lnout_b;
+  float lnout_eps;
 };
 
 constexpr int kMaxGroups = 2;
@@ -137,11 +154,6 @@ struct GemmBatch {
 int launch_gemm(const GemmBatch& b, int aload, int blayout, bool a_relu,
                 hipStream_t s, bool bf16 = false);
 int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16 = false);
-// True when an fp32 plain-row launch of ngroups problems of M x N (aligned,
-// NT weights, no scatter) runs the 256 x 128 (or 192-row) direct-to-LDS
-// kernel. The model materialises a LayerNorm for such launches instead of
-// applying it in the GEMM's A load.
-bool gemm_f32_w2_takes(int64_t M, int N, int ngroups);
 
 // ---- attention -----------------------------------------------------------------
 struct AttnArgs {

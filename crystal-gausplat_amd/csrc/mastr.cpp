@@ -301,9 +301,26 @@ struct LnFuse {
   const float* b = nullptr;
 };
 
+// The LayerNorm that follows a GEMM on its output rows (EPI_LNOUT): gamma,
+// beta and the destination of the normalised rows.
+struct LnNext {
+  const float* g = nullptr;
+  const float* b = nullptr;
+  float* y = nullptr;
+};
+
+void with_lnout(GemmArgs& a, const Ctx& c, const LnNext& n) {
+  a.flags |= EPI_LNOUT;
+  a.lnout = n.y;
+  a.lnout_g = n.g;
+  a.lnout_b = n.b;
+  a.lnout_eps = c.cfg.ln_eps;
+}
+
 int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, float* C,
                 int64_t ldc, int64_t M, int N, int K, int flags, hipStream_t s, int groups = 1,
-                int rope_cols = 0, int aload = A_PLAIN, LnFuse lnf = LnFuse()) {
+                int rope_cols = 0, int aload = A_PLAIN, LnFuse lnf = LnFuse(),
+                LnNext lnext = LnNext()) {
   const float* Wt = W(c, name + ".weight");
   const float* b = W(c, name + ".bias");
   if (c.cfg.linear_layout == 0) {
@@ -311,6 +328,7 @@ int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, fl
     a.ln_stats = lnf.stats;
     a.ln_g = lnf.g;
     a.ln_b = lnf.b;
+    if (lnext.y) with_lnout(a, c, lnext);
     if (rope_cols) with_rope(a, c, rope_cols);
     if (flags & EPI_RES1) {
       a.R1 = C;
@@ -319,6 +337,7 @@ int linear_mode(Ctx& c, const std::string& name, const float* A, int64_t lda, fl
     return run1(c, a, aload, s);
   }
   GS_REQUIRE(aload == A_PLAIN, "linear: the literal layout takes fp32 activations");
+  GS_REQUIRE(!lnext.y, "linear: the literal layout has no fused LayerNorm output");
   const int Ng = N / groups;
   for (int g = 0; g < groups; ++g) {
     GemmArgs a = lin(A, lda, Wt + (int64_t)g * Ng * K, b ? b + (int64_t)g * Ng : nullptr,
@@ -374,7 +393,11 @@ AttnArgs attn_args(const float* q, int64_t ldq, const float* k, int64_t ldk, con
 }
 
 // MASt3REncoderBlockV2#forward, in place on x [M, De] (M = images * N).
-int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
+// pre_normed: c.h already holds norm1(x) (the previous block's fc2 wrote it);
+// next: the LayerNorm after this block (the next block's norm1 or enc_norm),
+// run on the fc2 output rows by the fc2 launch (fp32 products only).
+int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s, bool pre_normed = false,
+                  LnNext next = LnNext()) {
   const gs_mastr_config& f = c.cfg;
   const int D = f.enc_dim, H = f.enc_heads;
   const std::string p = "enc_blocks." + std::to_string(l);
@@ -383,15 +406,20 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   // are stored as bf16 (the same rounding the GEMM's A load applies to fp32)
   const bool hb = f.precision == 1;
   const int aH = hb ? A_PLAIN_H : A_PLAIN;
-  // fp32 products (precisions 0 and 2): the norm1 / norm2 apply steps run in
-  // the qkv / fc1 A loads, after a statistics-only LayerNorm pass, except
-  // where the plain-row launch runs the 256 x 128 fp32 kernel: there the
-  // normalised rows are written once and that kernel reads them (measured at
-  // config 3: encoder fc1 125 -> 136 TFLOP/s, qkv 122 -> 134, with the
-  // LayerNorm pass 25 us longer)
-  const bool fuse0 = f.precision != 1 && f.linear_layout == 0;
-  const bool fuse = fuse0 && !(f.precision == 0 && gemm_f32_w2_takes(M, 3 * D, 1));
-  const bool fuse_mlp = fuse0 && !(f.precision == 0 && gemm_f32_w2_takes(M, f.enc_mlp, 1));
+  // bf16x6 products (precision 2): the norm1 / norm2 apply steps run in the
+  // qkv / fc1 A loads, after a statistics-only LayerNorm pass. fp32 products
+  // (precision 0) write the normalised rows once and read them as plain
+  // rows: large launches then run the 256 x 128 kernel (measured at config 3:
+  // encoder fc1 125 -> 136 TFLOP/s, qkv 122 -> 134, with the LayerNorm pass
+  // 25 us longer), small ones the direct-to-LDS kernel (one image: qkv 68.8
+  // -> 59.1 us, fc1 70.4 -> 67.9 us, the LayerNorm pass ~2 us longer)
+  const bool fuse = f.precision == 2 && f.linear_layout == 0;
+  const bool fuse_mlp = fuse;
+  // fp32 products: the GEMM before each LayerNorm also writes it (EPI_LNOUT,
+  // in the split-K reduce pass where the launch splits: one launch and one
+  // read of the rows fewer per LayerNorm)
+  const bool chain = f.precision == 0 && f.linear_layout == 0;
+  GS_REQUIRE(!pre_normed || chain, "encoder block: pre-normalised rows need fp32 products");
   const LnFuse ln1{c.lnst, W(c, p + ".norm1.weight"), W(c, p + ".norm1.bias")};
   const LnFuse ln2{c.lnst, W(c, p + ".norm2.weight"), W(c, p + ".norm2.bias")};
   if (fuse) {
@@ -399,7 +427,7 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
     RC(linear_mode(c, p + ".attn.qkv", x, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope, A_LN,
                    ln1));
   } else {
-    RC(layernorm1(x, ln1.g, ln1.b, c.h, M, D, f.ln_eps, s, hb));
+    if (!pre_normed) RC(layernorm1(x, ln1.g, ln1.b, c.h, M, D, f.ln_eps, s, hb));
     RC(linear_mode(c, p + ".attn.qkv", c.h, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope, aH));
   }
   AttnBatch ab;
@@ -408,18 +436,20 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s) {
   ab.g[0].o_bf16 = hb;
   ab.ngroups = 1;
   RC(attention(c, ab, s));
-  RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s, 1, 0, aH));
+  RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s, 1, 0, aH, LnFuse(),
+                 chain ? LnNext{ln2.g, ln2.b, c.h} : LnNext()));
   if (fuse_mlp) {
     RC(layernorm1(x, ln2.g, ln2.b, nullptr, M, D, f.ln_eps, s, false, c.lnst));
     RC(linear_mode(c, p + ".mlp.fc1", x, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D, EPI_GELU, s, 1, 0,
                    A_LN, ln2));
   } else {
-    RC(layernorm1(x, ln2.g, ln2.b, c.h, M, D, f.ln_eps, s, hb));
+    if (!chain) RC(layernorm1(x, ln2.g, ln2.b, c.h, M, D, f.ln_eps, s, hb));
     RC(linear_mode(c, p + ".mlp.fc1", c.h, D, c.mlp, f.enc_mlp, M, f.enc_mlp, D,
                    EPI_GELU | (hb ? EPI_BF16OUT : 0), s, 1, 0, aH));
   }
+  GS_REQUIRE(!next.y || chain, "encoder block: a fused next LayerNorm needs fp32 products");
   RC(linear_mode(c, p + ".mlp.fc2", c.mlp, f.enc_mlp, x, D, M, D, f.enc_mlp, EPI_RES1, s, 1, 0,
-                 aH));
+                 aH, LnFuse(), next));
   return 0;
 }
 
@@ -435,8 +465,20 @@ int encoder_from_patches(Ctx& c, int64_t nimg, float* out, hipStream_t s) {
   } else {
     RC(linear_mode(c, "patch_embed.proj", c.P, K, c.x, D, M, D, K, 0, s));
   }
-  for (int l = 0; l < f.enc_depth; ++l) RC(encoder_block(c, l, c.x, M, s));
-  RC(layernorm1(c.x, W(c, "enc_norm.weight"), W(c, "enc_norm.bias"), out, M, D, f.ln_eps, s));
+  // fp32 products: each block's fc2 also writes the next LayerNorm (the next
+  // block's norm1, after the last block enc_norm into out)
+  const bool chain = f.precision == 0 && f.linear_layout == 0 && f.enc_depth > 0;
+  for (int l = 0; l < f.enc_depth; ++l) {
+    LnNext next;
+    if (chain) {
+      const std::string nn = "enc_blocks." + std::to_string(l + 1) + ".norm1";
+      next = l + 1 < f.enc_depth ? LnNext{W(c, nn + ".weight"), W(c, nn + ".bias"), c.h}
+                                 : LnNext{W(c, "enc_norm.weight"), W(c, "enc_norm.bias"), out};
+    }
+    RC(encoder_block(c, l, c.x, M, s, chain && l > 0, next));
+  }
+  if (!chain)
+    RC(layernorm1(c.x, W(c, "enc_norm.weight"), W(c, "enc_norm.bias"), out, M, D, f.ln_eps, s));
   return 0;
 }
 
@@ -467,19 +509,28 @@ int decoder(Ctx& c, int B, hipStream_t s) {
     float* qc[2] = {c.q, c.q + Mv * D};
     float* ac[2] = {c.att, c.att + Mv * D};
     float* mc[2] = {c.mlp, c.mlp + Mv * f.dec_mlp};
-    // LayerNorm of src per chain. fp32 products (precisions 0 and 2): a
+    // LayerNorm of src per chain. bf16x6 products (precision 2): a
     // statistics-only pass, the apply step runs in the next GEMM's A load
-    // (A_LN) on src; otherwise, and where the next GEMM (n_next columns per
-    // chain) is a plain-row launch of the 256 x 128 fp32 kernel, the
-    // normalised rows are written to dst. Sets the next GEMM's A sources
-    // (asrc) and loader (al).
-    const bool fuse0 = f.precision != 1 && f.linear_layout == 0;
-    bool fuse = fuse0;
+    // (A_LN) on src; otherwise the normalised rows are written to dst (fp32
+    // products read them as plain rows, on the 256 x 128 kernel where the
+    // launch is large and the direct-to-LDS kernel where it is small; one
+    // pair: decoder fc1 96.8 -> 85.4 us, qkv 71.2 -> 63.6, kv 53.5 -> 48.9).
+    // Sets the next GEMM's A sources (asrc) and loader (al).
+    const bool fuse = f.precision == 2 && f.linear_layout == 0;
     const float* asrc[2];
     int al = aH;
     const char* lnm = "";
-    auto ln2 = [&](const char* nm, float* const* src, float* const* dst, int n_next) {
-      fuse = fuse0 && !(f.precision == 0 && gemm_f32_w2_takes(Mv, n_next, 2));
+    // fp32 products: the proj GEMM before norm3 / norm2 writes that
+    // LayerNorm of its output rows into hc (EPI_LNOUT); ln2 then only sets
+    // the next GEMM's sources (written == true)
+    const bool chain = f.precision == 0 && f.linear_layout == 0;
+    auto ln2 = [&](const char* nm, float* const* src, float* const* dst, bool written = false) {
+      if (written) {
+        for (int k = 0; k < 2; ++k) asrc[k] = dst[k];
+        al = aH;
+        lnm = nm;
+        return 0;
+      }
       LnBatch bt;
       for (int k = 0; k < 2; ++k) {
         bt.g[k] = LnArgs{src[k], W(c, p[k] + nm + ".weight"), W(c, p[k] + nm + ".bias"),
@@ -505,7 +556,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       other[0] = c.dmem;
       other[1] = c.dmem + Mv * D;
     }
-    RC(ln2(".norm_y", other, yc, 2 * D));
+    RC(ln2(".norm_y", other, yc));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
@@ -517,7 +568,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       RC(run2(c, a[0], a[1], al, s));
     }
     // self-attention
-    RC(ln2(".norm1", dc, hc, 3 * D));
+    RC(ln2(".norm1", dc, hc));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
@@ -540,11 +591,13 @@ int decoder(Ctx& c, int B, hipStream_t s) {
                    dc[k], D, Mv, D, D, EPI_RES1);
         a[k].R1 = dc[k];
         a[k].ldr1 = D;
+        if (chain)
+          with_lnout(a[k], c, LnNext{W(c, p[k] + ".norm3.weight"), W(c, p[k] + ".norm3.bias"), hc[k]});
       }
       RC(run2(c, a[0], a[1], aH, s));
     }
     // cross-attention (query norm3, reference role naming)
-    RC(ln2(".norm3", dc, hc, D));
+    RC(ln2(".norm3", dc, hc, chain));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
@@ -566,11 +619,13 @@ int decoder(Ctx& c, int B, hipStream_t s) {
                    W(c, p[k] + ".cross_attn.proj.bias"), dc[k], D, Mv, D, D, EPI_RES1);
         a[k].R1 = dc[k];
         a[k].ldr1 = D;
+        if (chain)
+          with_lnout(a[k], c, LnNext{W(c, p[k] + ".norm2.weight"), W(c, p[k] + ".norm2.bias"), hc[k]});
       }
       RC(run2(c, a[0], a[1], aH, s));
     }
     // MLP (norm2, reference role naming)
-    RC(ln2(".norm2", dc, hc, f.dec_mlp));
+    RC(ln2(".norm2", dc, hc, chain));
     {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
