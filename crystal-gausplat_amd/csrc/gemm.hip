@@ -1183,7 +1183,9 @@ __global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
   }
 }
 
-// fp32 kernel of the same structure for large launches with plain rows:
+// fp32 kernel of the same structure for large launches with plain rows or an
+// implicit conv (CONV: each K step's A rows gathered from the NHWC input, see
+// below):
 // workgroup tile BM x 128 (BM = 256 or 192) of 2 x 2 waves at (BM / 2) x 64
 // (BM / 64 x 2 blocks of v_mfma_f32_32x32x2_f32), 16-deep K steps (64-byte
 // rows: the bf16 kernel's LDS geometry, loader and slot swizzle) streamed into
@@ -1209,7 +1211,10 @@ __device__ __forceinline__ bool f2_tile(const GemmArgs& p, int& m0, int& n0) {
   return true;
 }
 
-template <int BM>
+// 64 zero bytes: the source of a padded conv tap's 16-byte loads
+__device__ __attribute__((aligned(64))) float g_zero16[16] = {};
+
+template <int BM, bool CONV>
 __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   constexpr int FK = 16;                     // floats per K step
   constexpr int WTM = BM / 64;               // 32-row blocks per wave
@@ -1229,10 +1234,27 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   const int rin = lane >> 2, chunk = (lane & 3) ^ ((rin >> 2) & 3);
   const float* ag[BM / 64];
   const float* bg[W2N / 64];
+  // implicit conv (A_CONV): per row, the top-left input coordinate of its
+  // window and the address of that (possibly padded) pixel's channel
+  // 4 * chunk; a K step of 16 channels lies inside one tap (Cin % 16 == 0),
+  // so a lane's 16 bytes are contiguous. Taps outside the image, and rows
+  // past M, load from g_zero16.
+  int ohs[BM / 64], ows[BM / 64];
 #pragma unroll
   for (int i = 0; i < BM / 64; ++i) {
-    const int64_t m = min(m0 + 16 * (4 * i + wave) + rin, M - 1);
-    ag[i] = p.A + m * p.lda + 4 * chunk;
+    const int mr = m0 + 16 * (4 * i + wave) + rin;
+    const int64_t m = min(mr, M - 1);
+    if constexpr (CONV) {
+      const int hw = p.cHo * p.cWo;
+      const int img = (int)(m / hw), rem = (int)(m - (int64_t)img * hw);
+      const int oh = rem / p.cWo, ow = rem - oh * p.cWo;
+      const int ih0 = oh * p.cs - p.cp;
+      ows[i] = ow * p.cs - p.cp;
+      ag[i] = p.A + (((int64_t)img * p.cH + ih0) * p.cW + ows[i]) * p.cCin + 4 * chunk;
+      ohs[i] = mr < M ? ih0 : -(1 << 20);  // rows past M: never in bounds
+    } else {
+      ag[i] = p.A + m * p.lda + 4 * chunk;
+    }
   }
 #pragma unroll
   for (int i = 0; i < W2N / 64; ++i) {
@@ -1240,10 +1262,31 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
     bg[i] = p.B + n * p.ldb + 4 * chunk;
   }
   const uint32_t lds0 = lds_addr(lds);
+  // conv tap state of the next step to issue (wave-uniform)
+  int tkh = 0, tkw = 0, tic = 0;
+  const float* zrow = g_zero16 + 4 * chunk;
 #define GS_F2_ISSUE(BUF, K0)                                                                 \
   {                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < BM / 64; ++i)                                      \
-      lds_dma16(ag[i] + (K0), lds0 + ((BUF) * FSTAGE + 16 * (4 * i + wave) * FK) * 4);       \
+    if constexpr (CONV) {                                                                    \
+      const int64_t toff = ((int64_t)tkh * p.cW + tkw) * p.cCin + tic;                       \
+      _Pragma("unroll") for (int i = 0; i < BM / 64; ++i) {                                  \
+        const bool ok = (unsigned)(ohs[i] + tkh) < (unsigned)p.cH &&                          \
+                        (unsigned)(ows[i] + tkw) < (unsigned)p.cW;                            \
+        lds_dma16(ok ? ag[i] + toff : zrow,                                                  \
+                  lds0 + ((BUF) * FSTAGE + 16 * (4 * i + wave) * FK) * 4);                   \
+      }                                                                                      \
+      tic += FK;                                                                             \
+      if (tic == p.cCin) {                                                                   \
+        tic = 0;                                                                             \
+        if (++tkw == p.ck) {                                                                 \
+          tkw = 0;                                                                           \
+          ++tkh;                                                                             \
+        }                                                                                    \
+      }                                                                                      \
+    } else {                                                                                 \
+      _Pragma("unroll") for (int i = 0; i < BM / 64; ++i)                                    \
+        lds_dma16(ag[i] + (K0), lds0 + ((BUF) * FSTAGE + 16 * (4 * i + wave) * FK) * 4);     \
+    }                                                                                        \
     _Pragma("unroll") for (int i = 0; i < W2N / 64; ++i)                                     \
       lds_dma16(bg[i] + (K0), lds0 + ((BUF) * FSTAGE + (BM + 16 * (4 * i + wave)) * FK) * 4); \
   }
@@ -1808,9 +1851,14 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   int kern = b.kernel;
   if (kern == 0) {
     kern = dl_ok && (long_k || dl_small) ? 2 : 1;
-    // large unsplit launches with plain rows: the 256 x 128 kernel, when its
-    // tiles fill the CUs at least once
-    if (!bf16 && blayout == B_NT && !a_relu && b.ksplit == 1 && aload == A_PLAIN) {
+    // large unsplit launches with plain rows or an implicit conv (no ReLU
+    // prologue): the 256 x 128 kernel, when its tiles fill the CUs at least
+    // once. Convs take its 192-row form: the 256-row form's gather state
+    // spills at three workgroups per CU, and measured at the config-3 conv
+    // shapes the 192-row form runs 108-130 TFLOP/s against 106-126 for the
+    // register-staged conv (the spilling 256-row form 104-122)
+    const bool w2_conv = aload == A_CONV;
+    if (!bf16 && blayout == B_NT && !a_relu && b.ksplit == 1 && (aload == A_PLAIN || w2_conv)) {
       // 256-row tiles, else 192-row tiles, if they fill the CUs at least once
       int t256 = 0, tot256 = 0, t192 = 0, tot192 = 0;
       bool ok = true;
@@ -1822,8 +1870,9 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
         tot256 += ta;
         t192 = std::max(t192, tb);
         tot192 += tb;
-        ok = ok && g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
-             aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+        ok = ok && g.K % 16 == 0 && (w2_conv ? g.cCin % 16 == 0 : g.lda % 4 == 0) &&
+             aligned16(g.A) && g.ldb % 4 == 0 && aligned16(g.B) && row_epi_ok(g) &&
+             (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
       }
       // the tile height whose tiles fill the last round of workgroup slots
       // best (decoder qkv / kv: 2.25 / 1.5 rounds of 256-row tiles, 3 / 2 of
@@ -1833,20 +1882,24 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
         return (double)t / ((double)rounds * kF2MinTiles);
       };
       int bm = 0;
-      if (ok && tot256 >= kF2MinTiles) bm = 256;
+      if (ok && tot256 >= kF2MinTiles && !w2_conv) bm = 256;
       if (ok && tot192 >= kF2MinTiles && (bm == 0 || fill(tot192) > fill(tot256))) bm = 192;
       if (bm) {
         hipEvent_t ev = prof_start(s);
+        const dim3 grid2(bm == 256 ? t256 : t192, 1, b.ngroups);
         if (bm == 256)
-          hipLaunchKernelGGL(gemm_f32_w2_kernel<256>, dim3(t256, 1, b.ngroups), dim3(256), 0, s, b);
+          hipLaunchKernelGGL((gemm_f32_w2_kernel<256, false>), grid2, dim3(256), 0, s, b);
+        else if (w2_conv)
+          hipLaunchKernelGGL((gemm_f32_w2_kernel<192, true>), grid2, dim3(256), 0, s, b);
         else
-          hipLaunchKernelGGL(gemm_f32_w2_kernel<192>, dim3(t192, 1, b.ngroups), dim3(256), 0, s, b);
+          hipLaunchKernelGGL((gemm_f32_w2_kernel<192, false>), grid2, dim3(256), 0, s, b);
         GS_CHECK_HIP(hipGetLastError());
-        if (ev)
-          prof_stop(s, ev,
-                    gemm_prof_name(bm == 256 ? "gemm_f32_w2_kernel<256>" : "gemm_f32_w2_kernel<192>",
-                                   b).c_str(),
-                    flops, bytes);
+        if (ev) {
+          const char* nm = bm == 256 ? "gemm_f32_w2_kernel<256>"
+                                     : (w2_conv ? "gemm_f32_w2_kernel<192,A_CONV>"
+                                                : "gemm_f32_w2_kernel<192>");
+          prof_stop(s, ev, gemm_prof_name(nm, b).c_str(), flops, bytes);
+        }
         return post_layernorm(b, s);
       }
     }
