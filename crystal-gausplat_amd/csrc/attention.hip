@@ -343,6 +343,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
 
   floatx16 o0 = {}, o1 = {};
   float m_run = -INFINITY, l_run = 0.f;
+  // rank-one operands of the reference subtraction: k slot 0 of the lanes
+  // with hl == 0 holds 1 (key side) and -m_run (query side)
+  bf16x8 ones_k0 = {}, negm_k0 = {};
+  ones_k0[0] = hl == 0 ? (__bf16)1.0f : (__bf16)0.0f;
 
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
   fx4 rk[4], rv[4];
@@ -396,12 +400,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
     for (int sub = 0; sub < KT / 32; ++sub) {
       const int sb = kbase + sub * 32;
       if (sb >= Nkv) break;
+      // Scores relative to the running reference m_run, which is kept
+      // bf16-exact: a fifth MFMA adds the rank-one product ones x (-m_run)
+      // (k slot 0 of the halves with hl == 0), so the exponentials take the
+      // accumulators as they are and the VALU, which bounds this kernel,
+      // does no subtraction.
       floatx16 s = {};
       const __bf16* kr = &Ks[sub * 32 + l32][hl * 8];
 #pragma unroll
       for (int t = 0; t < 4; ++t)
         s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(*(const bf16x8*)(kr + 16 * t), qf[t], s, 0, 0,
                                                     0);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones_k0, negm_k0, s, 0, 0, 0);
       if (sb + 32 > Nkv) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -412,35 +422,45 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
       float mb = s[0];
 #pragma unroll
       for (int r = 1; r < 16; ++r) mb = fmaxf(mb, s[r]);
-      mb = fmaxf(mb, __shfl_xor(mb, 32));
+      mb = fmaxf(mb, __shfl_xor(mb, 32));  // block maximum relative to m_run (0 at first)
       // Lazy rescaling: the reference maximum m_run only moves (and O, l
       // are rescaled) when some query of the wave sees a score more than
-      // 2^8 above it, so exp2(s - m_run) <= 256 and the rescale multiplies
-      // are skipped for most blocks (the first block always moves it from
-      // -inf). O / l is unchanged by the choice of reference.
-      const float m_cand = fmaxf(m_run, mb);
-      if (__any(m_cand > m_run + 8.0f)) {
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_cand);
+      // 2^8 above it, so exp2(s - m_run) <= 2^8 (and a bf16 rounding) and
+      // the rescale multiplies are skipped for most blocks (the first block
+      // always moves it from -inf). O / l is unchanged by the choice of
+      // reference.
+      if (__any(m_run == -INFINITY || mb > 8.0f)) {
+        const float m_base = m_run == -INFINITY ? 0.f : m_run;
+        const float m_new = (float)(__bf16)fmaxf(m_run, m_base + mb);
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           o0[r] *= alpha;
           o1[r] *= alpha;
         }
-        m_run = m_cand;
+        const float shift = m_new - m_base;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[r] -= shift;
+        m_run = m_new;
+        negm_k0[0] = hl == 0 ? (__bf16)(-m_new) : (__bf16)0.0f;
       }
       float ps = 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        s[r] = __builtin_amdgcn_exp2f(s[r] - m_run);
+        s[r] = __builtin_amdgcn_exp2f(s[r]);
         ps += s[r];
       }
       l_run += ps;
+      // P in bf16, the PV product's B operand
+      u32x4 pq[2];
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) pq[sl][u] = cvt_pk_bf16(s[8 * sl + 2 * u], s[8 * sl + 2 * u + 1]);
 #pragma unroll
       for (int sl = 0; sl < 2; ++sl) {
-        const u32x4 pp = {cvt_pk_bf16(s[8 * sl], s[8 * sl + 1]), cvt_pk_bf16(s[8 * sl + 2], s[8 * sl + 3]),
-                          cvt_pk_bf16(s[8 * sl + 4], s[8 * sl + 5]), cvt_pk_bf16(s[8 * sl + 6], s[8 * sl + 7])};
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, pp);
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, pq[sl]);
         // keys sub*32 + 16 sl + 4 hl + {0..3, 8..11}: key groups 8 sub + 4 sl + hl (+2)
         const int ix = 4 * sub + 2 * sl;
         const bf16x4 va0 = *(const bf16x4*)&Vt[vto[0][ix]];
