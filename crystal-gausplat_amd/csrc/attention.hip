@@ -21,6 +21,7 @@
 // 2^-126 below the running row maximum (exp2(-inf) = 0 for masked keys and
 // for the first rescale).
 #include <string>
+#include <type_traits>
 
 #include "bf16_split.h"
 #include "internal.h"
@@ -293,6 +294,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // per write cycle (an 8-way conflict) and 2 per read.
 __device__ __forceinline__ int vt_swz(int h) { return ((h >> 2) ^ (((h >> 1) & 1) << 3)) & 15; }
 
+// INH: q, k and v hold bf16 (written so by the projection GEMMs); their K and V
+// tiles go to LDS without conversion and the loads move half the bytes.
+template <bool INH>
 __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, int32_t Bcount) {
   const AttnTile tile = attn_tile();
   const int grp = tile.z / Bcount;
@@ -318,9 +322,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
       vto[e][ix] = h * KT + 4 * (G ^ vt_swz(h));
     }
 
-  const float* qb = p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh;
-  const float* kb = p.k + (int64_t)b * p.k_sb + (int64_t)head * p.k_sh;
-  const float* vb = p.v + (int64_t)b * p.v_sb + (int64_t)head * p.v_sh;
+  // element type of q, k, v: fp32, or bf16 (INH); strides are in elements
+  typedef typename std::conditional<INH, __bf16, float>::type in_t;
+  constexpr int ES = sizeof(in_t);
+  const in_t* qb = (const in_t*)p.q + (int64_t)b * p.q_sb + (int64_t)head * p.q_sh;
+  const in_t* kb = (const in_t*)p.k + (int64_t)b * p.k_sb + (int64_t)head * p.k_sh;
+  const in_t* vb = (const in_t*)p.v + (int64_t)b * p.v_sb + (int64_t)head * p.v_sh;
   float* ob = p.o + (int64_t)b * p.o_sb + (int64_t)head * p.o_sh;
 
   const int q0 = tile.x * QT + wave * 32;
@@ -328,11 +335,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
   bf16x8 qf[4];
   {
     const int qrow = min(q0 + l32, Nq - 1);
-    const float* qr = qb + (int64_t)qrow * p.q_sn + hl * 8;
+    const in_t* qr = qb + (int64_t)qrow * p.q_sn + hl * 8;
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const fx4 v0 = *(const fx4*)(qr + 16 * t);
-      const fx4 v1 = *(const fx4*)(qr + 16 * t + 4);
+      fx4 v0, v1;
+      if constexpr (INH) {
+        const u32x4 w = *(const u32x4*)(qr + 16 * t);
+        v0 = mk4(bf16_lo(w[0]), bf16_hi(w[0]), bf16_lo(w[1]), bf16_hi(w[1]));
+        v1 = mk4(bf16_lo(w[2]), bf16_hi(w[2]), bf16_lo(w[3]), bf16_hi(w[3]));
+      } else {
+        v0 = *(const fx4*)(qr + 16 * t);
+        v1 = *(const fx4*)(qr + 16 * t + 4);
+      }
       const u32x4 h = {cvt_pk_bf16(v0.x * qscale, v0.y * qscale),
                        cvt_pk_bf16(v0.z * qscale, v0.w * qscale),
                        cvt_pk_bf16(v1.x * qscale, v1.y * qscale),
@@ -349,7 +363,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
   ones_k0[0] = hl == 0 ? (__bf16)1.0f : (__bf16)0.0f;
 
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
-  fx4 rk[4], rv[4];
+  fx4 rk[4], rv[4];     // fp32 inputs: 4 values each
+  uint64_t hk[4], hv[4];  // bf16 inputs (INH): 4 values each
   // K rows lrow + 16 i; V rows 4 lrow + i, so each thread holds four
   // consecutive keys of V and writes its transpose with 8-byte stores.
   // The loads go through buffer resources whose base is the tile's first key
@@ -360,21 +375,26 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
   uint32_t kvo[4], vvo[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    kvo[i] = (uint32_t)(((int64_t)(lrow + 16 * i) * p.k_sn + lc4) * 4);
-    vvo[i] = (uint32_t)(((int64_t)(4 * lrow + i) * p.v_sn + lc4) * 4);
+    kvo[i] = (uint32_t)(((int64_t)(lrow + 16 * i) * p.k_sn + lc4) * ES);
+    vvo[i] = (uint32_t)(((int64_t)(4 * lrow + i) * p.v_sn + lc4) * ES);
   }
-  const int64_t kspan = ((int64_t)(Nkv - 1) * p.k_sn + HD) * 4;
-  const int64_t vspan = ((int64_t)(Nkv - 1) * p.v_sn + HD) * 4;
+  const int64_t kspan = ((int64_t)(Nkv - 1) * p.k_sn + HD) * ES;
+  const int64_t vspan = ((int64_t)(Nkv - 1) * p.v_sn + HD) * ES;
 #define GS_ATT_LOAD(KB)                                                                      \
   {                                                                                          \
     const int64_t ko = (int64_t)(KB) * p.k_sn, vo = (int64_t)(KB) * p.v_sn;                  \
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(                    \
-        (void*)(kb + ko), (short)0, (int)(kspan - 4 * ko), 0x00020000);                      \
+        (void*)(kb + ko), (short)0, (int)(kspan - ES * ko), 0x00020000);                     \
     const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(                    \
-        (void*)(vb + vo), (short)0, (int)(vspan - 4 * vo), 0x00020000);                      \
+        (void*)(vb + vo), (short)0, (int)(vspan - ES * vo), 0x00020000);                     \
     _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                          \
-      rk[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo[i], 0, 0)); \
-      rv[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vvo[i], 0, 0)); \
+      if constexpr (INH) {                                                                   \
+        hk[i] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(krs, kvo[i], 0, 0)); \
+        hv[i] = __builtin_bit_cast(uint64_t, __builtin_amdgcn_raw_buffer_load_b64(vrs, vvo[i], 0, 0)); \
+      } else {                                                                               \
+        rk[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo[i], 0, 0)); \
+        rv[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vvo[i], 0, 0)); \
+      }                                                                                      \
     }                                                                                        \
   }
 
@@ -383,15 +403,27 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      *(uint64_t*)&Ks[lrow + 16 * i][lc4] =
-          (uint64_t)cvt_pk_bf16(rk[i].x, rk[i].y) | ((uint64_t)cvt_pk_bf16(rk[i].z, rk[i].w) << 32);
-      // V^T (head-dim major): column lc4 + i of the keys 4 lrow .. 4 lrow + 3
-      const float c0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
-      const float c1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
-      const float c2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
-      const float c3[4] = {rv[3].x, rv[3].y, rv[3].z, rv[3].w};
-      *(uint64_t*)&Vt[(lc4 + i) * KT + 4 * (lrow ^ vt_swz(lc4 + i))] =
-          (uint64_t)cvt_pk_bf16(c0[i], c1[i]) | ((uint64_t)cvt_pk_bf16(c2[i], c3[i]) << 32);
+      if constexpr (INH) {
+        *(uint64_t*)&Ks[lrow + 16 * i][lc4] = hk[i];
+        // V^T: column lc4 + i of the keys 4 lrow .. + 3, the 16-bit value i
+        // of each of the four rows, packed in key order
+        const int sh = 16 * (i & 1), w = i >> 1;
+        uint32_t e[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) e[j] = (uint32_t)(hv[j] >> (32 * w + sh)) & 0xffffu;
+        *(uint64_t*)&Vt[(lc4 + i) * KT + 4 * (lrow ^ vt_swz(lc4 + i))] =
+            (uint64_t)(e[0] | (e[1] << 16)) | ((uint64_t)(e[2] | (e[3] << 16)) << 32);
+      } else {
+        *(uint64_t*)&Ks[lrow + 16 * i][lc4] =
+            (uint64_t)cvt_pk_bf16(rk[i].x, rk[i].y) | ((uint64_t)cvt_pk_bf16(rk[i].z, rk[i].w) << 32);
+        // V^T (head-dim major): column lc4 + i of the keys 4 lrow .. 4 lrow + 3
+        const float c0[4] = {rv[0].x, rv[0].y, rv[0].z, rv[0].w};
+        const float c1[4] = {rv[1].x, rv[1].y, rv[1].z, rv[1].w};
+        const float c2[4] = {rv[2].x, rv[2].y, rv[2].z, rv[2].w};
+        const float c3[4] = {rv[3].x, rv[3].y, rv[3].z, rv[3].w};
+        *(uint64_t*)&Vt[(lc4 + i) * KT + 4 * (lrow ^ vt_swz(lc4 + i))] =
+            (uint64_t)cvt_pk_bf16(c0[i], c1[i]) | ((uint64_t)cvt_pk_bf16(c2[i], c3[i]) << 32);
+      }
     }
     __syncthreads();
     GS_ATT_LOAD(min(kbase + KT, ((Nkv - 1) / KT) * KT))
@@ -713,6 +745,10 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, int prec) {
                "attention: grouped problems must share shapes");
     GS_REQUIRE(a.q && a.k && a.v && a.o, "attention: null operand");
     GS_REQUIRE(!a.o_bf16 || bf16, "attention: bf16 output needs the bf16 kernel");
+    GS_REQUIRE(!a.in_bf16 || (bf16 && a.q_sb % 8 == 0 && a.q_sh % 8 == 0 && a.q_sn % 8 == 0),
+               "attention: bf16 q / k / v need the bf16 kernel and q strides that are multiples "
+               "of 8");
+    GS_REQUIRE(a.in_bf16 == a0.in_bf16, "attention: grouped problems must share the input type");
     GS_REQUIRE(aligned16(a.q) && aligned16(a.k) && aligned16(a.v) && aligned16(a.o),
                "attention: operands must be 16-byte aligned");
     const int64_t st[12] = {a.q_sb, a.q_sh, a.q_sn, a.k_sb, a.k_sh, a.k_sn,
@@ -770,7 +806,10 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, int prec) {
   dim3 grid(qtiles * b.kv_split, a0.H, a0.B * bt.ngroups), block(256);
   hipEvent_t ev = prof_start(s);
   if (bf16) {
-    hipLaunchKernelGGL(attn_fwd_bf16_kernel, grid, block, 0, s, b, a0.B);
+    if (a0.in_bf16)
+      hipLaunchKernelGGL(attn_fwd_bf16_kernel<true>, grid, block, 0, s, b, a0.B);
+    else
+      hipLaunchKernelGGL(attn_fwd_bf16_kernel<false>, grid, block, 0, s, b, a0.B);
   } else if (x6 && b.kv_split == 1) {
     hipLaunchKernelGGL(attn_fwd_x6_kernel, grid, block, 0, s, b, a0.B);
   } else if (b.kv_split > 1) {
@@ -793,7 +832,8 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, int prec) {
             std::to_string(a0.Nq) + " groups=" + std::to_string(bt.ngroups) +
             (b.kv_split > 1 ? " kvsplit=" + std::to_string(b.kv_split) : std::string());
     prof_stop(s, ev, nm.c_str(), units * 4.0 * a0.Nq * (double)a0.Nkv * 64.0,
-              units * 64.0 * ((a0.o_bf16 ? 6.0 : 8.0) * a0.Nq + 8.0 * a0.Nkv));
+              units * 64.0 *
+                  ((a0.in_bf16 ? 2.0 : 4.0) * (a0.Nq + 2.0 * a0.Nkv) + (a0.o_bf16 ? 2.0 : 4.0) * a0.Nq));
   }
   return 0;
 }

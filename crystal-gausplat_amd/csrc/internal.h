@@ -165,6 +165,7 @@ struct AttnArgs {
   int32_t B, H, Nq, Nkv;
   float scale;
   int32_t o_bf16 = 0;  // o holds bf16 (strides in elements); bf16 kernel only
+  int32_t in_bf16 = 0; // q, k, v hold bf16 (strides in elements); bf16 kernel only
 };
 struct AttnBatch {
   AttnArgs g[kMaxGroups];

@@ -365,6 +365,13 @@ int layernorm1(const float* x, const float* g, const float* b, float* y, int64_t
   return launch_layernorm(bt, s);
 }
 
+// Column `off` of rows that start at `base`: fp32 elements, or bf16 elements
+// when the producing GEMM wrote bf16 (EPI_BF16OUT); row starts and strides
+// count elements of the same type.
+const float* col_at(const float* base, int64_t off, bool bf16) {
+  return bf16 ? (const float*)((const __bf16*)base + off) : base + off;
+}
+
 AttnArgs attn_args(const float* q, int64_t ldq, const float* k, int64_t ldk, const float* v,
                    int64_t ldv, float* o, int64_t ldo, int B, int H, int N) {
   AttnArgs a;
@@ -428,12 +435,14 @@ int encoder_block(Ctx& c, int l, float* x, int64_t M, hipStream_t s, bool pre_no
                    ln1));
   } else {
     if (!pre_normed) RC(layernorm1(x, ln1.g, ln1.b, c.h, M, D, f.ln_eps, s, hb));
-    RC(linear_mode(c, p + ".attn.qkv", c.h, D, c.qkv, 3 * D, M, 3 * D, D, 0, s, 3, rope, aH));
+    RC(linear_mode(c, p + ".attn.qkv", c.h, D, c.qkv, 3 * D, M, 3 * D, D,
+                   hb ? EPI_BF16OUT : 0, s, 3, rope, aH));
   }
   AttnBatch ab;
-  ab.g[0] = attn_args(c.qkv, 3 * D, c.qkv + D, 3 * D, c.qkv + 2 * D, 3 * D, c.att, D,
+  ab.g[0] = attn_args(c.qkv, 3 * D, col_at(c.qkv, D, hb), 3 * D, col_at(c.qkv, 2 * D, hb), 3 * D, c.att, D,
                       (int)(M / c.N), H, c.N);
   ab.g[0].o_bf16 = hb;
+  ab.g[0].in_bf16 = hb;
   ab.ngroups = 1;
   RC(attention(c, ab, s));
   RC(linear_mode(c, p + ".attn.proj", c.att, D, x, D, M, D, D, EPI_RES1, s, 1, 0, aH, LnFuse(),
@@ -561,7 +570,7 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(asrc[k], D, c.derived[p[k] + ".kv.weight"], c.derived[p[k] + ".kv.bias"],
-                   kvc[k], 2 * D, Mv, 2 * D, D, 0);
+                   kvc[k], 2 * D, Mv, 2 * D, D, hb ? EPI_BF16OUT : 0);
         lnset(a[k], k);
         if (rope) with_rope(a[k], c, D);
       }
@@ -573,16 +582,17 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(asrc[k], D, W(c, p[k] + ".attn.qkv.weight"), W(c, p[k] + ".attn.qkv.bias"),
-                   qkvc[k], 3 * D, Mv, 3 * D, D, 0);
+                   qkvc[k], 3 * D, Mv, 3 * D, D, hb ? EPI_BF16OUT : 0);
         lnset(a[k], k);
         if (rope) with_rope(a[k], c, 2 * D);
       }
       RC(run2(c, a[0], a[1], al, s));
       AttnBatch ab;
       for (int k = 0; k < 2; ++k) {
-        ab.g[k] = attn_args(qkvc[k], 3 * D, qkvc[k] + D, 3 * D, qkvc[k] + 2 * D, 3 * D, ac[k], D, B,
-                            H, c.N);
+        ab.g[k] = attn_args(qkvc[k], 3 * D, col_at(qkvc[k], D, hb), 3 * D,
+                            col_at(qkvc[k], 2 * D, hb), 3 * D, ac[k], D, B, H, c.N);
         ab.g[k].o_bf16 = hb;
+        ab.g[k].in_bf16 = hb;
       }
       ab.ngroups = 2;
       RC(attention(c, ab, s));
@@ -602,15 +612,18 @@ int decoder(Ctx& c, int B, hipStream_t s) {
       GemmArgs a[2];
       for (int k = 0; k < 2; ++k) {
         a[k] = lin(asrc[k], D, W(c, p[k] + ".cross_attn.projq.weight"),
-                   W(c, p[k] + ".cross_attn.projq.bias"), qc[k], D, Mv, D, D, 0);
+                   W(c, p[k] + ".cross_attn.projq.bias"), qc[k], D, Mv, D, D,
+                   hb ? EPI_BF16OUT : 0);
         lnset(a[k], k);
         if (rope) with_rope(a[k], c, D);
       }
       RC(run2(c, a[0], a[1], al, s));
       AttnBatch ab;
       for (int k = 0; k < 2; ++k) {
-        ab.g[k] = attn_args(qc[k], D, kvc[k], 2 * D, kvc[k] + D, 2 * D, ac[k], D, B, H, c.N);
+        ab.g[k] = attn_args(qc[k], D, kvc[k], 2 * D, col_at(kvc[k], D, hb), 2 * D, ac[k], D, B, H,
+                            c.N);
         ab.g[k].o_bf16 = hb;
+        ab.g[k].in_bf16 = hb;
       }
       ab.ngroups = 2;
       RC(attention(c, ab, s));
