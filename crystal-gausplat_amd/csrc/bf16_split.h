@@ -9,12 +9,16 @@
 namespace gs {
 
 // Two floats to packed bf16, the first in the low half (round to nearest
-// even: the instruction the compiler emits for one scalar __bf16 cast, here
-// issued once per pair).
+// even). A vector conversion, which the compiler issues as one
+// v_cvt_pk_bf16_f32 and, unlike an inline-asm form of that instruction, also
+// schedules: it then inserts the wait states that a matrix-core instruction
+// reading the result (and a VALU instruction reading a transcendental's
+// result) needs. Inline asm left those to chance.
+typedef float gs_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 gs_bf16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
-  uint32_t r;
-  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
+  const gs_f32x2 v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, gs_bf16x2));
 }
 __device__ __forceinline__ float bf16_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
