@@ -100,6 +100,7 @@ __global__ void unfold_kernel(const float* __restrict__ img, int32_t B, int32_t 
 // No FMA contraction: a fused sh*oy - y0 moves the lerp weight by an ulp of
 // the source coordinate; this kernel is HBM-bound, so it keeps the plain
 // operation sequence of the CPU formula.
+template <bool OUT_BF16>
 __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict__ x,
                                                          int32_t H, int32_t W, int32_t C,
                                                          int32_t blocks_per_row,
@@ -135,7 +136,14 @@ __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict
   o.w = hy * (hx * a.w + lx * bq.w) + ly * (hx * cq.w + lx * d.w);
   // the output (4x the input) is streamed out with non-temporal stores so it
   // does not displace the source rows that neighbouring output rows re-read
-  __builtin_nontemporal_store(o, (fx4*)(y + ((int64_t)row * Wo * C4 + e) * 4));
+  const int64_t oi = ((int64_t)row * Wo * C4 + e) * 4;
+  if constexpr (OUT_BF16) {  // round to nearest even, the conversion the bf16 GEMMs apply
+    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+    const bf16x4_t h = {(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
+    __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, h), (uint64_t*)((__bf16*)y + oi));
+  } else {
+    __builtin_nontemporal_store(o, (fx4*)(y + oi));
+  }
 }
 
 // 2D RoPE in place; one thread per rotated pair (token, head, axis, j < 16).
@@ -296,7 +304,7 @@ int launch_unfold(const float* img, int32_t B, int32_t H, int32_t W, int32_t p,
 }
 
 int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C,
-                      float* y, hipStream_t s) {
+                      float* y, hipStream_t s, bool out_bf16) {
   GS_REQUIRE(C > 0 && C % 4 == 0 && H > 0 && W > 0 && B >= 0, "upsample2x: need C % 4 == 0");
   GS_REQUIRE(aligned16(x) && aligned16(y), "upsample2x: operands must be 16-byte aligned");
   GS_REQUIRE((int64_t)2 * W * (C / 4) <= INT32_MAX && (int64_t)2 * B * H <= INT32_MAX,
@@ -306,10 +314,14 @@ int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   GS_REQUIRE(nblk < INT32_MAX, "upsample2x: too many elements");
   if (nblk == 0) return 0;
   hipEvent_t ev = prof_start(s);
-  hipLaunchKernelGGL(upsample2x_kernel, dim3((uint32_t)nblk), dim3(256), 0, s, x, H, W, C,
-                     blocks_per_row, y);
+  if (out_bf16)
+    hipLaunchKernelGGL(upsample2x_kernel<true>, dim3((uint32_t)nblk), dim3(256), 0, s, x, H, W, C,
+                       blocks_per_row, y);
+  else
+    hipLaunchKernelGGL(upsample2x_kernel<false>, dim3((uint32_t)nblk), dim3(256), 0, s, x, H, W, C,
+                       blocks_per_row, y);
   GS_CHECK_HIP(hipGetLastError());
-  prof_stop(s, ev, "upsample2x_kernel", 0.0, 4.0 * (double)B * H * W * C * 5.0);
+  prof_stop(s, ev, "upsample2x_kernel", 0.0, (double)B * H * W * C * (4.0 + (out_bf16 ? 8.0 : 16.0)));
   return 0;
 }
 

@@ -458,7 +458,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_ln(GemmBatch batch) {
       lnm[i] = p.ln_stats[2 * (int64_t)arow[i]];                                         \
       lnr[i] = p.ln_stats[2 * (int64_t)arow[i] + 1];                                     \
     }                                                                                    \
-    if (ALOAD == A_CONV) {                                                               \
+    if (ALOAD == A_CONV || ALOAD == A_CONV_H) {                                          \
       const int hw = p.cHo * p.cWo;                                                      \
       const int img = arow[i] / hw;                                                      \
       const int rem = arow[i] - img * hw;                                                \
@@ -836,6 +836,21 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
       const __bf16* Ah = (const __bf16*)p.A;                                     \
       _Pragma("unroll") for (int i = 0; i < 4; ++i)                              \
         rahc[C][i] = *(const bf16x4*)(Ah + (int64_t)arow[i] * p.lda + (K0) + lc4); \
+    } else if (ALOAD == A_CONV_H) {                                              \
+      /* bf16 NHWC input: tap (kh, kw), channels ic0..; padded taps read */      \
+      /* element lc4 (in bounds) and are zeroed at the LDS write */              \
+      const __bf16* Ah = (const __bf16*)p.A;                                     \
+      const int kk = (K0) / p.cCin;                                              \
+      const int ic0 = (K0) - kk * p.cCin;                                        \
+      const int kh = kk / p.ck, kw = kk - kh * p.ck;                             \
+      const int64_t toff = ((int64_t)kh * p.cW + kw) * p.cCin + ic0;             \
+      _Pragma("unroll") for (int i = 0; i < 4; ++i) {                            \
+        const int ih = ohs[i] + kh, iw = ows[i] + kw;                            \
+        const bool ok = aval[i] && (unsigned)ih < (unsigned)p.cH &&               \
+                        (unsigned)iw < (unsigned)p.cW;                           \
+        aok[i] = ok;                                                             \
+        rahc[C][i] = *(const bf16x4*)(Ah + (ok ? cbase[i] + toff : 0) + lc4);     \
+      }                                                                          \
     } else {                                                                     \
       GS_LOAD_A(K0)                                                              \
     }                                                                            \
@@ -855,7 +870,8 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
   // (plain rows after the first group: fp32 rows 14 %, bf16 rows 1 % faster;
   // conv after the third, concat before the first). Clamped to the last
   // group, so every step issues its prefetch.
-  constexpr int lp_want = ALOAD == A_CONV ? 3 : (ALOAD == A_PLAIN || ALOAD == A_PLAIN_H) ? 1 : 0;
+  constexpr int lp_want = (ALOAD == A_CONV || ALOAD == A_CONV_H) ? 3
+                         : (ALOAD == A_PLAIN || ALOAD == A_PLAIN_H) ? 1 : 0;
   constexpr int loadpos = lp_want < 2 * KC ? lp_want : 2 * KC - 1;
   int kbeg, kend;
   split_range(K, batch.ksplit, SK, kbeg, kend);
@@ -869,12 +885,15 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
       const bool* const aok = aokc[c];
       (void)lgb;
       (void)aok;
-      if (ALOAD != A_PLAIN_H) GS_FIX_A()
+      if (ALOAD != A_PLAIN_H && ALOAD != A_CONV_H) GS_FIX_A()
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         bf16x4 h;
         if (ALOAD == A_PLAIN_H) {
           h = rahc[c][i];
+        } else if (ALOAD == A_CONV_H) {
+          const bf16x4 z = {};
+          h = aok[i] ? rahc[c][i] : z;  // padded tap
         } else {
           h.x = (__bf16)ra[i].x;
           h.y = (__bf16)ra[i].y;
@@ -1550,19 +1569,19 @@ int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16) {
   GS_REQUIRE(a.A && a.B && a.C, "gemm: null operand");
   GS_REQUIRE(aligned16(a.A) && aligned16(a.B), "gemm: operands must be 16-byte aligned");
   GS_REQUIRE(a.ldb % 4 == 0, "gemm: ldb must be a multiple of 4");
-  if (aload != A_CONV) GS_REQUIRE(a.lda % 4 == 0 && a.lda >= (aload == A_CONCAT ? a.K1 : a.K),
-                                  "gemm: bad lda");
+  if (aload != A_CONV && aload != A_CONV_H)
+    GS_REQUIRE(a.lda % 4 == 0 && a.lda >= (aload == A_CONCAT ? a.K1 : a.K), "gemm: bad lda");
   if (aload == A_LN)
     GS_REQUIRE(!bf16 && a.ln_stats && a.ln_g && a.ln_b && aligned16(a.ln_g) && aligned16(a.ln_b),
                "gemm: the fused LayerNorm load needs row statistics, gamma and beta "
                "(fp32 kernels)");
-  if (aload == A_PLAIN_H)
+  if (aload == A_PLAIN_H || aload == A_CONV_H)
     GS_REQUIRE(blayout == B_NT && bf16, "gemm: bf16 A needs the bf16 kernel and the NT layout");
   if (aload == A_CONCAT)
     GS_REQUIRE(a.A2 && aligned16(a.A2) && a.K1 % BK == 0 && a.K1 > 0 && a.K1 < a.K &&
                    a.lda2 % 4 == 0 && a.lda2 >= a.K - a.K1,
                "gemm: bad concat operand");
-  if (aload == A_CONV) {
+  if (aload == A_CONV || aload == A_CONV_H) {
     GS_REQUIRE(a.cCin % BK == 0, "conv: Cin must be a multiple of 32");
     GS_REQUIRE(a.K == a.ck * a.ck * a.cCin, "conv: K != k*k*Cin");
     GS_REQUIRE(a.cHo == (a.cH + 2 * a.cp - a.ck) / a.cs + 1 &&
@@ -1756,7 +1775,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     for (int i = 0; i < b.ngroups; ++i) {
       const GemmArgs& g = b.g[i];
       flops += 2.0 * g.M * (double)g.N * g.K;
-      const double ea = aload == A_PLAIN_H ? 2.0 : 4.0, eb = bf16 ? 2.0 : 4.0,
+      const double ea = (aload == A_PLAIN_H || aload == A_CONV_H) ? 2.0 : 4.0, eb = bf16 ? 2.0 : 4.0,
                    ec = (g.flags & EPI_BF16OUT) ? 2.0 : 4.0;
       bytes += ea * g.M * (double)g.K + eb * g.N * (double)g.K + ec * g.M * (double)g.N;
     }
@@ -1808,6 +1827,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   GS_GEMM_BF16_CASE(A_CONCAT, false)
   GS_GEMM_BF16_CASE(A_CONV, false)
   GS_GEMM_BF16_CASE(A_CONV, true)
+  GS_GEMM_BF16_CASE(A_CONV_H, false)
 #undef GS_GEMM_BF16_CASE
   bool presplit = true;
   for (int i = 0; i < b.ngroups; ++i) presplit = presplit && b.g[i].bh_plane > 0;

@@ -65,7 +65,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 // a = (x - mean[row]) * inv_std[row] * gamma[k] + beta[k], the same
 // expression as the LayerNorm kernel (bit-identical operands), row statistics
 // from its stats pass.
-enum ALoad : int { A_PLAIN = 0, A_CONCAT = 1, A_CONV = 2, A_PLAIN_H = 3, A_LN = 4 };
+// A_CONV_H: implicit conv on a bf16 NHWC input (the bf16 kernels only).
+enum ALoad : int { A_PLAIN = 0, A_CONCAT = 1, A_CONV = 2, A_PLAIN_H = 3, A_LN = 4, A_CONV_H = 5 };
 enum BLayout : int { B_NT = 0, B_NN = 1 };
 
 enum EpiFlags : int {
@@ -204,8 +205,9 @@ int launch_layernorm(const LnBatch& b, hipStream_t s);
 // ---- small kernels -----------------------------------------------------------
 int launch_unfold(const float* img, int32_t B, int32_t H, int32_t W, int32_t p,
                   float* out, hipStream_t s);
+// out_bf16: y holds bf16 (for a bf16 conv that reads it, A_CONV_H)
 int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W,
-                      int32_t C, float* y, hipStream_t s);
+                      int32_t C, float* y, hipStream_t s, bool out_bf16 = false);
 int launch_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld,
                   int32_t grid_w, const float* cos_t, const float* sin_t,
                   hipStream_t s);

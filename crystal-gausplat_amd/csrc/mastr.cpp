@@ -683,7 +683,8 @@ struct Heads {
 int conv(Ctx& c, const Heads& hs, const std::string& suffix, const float* const x[2], int imgs,
          int H, int W_, int Cin, int Cout, int k, int stride, int pad, bool bias,
          float* const y[2], int flags, bool relu_in, hipStream_t s,
-         const float* const r1[2] = nullptr, const float* const r2[2] = nullptr) {
+         const float* const r1[2] = nullptr, const float* const r2[2] = nullptr,
+         bool in_bf16 = false) {
   const int Ho = (H + 2 * pad - k) / stride + 1, Wo = (W_ + 2 * pad - k) / stride + 1;
   GemmBatch b;
   b.ngroups = hs.n;
@@ -712,7 +713,10 @@ int conv(Ctx& c, const Heads& hs, const std::string& suffix, const float* const 
     b.g[v] = a;
   }
   const bool pointwise = (k == 1 && stride == 1 && pad == 0);
-  return gemm(c, b, pointwise ? A_PLAIN : A_CONV, relu_in, s);
+  // in_bf16: x holds bf16 (the bf16 mode's head upsample writes it so)
+  GS_REQUIRE(!in_bf16 || (!pointwise && !relu_in && c.cfg.precision == 1),
+             "conv: a bf16 input needs a 3x3 conv without ReLU prologue in the bf16 mode");
+  return gemm(c, b, pointwise ? A_PLAIN : (in_bf16 ? A_CONV_H : A_CONV), relu_in, s);
 }
 
 // ConvTranspose (k == s) from [rows, Cin] token tensors on the gh x gw grid.
@@ -803,10 +807,14 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
   RC(fusion(c, hs, rp + "1", rAc, Lc[0], B, ah[0], aw[0], c.rB, s));
   const int h1 = 2 * ah[0], w1 = 2 * aw[0];
   RC(conv(c, hs, ".dpt.head.0", rBc, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s));
-  for (int v = 0; v < hs.n; ++v) RC(launch_upsample2x(c.hd0[v], B, h1, w1, F / 2, c.hup[v], s));
+  // bf16 mode: the full-resolution upsample feeds only the next conv, so it is
+  // written in bf16 (the rounding that conv's A load would apply) and read so
+  const bool hb = f.precision == 1;
+  for (int v = 0; v < hs.n; ++v)
+    RC(launch_upsample2x(c.hd0[v], B, h1, w1, F / 2, c.hup[v], s, hb));
   const float* hupc[2] = {c.hup[0], c.hup[1]};
   RC(conv(c, hs, ".dpt.head.2", hupc, B, 2 * h1, 2 * w1, F / 2, f.head_mid, 3, 1, 1, true, c.hd2,
-          EPI_RELU, false, s));
+          EPI_RELU, false, s, nullptr, nullptr, hb));
   for (int v = 0; v < hs.n; ++v)
     RC(launch_head_out(c.hd2[v], (int64_t)B * 4 * h1 * w1, f.head_mid,
                        W(c, hs.pre(v) + ".dpt.head.4.weight"), W(c, hs.pre(v) + ".dpt.head.4.bias"),
