@@ -1091,128 +1091,6 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-__device__ __forceinline__ bool w2_tile(const GemmArgs& p, int& m0, int& n0) {
-  const int tiles_m = (p.M + W2M - 1) / W2M, tiles_n = (p.N + W2N - 1) / W2N;
-  const int ntiles = tiles_m * tiles_n;
-  int bid = blockIdx.x;
-  const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
-  if (bid >= ntiles) return false;
-  const int per_group = GROUP_M * tiles_n;
-  const int gid = bid / per_group;
-  const int first_m = gid * GROUP_M;
-  const int gsz = min(tiles_m - first_m, GROUP_M);
-  m0 = (first_m + (bid % per_group) % gsz) * W2M;
-  n0 = ((bid % per_group) / gsz) * W2N;
-  return true;
-}
-
-__global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
-  const GemmArgs& p = batch.g[blockIdx.z];
-  const int M = p.M, N = p.N, K = p.K;
-  int m0, n0;
-  if (!w2_tile(p, m0, n0)) return;
-  __shared__ __attribute__((aligned(16))) __bf16 lds[2 * W2_STAGE];
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
-  const int l32 = lane & 31, hl = lane >> 5;
-  // loader: wave w, instruction i fills tile rows 16 (4i + w) .. +15; the
-  // slot swizzle (r >> 2) & 3 of those rows is (rin >> 2) & 3 for every i
-  const int rin = lane >> 2, chunk = (lane & 3) ^ ((rin >> 2) & 3);
-  const __bf16* Ah = (const __bf16*)p.A;
-  const __bf16* Bh = (const __bf16*)p.Bh;
-  const __bf16* ag[W2M / 64];
-  const __bf16* bg[W2N / 64];
-#pragma unroll
-  for (int i = 0; i < W2M / 64; ++i) {
-    const int64_t m = min(m0 + 16 * (4 * i + wave) + rin, M - 1);
-    ag[i] = Ah + m * p.lda + 8 * chunk;
-  }
-#pragma unroll
-  for (int i = 0; i < W2N / 64; ++i) {
-    const int64_t n = min(n0 + 16 * (4 * i + wave) + rin, N - 1);
-    bg[i] = Bh + n * p.ldb + 8 * chunk;
-  }
-  const uint32_t lds0 = lds_addr((const float*)lds);
-#define GS_W2_ISSUE(BUF, K0)                                                                 \
-  {                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < W2M / 64; ++i)                                     \
-      lds_dma16((const float*)(ag[i] + (K0)),                                                \
-                lds0 + ((BUF) * W2_STAGE + 16 * (4 * i + wave) * W2K) * 2);                  \
-    _Pragma("unroll") for (int i = 0; i < W2N / 64; ++i)                                     \
-      lds_dma16((const float*)(bg[i] + (K0)),                                                \
-                lds0 + ((BUF) * W2_STAGE + (W2M + 16 * (4 * i + wave)) * W2K) * 2);          \
-  }
-  const int swz = (l32 >> 2) & 3;
-  const int ra0 = (wm * 128 + l32) * W2K, rb0 = (wn * 64 + l32) * W2K;
-  floatx16 c00 = {}, c01 = {}, c10 = {}, c11 = {}, c20 = {}, c21 = {}, c30 = {}, c31 = {};
-  int buf = 0;
-  GS_W2_ISSUE(0, 0)
-  for (int k0 = 0; k0 < K; k0 += W2K) {
-    // step k0 in stage buf, step k0 + W2K streaming into the other stage:
-    // each wave waits for its own 6 loads of step k0, the barrier makes all
-    // of them visible; the fragment reads drain before the barrier that lets
-    // the stage be refilled
-    if (k0 + W2K < K) {
-      GS_W2_ISSUE(buf ^ 1, k0 + W2K)
-      asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    }
-    const __bf16* as = lds + buf * W2_STAGE;
-    const __bf16* bs = as + W2M * W2K;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const int co = ((2 * s + hl) ^ swz) << 3;
-      const bf16x8 a0 = *(const bf16x8*)(as + ra0 + co);
-      const bf16x8 a1 = *(const bf16x8*)(as + ra0 + 32 * W2K + co);
-      const bf16x8 a2 = *(const bf16x8*)(as + ra0 + 64 * W2K + co);
-      const bf16x8 a3 = *(const bf16x8*)(as + ra0 + 96 * W2K + co);
-      const bf16x8 b0 = *(const bf16x8*)(bs + rb0 + co);
-      const bf16x8 b1 = *(const bf16x8*)(bs + rb0 + 32 * W2K + co);
-      c00 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, c00, 0, 0, 0);
-      c01 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, c01, 0, 0, 0);
-      c10 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, c10, 0, 0, 0);
-      c11 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, c11, 0, 0, 0);
-      c20 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b0, c20, 0, 0, 0);
-      c21 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b1, c21, 0, 0, 0);
-      c30 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b0, c30, 0, 0, 0);
-      c31 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b1, c31, 0, 0, 0);
-    }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    buf ^= 1;
-  }
-#undef GS_W2_ISSUE
-  // four 32-row block rows per wave through the staged epilogue (the wave's
-  // 32 x 68-float stage; the LDS stages are free after the last barrier)
-  const int mw = m0 + wm * 128, nw = n0 + wn * 64;
-  float* stage = (float*)lds + wave * 32 * W2_SS;
-  if (p.flags & EPI_ROPE) {
-    w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
-    w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
-    w2_epi_row<true>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
-    w2_epi_row<true>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
-  } else {
-    w2_epi_row<false>(p, c00, c01, mw, nw, stage, lane, l32, hl);
-    w2_epi_row<false>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
-    w2_epi_row<false>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
-    w2_epi_row<false>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
-  }
-}
-
-// fp32 kernel of the same structure for large launches with plain rows or an
-// implicit conv (CONV: each K step's A rows gathered from the NHWC input, see
-// below):
-// workgroup tile BM x 128 (BM = 256 or 192) of 2 x 2 waves at (BM / 2) x 64
-// (BM / 64 x 2 blocks of v_mfma_f32_32x32x2_f32), 16-deep K steps (64-byte
-// rows: the bf16 kernel's LDS geometry, loader and slot swizzle) streamed into
-// two LDS stages (48 / 40 KB), three workgroups per CU, epilogue through
-// w2_epi_row. Lane l (half h) feeds MFMA step t of a K step with k = 8h + t.
-// BM = 192 serves launches whose 256-row tiles would leave part of the last
-// round of workgroup slots empty (the decoder's N = 768 linears: 576 tiles of
-// 256 rows on 768 slots, exactly 768 of 192 rows).
 template <int BM>
 __device__ __forceinline__ bool f2_tile(const GemmArgs& p, int& m0, int& n0) {
   const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + W2N - 1) / W2N;
@@ -1232,6 +1110,161 @@ __device__ __forceinline__ bool f2_tile(const GemmArgs& p, int& m0, int& n0) {
 
 // 64 zero bytes: the source of a padded conv tap's 16-byte loads
 __device__ __attribute__((aligned(64))) float g_zero16[16] = {};
+
+// BM = 256 or 192 rows; CONV: the A rows gathered from a bf16 NHWC input
+// (implicit conv, A_CONV_H; a 32-deep K step is 32 channels of one tap, so a
+// lane's 16 bytes are contiguous; padded taps load from g_zero16).
+template <int BM, bool CONV>
+__global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
+  constexpr int WTM = BM / 64;                 // 32-row blocks per wave
+  constexpr int BSTAGE = (BM + W2N) * W2K;     // bf16 per LDS stage
+  static_assert(BM == 256 || BM == 192, "tile rows");
+  static_assert(4 * 32 * W2_SS * 4 <= 2 * BSTAGE * 2, "w2 epilogue stages fit the LDS stages");
+  const GemmArgs& p = batch.g[blockIdx.z];
+  const int M = p.M, N = p.N, K = p.K;
+  int m0, n0;
+  if (!f2_tile<BM>(p, m0, n0)) return;
+  __shared__ __attribute__((aligned(16))) __bf16 lds[2 * BSTAGE];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int l32 = lane & 31, hl = lane >> 5;
+  // loader: wave w, instruction i fills tile rows 16 (4i + w) .. +15; the
+  // slot swizzle (r >> 2) & 3 of those rows is (rin >> 2) & 3 for every i
+  const int rin = lane >> 2, chunk = (lane & 3) ^ ((rin >> 2) & 3);
+  const __bf16* Ah = (const __bf16*)p.A;
+  const __bf16* Bh = (const __bf16*)p.Bh;
+  const __bf16* ag[BM / 64];
+  const __bf16* bg[W2N / 64];
+  int ohs[BM / 64], ows[BM / 64];
+#pragma unroll
+  for (int i = 0; i < BM / 64; ++i) {
+    const int mr = m0 + 16 * (4 * i + wave) + rin;
+    const int64_t m = min(mr, M - 1);
+    if constexpr (CONV) {
+      const int hw = p.cHo * p.cWo;
+      const int img = (int)(m / hw), rem = (int)(m - (int64_t)img * hw);
+      const int oh = rem / p.cWo, ow = rem - oh * p.cWo;
+      const int ih0 = oh * p.cs - p.cp;
+      ows[i] = ow * p.cs - p.cp;
+      ag[i] = Ah + (((int64_t)img * p.cH + ih0) * p.cW + ows[i]) * p.cCin + 8 * chunk;
+      ohs[i] = mr < M ? ih0 : -(1 << 20);  // rows past M: never in bounds
+    } else {
+      ag[i] = Ah + m * p.lda + 8 * chunk;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < W2N / 64; ++i) {
+    const int64_t n = min(n0 + 16 * (4 * i + wave) + rin, N - 1);
+    bg[i] = Bh + n * p.ldb + 8 * chunk;
+  }
+  const uint32_t lds0 = lds_addr((const float*)lds);
+  // conv tap state of the next step to issue (wave-uniform)
+  int tkh = 0, tkw = 0, tic = 0;
+  const float* zrow = g_zero16 + 4 * chunk;
+#define GS_W2_ISSUE(BUF, K0)                                                                 \
+  {                                                                                          \
+    if constexpr (CONV) {                                                                    \
+      const int64_t toff = ((int64_t)tkh * p.cW + tkw) * p.cCin + tic;                       \
+      _Pragma("unroll") for (int i = 0; i < BM / 64; ++i) {                                  \
+        const bool ok = (unsigned)(ohs[i] + tkh) < (unsigned)p.cH &&                          \
+                        (unsigned)(ows[i] + tkw) < (unsigned)p.cW;                            \
+        lds_dma16(ok ? (const float*)(ag[i] + toff) : zrow,                                  \
+                  lds0 + ((BUF) * BSTAGE + 16 * (4 * i + wave) * W2K) * 2);                  \
+      }                                                                                      \
+      tic += W2K;                                                                            \
+      if (tic == p.cCin) {                                                                   \
+        tic = 0;                                                                             \
+        if (++tkw == p.ck) {                                                                 \
+          tkw = 0;                                                                           \
+          ++tkh;                                                                             \
+        }                                                                                    \
+      }                                                                                      \
+    } else {                                                                                 \
+      _Pragma("unroll") for (int i = 0; i < BM / 64; ++i)                                    \
+        lds_dma16((const float*)(ag[i] + (K0)),                                              \
+                  lds0 + ((BUF) * BSTAGE + 16 * (4 * i + wave) * W2K) * 2);                  \
+    }                                                                                        \
+    _Pragma("unroll") for (int i = 0; i < W2N / 64; ++i)                                     \
+      lds_dma16((const float*)(bg[i] + (K0)),                                                \
+                lds0 + ((BUF) * BSTAGE + (BM + 16 * (4 * i + wave)) * W2K) * 2);             \
+  }
+  const int swz = (l32 >> 2) & 3;
+  const int ra0 = (wm * 32 * WTM + l32) * W2K, rb0 = (wn * 64 + l32) * W2K;
+  floatx16 c00 = {}, c01 = {}, c10 = {}, c11 = {}, c20 = {}, c21 = {}, c30 = {}, c31 = {};
+  int buf = 0;
+  GS_W2_ISSUE(0, 0)
+  for (int k0 = 0; k0 < K; k0 += W2K) {
+    // step k0 in stage buf, step k0 + W2K streaming into the other stage:
+    // each wave waits for its own BM / 64 + 2 loads of step k0, the barrier
+    // makes all of them visible; the fragment reads drain before the barrier
+    // that lets the stage be refilled
+    if (k0 + W2K < K) {
+      GS_W2_ISSUE(buf ^ 1, k0 + W2K)
+      if constexpr (BM == 256)
+        asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    const __bf16* as = lds + buf * BSTAGE;
+    const __bf16* bs = as + BM * W2K;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const int co = ((2 * s + hl) ^ swz) << 3;
+      const bf16x8 a0 = *(const bf16x8*)(as + ra0 + co);
+      const bf16x8 a1 = *(const bf16x8*)(as + ra0 + 32 * W2K + co);
+      const bf16x8 a2 = *(const bf16x8*)(as + ra0 + 64 * W2K + co);
+      bf16x8 a3 = {};
+      if constexpr (WTM == 4) a3 = *(const bf16x8*)(as + ra0 + 96 * W2K + co);
+      const bf16x8 b0 = *(const bf16x8*)(bs + rb0 + co);
+      const bf16x8 b1 = *(const bf16x8*)(bs + rb0 + 32 * W2K + co);
+      c00 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, c00, 0, 0, 0);
+      c01 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, c01, 0, 0, 0);
+      c10 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, c10, 0, 0, 0);
+      c11 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1, c11, 0, 0, 0);
+      c20 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b0, c20, 0, 0, 0);
+      c21 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b1, c21, 0, 0, 0);
+      if constexpr (WTM == 4) {
+        c30 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b0, c30, 0, 0, 0);
+        c31 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b1, c31, 0, 0, 0);
+      }
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    buf ^= 1;
+  }
+#undef GS_W2_ISSUE
+  // WTM 32-row block rows per wave through the staged epilogue (the wave's
+  // 32 x 68-float stage; the LDS stages are free after the last barrier)
+  const int mw = m0 + wm * 32 * WTM, nw = n0 + wn * 64;
+  float* stage = (float*)lds + wave * 32 * W2_SS;
+  if (p.flags & EPI_ROPE) {
+    w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
+    w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
+    w2_epi_row<true>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
+    if constexpr (WTM == 4) w2_epi_row<true>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
+  } else {
+    w2_epi_row<false>(p, c00, c01, mw, nw, stage, lane, l32, hl);
+    w2_epi_row<false>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
+    w2_epi_row<false>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
+    if constexpr (WTM == 4) w2_epi_row<false>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
+  }
+}
+
+// fp32 kernel of the same structure for large launches with plain rows or an
+// implicit conv (CONV: each K step's A rows gathered from the NHWC input, see
+// below):
+// workgroup tile BM x 128 (BM = 256 or 192) of 2 x 2 waves at (BM / 2) x 64
+// (BM / 64 x 2 blocks of v_mfma_f32_32x32x2_f32), 16-deep K steps (64-byte
+// rows: the bf16 kernel's LDS geometry, loader and slot swizzle) streamed into
+// two LDS stages (48 / 40 KB), three workgroups per CU, epilogue through
+// w2_epi_row. Lane l (half h) feeds MFMA step t of a K step with k = 8h + t.
+// BM = 192 serves launches whose 256-row tiles would leave part of the last
+// round of workgroup slots empty (the decoder's N = 768 linears: 576 tiles of
+// 256 rows on 768 slots, exactly 768 of 192 rows).
+
 
 template <int BM, bool CONV>
 __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
@@ -1802,23 +1835,37 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   // kernel: encoder fc1 873 against 648 TFLOP/s, qkv 742 against 562, fc2 846
   // against 764; a 256 x 256 kernel at one workgroup per CU, which it replaced,
   // ran fc2 at 812 and lost at K <= 1024 (its epilogue is exposed)
-  if (bf16 && aload == A_PLAIN_H && !a_relu && b.ksplit == 1) {
+  // Implicit convs on a bf16 input (A_CONV_H) take its 192-row form with the
+  // per-tap gather (the gather state of 256-row tiles does not fit the
+  // three-workgroup register budget).
+  if (bf16 && (aload == A_PLAIN_H || aload == A_CONV_H) && !a_relu && b.ksplit == 1) {
+    const bool conv = aload == A_CONV_H;
+    const int bm = conv ? 192 : 256;
     int wt = 0, wtot = 0;
     bool ok = true;
     for (int i = 0; i < b.ngroups; ++i) {
       const GemmArgs& g = b.g[i];
-      const int t = ((g.M + W2M - 1) / W2M) * ((g.N + W2N - 1) / W2N);
+      const int t = ((g.M + bm - 1) / bm) * ((g.N + W2N - 1) / W2N);
       wt = std::max(wt, t);
       wtot += t;
-      ok = ok && g.K % W2K == 0 && g.lda % 8 == 0 && aligned16(g.A) && g.ldb % 8 == 0 &&
-           aligned16(g.Bh) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+      ok = ok && g.K % W2K == 0 && (conv ? g.cCin % W2K == 0 : g.lda % 8 == 0) &&
+           aligned16(g.A) && g.ldb % 8 == 0 && aligned16(g.Bh) && row_epi_ok(g) &&
+           (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
     }
     if (ok && wtot >= 512) {
       hipEvent_t ev = prof_start(s);
-      hipLaunchKernelGGL(gemm_bf16_w2_kernel, dim3(wt, 1, b.ngroups), dim3(256), 0, s, b);
+      if (conv)
+        hipLaunchKernelGGL((gemm_bf16_w2_kernel<192, true>), dim3(wt, 1, b.ngroups), dim3(256), 0,
+                           s, b);
+      else
+        hipLaunchKernelGGL((gemm_bf16_w2_kernel<256, false>), dim3(wt, 1, b.ngroups), dim3(256), 0,
+                           s, b);
       GS_CHECK_HIP(hipGetLastError());
-      if (ev) prof_stop(s, ev, gemm_prof_name("gemm_bf16_w2_kernel<A_PLAIN_H>", b).c_str(), flops,
-                        bytes);
+      if (ev)
+        prof_stop(s, ev,
+                  gemm_prof_name(conv ? "gemm_bf16_w2_kernel<192,A_CONV_H>"
+                                      : "gemm_bf16_w2_kernel<A_PLAIN_H>", b).c_str(),
+                  flops, bytes);
       return post_layernorm(b, s);
     }
   }
