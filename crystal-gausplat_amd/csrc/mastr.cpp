@@ -743,27 +743,34 @@ int convt(Ctx& c, const Heads& hs, const std::string& suffix, const float* const
 // bilinear weights of each output pixel sum to one, so the bias passes
 // through), so out_conv runs at the input resolution: a quarter of its FLOPs
 // and of the upsample's input traffic. Differences are fp32 rounding only.
+// bf16 mode: each RCU's conv1 output feeds only its conv2, so it is written in
+// bf16 (the rounding conv2's A load would apply) and conv2 reads it so; with
+// out_bf16 the final upsample does the same for a single bf16 consumer.
 int fusion(Ctx& c, const Heads& hs, const std::string& suffix, const float* const x0[2],
-           const float* const x1[2], int B, int H, int W_, float* const out[2], hipStream_t s) {
+           const float* const x1[2], int B, int H, int W_, float* const out[2], hipStream_t s,
+           bool out_bf16 = false) {
   const int F = c.cfg.dpt_feat;
+  const bool hb = c.cfg.precision == 1;
+  const int ub = hb ? EPI_BF16OUT : 0;
   const float* sum[2] = {x0[0], x0[1]};
   if (x1) {
-    RC(conv(c, hs, suffix + ".resConfUnit1.conv1", x1, B, H, W_, F, F, 3, 1, 1, true, c.u, EPI_RELU,
-            true, s));
+    RC(conv(c, hs, suffix + ".resConfUnit1.conv1", x1, B, H, W_, F, F, 3, 1, 1, true, c.u,
+            EPI_RELU | ub, true, s));
     const float* uin[2] = {c.u[0], c.u[1]};
     RC(conv(c, hs, suffix + ".resConfUnit1.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.s, 0,
-            false, s, x1, x0));
+            false, s, x1, x0, hb));
     sum[0] = c.s[0];
     sum[1] = c.s[1];
   }
-  RC(conv(c, hs, suffix + ".resConfUnit2.conv1", sum, B, H, W_, F, F, 3, 1, 1, true, c.u, EPI_RELU,
-          true, s));
+  RC(conv(c, hs, suffix + ".resConfUnit2.conv1", sum, B, H, W_, F, F, 3, 1, 1, true, c.u,
+          EPI_RELU | ub, true, s));
   const float* uin[2] = {c.u[0], c.u[1]};
   RC(conv(c, hs, suffix + ".resConfUnit2.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.t, 0, false,
-          s, sum));
+          s, sum, nullptr, hb));
   const float* tin[2] = {c.t[0], c.t[1]};
   RC(conv(c, hs, suffix + ".out_conv", tin, B, H, W_, F, F, 1, 1, 0, true, c.up, 0, false, s));
-  for (int v = 0; v < hs.n; ++v) RC(launch_upsample2x(c.up[v], B, H, W_, F, out[v], s));
+  for (int v = 0; v < hs.n; ++v)
+    RC(launch_upsample2x(c.up[v], B, H, W_, F, out[v], s, out_bf16 && hb));
   return 0;
 }
 
@@ -804,9 +811,11 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
   RC(fusion(c, hs, rp + "4", Lc[3], nullptr, B, ah[3], aw[3], c.rA, s));
   RC(fusion(c, hs, rp + "3", rAc, Lc[2], B, ah[2], aw[2], c.rB, s));
   RC(fusion(c, hs, rp + "2", rBc, Lc[1], B, ah[1], aw[1], c.rA, s));
-  RC(fusion(c, hs, rp + "1", rAc, Lc[0], B, ah[0], aw[0], c.rB, s));
+  // refinenet1's output feeds only head.0: bf16 in the bf16 mode
+  RC(fusion(c, hs, rp + "1", rAc, Lc[0], B, ah[0], aw[0], c.rB, s, true));
   const int h1 = 2 * ah[0], w1 = 2 * aw[0];
-  RC(conv(c, hs, ".dpt.head.0", rBc, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s));
+  RC(conv(c, hs, ".dpt.head.0", rBc, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s,
+          nullptr, nullptr, f.precision == 1));
   // bf16 mode: the full-resolution upsample feeds only the next conv, so it is
   // written in bf16 (the rounding that conv's A load would apply) and read so
   const bool hb = f.precision == 1;
