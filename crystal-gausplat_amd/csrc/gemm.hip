@@ -1045,6 +1045,16 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
   const int rin = lane >> 4, c4 = (lane & 15) * 4;
   const int col = col0 + c4;
   const int colc = min(col, N - 4);
+  // sub-pixel scatter (EPI_SCATTER): column col = (i * sc_r + j) * sc_C + c;
+  // with sc_C and sc_Cout multiples of 4 the lane's 4 columns are one pixel's
+  // channels c .. c + 3, all kept or all dropped, 16 contiguous output bytes
+  int sc_i = 0, sc_j = 0, sc_c = 0;
+  if (flags & EPI_SCATTER) {
+    const int sidx = col / p.sc_C;
+    sc_c = col - sidx * p.sc_C;
+    sc_i = sidx / p.sc_r;
+    sc_j = sidx - sc_i * p.sc_r;
+  }
   // two halves of 16 rows, the residuals of a half read before its stores
 #pragma unroll
   for (int hq = 0; hq < 2; ++hq) {
@@ -1071,7 +1081,17 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
     if (flags & EPI_RES1) v = v + x1[u];
     if (flags & EPI_RES2) v = x2[u] + v;
     if (row < M && col < N) {
-      if (flags & EPI_BF16OUT) {
+      if (flags & EPI_SCATTER) {
+        if (sc_c < p.sc_Cout) {
+          const int hw = p.sc_gh * p.sc_gw;
+          const int img = row / hw;
+          const int rem = row - img * hw;
+          const int yy = rem / p.sc_gw, xx = rem - yy * p.sc_gw;
+          const int64_t oy = (int64_t)img * p.sc_gh * p.sc_r + yy * p.sc_r + sc_i;
+          const int64_t ox = (int64_t)xx * p.sc_r + sc_j;
+          *(fx4*)(p.C + (oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c) = v;
+        }
+      } else if (flags & EPI_BF16OUT) {
         typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
         bf16x4_t h;
         h.x = (__bf16)v.x;
@@ -1574,7 +1594,9 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 // The staged epilogue of the one-wave-per-SIMD kernels stores 4 columns per
 // lane with vector accesses.
 bool row_epi_ok(const GemmArgs& g) {
-  if (g.flags & EPI_SCATTER) return false;
+  if (g.flags & EPI_SCATTER)  // 4-column segments stay within one output pixel
+    return g.sc_C % 4 == 0 && g.sc_Cout % 4 == 0 && g.N % 4 == 0 && aligned16(g.C) &&
+           !(g.flags & (EPI_RES1 | EPI_RES2 | EPI_ROPE | EPI_DUAL | EPI_BF16OUT));
   if (g.N % 4 || g.ldc % 4 || !aligned16(g.C)) return false;
   if ((g.flags & EPI_RES1) && (g.ldr1 % 4 || !aligned16(g.R1))) return false;
   if ((g.flags & EPI_RES2) && (g.ldr2 % 4 || !aligned16(g.R2))) return false;

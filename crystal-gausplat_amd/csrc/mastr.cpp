@@ -880,8 +880,11 @@ int local_features(Ctx& c, const Heads& hs, const float* const e[2], const float
   b1.ngroups = b2.ngroups = hs.n;
   for (int v = 0; v < hs.n; ++v) {
     const std::string p = hs.pre(v) + ".head_local_features";
+    // bf16 mode: the hidden activations feed only fc2, so fc1 writes them in
+    // bf16 and fc2 reads them so (the 256 x 128 bf16 kernel, scatter epilogue)
     GemmArgs a = lin(e[v], f.enc_dim, W(c, p + ".fc1.weight"), W(c, p + ".fc1.bias"), c.lf[v],
-                     f.lf_hidden, Mv, f.lf_hidden, Din, EPI_GELU);
+                     f.lf_hidden, Mv, f.lf_hidden, Din,
+                     EPI_GELU | (f.precision == 1 ? EPI_BF16OUT : 0));
     a.A2 = dfin[v];
     a.lda2 = f.dec_dim;
     a.K1 = f.enc_dim;
@@ -897,7 +900,7 @@ int local_features(Ctx& c, const Heads& hs, const float* const e[2], const float
     b2.g[v] = g;
   }
   RC(gemm(c, b1, A_CONCAT, false, s));
-  return gemm(c, b2, A_PLAIN, false, s);
+  return gemm(c, b2, f.precision == 1 ? A_PLAIN_H : A_PLAIN, false, s);
 }
 
 // ---------------------------------------------------------------------------
