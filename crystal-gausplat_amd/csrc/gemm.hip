@@ -1131,20 +1131,33 @@ __device__ __forceinline__ bool f2_tile(const GemmArgs& p, int& m0, int& n0) {
 // 64 zero bytes: the source of a padded conv tap's 16-byte loads
 __device__ __attribute__((aligned(64))) float g_zero16[16] = {};
 
+// plain-row launches with at least this K per group take the three-stage
+// form (measured at config 4: descriptor fc2, K = 7168, 695 -> 832 TFLOP/s;
+// encoder fc2, K = 4096, 872 / 865; K <= 1024 linears and the implicit convs
+// 7-13 % slower, their epilogues exposed at two workgroups per CU)
+constexpr int kW2ThreeStageMinK = 6144;
+
 // BM = 256 or 192 rows; CONV: the A rows gathered from a bf16 NHWC input
 // (implicit conv, A_CONV_H; a 32-deep K step is 32 channels of one tap, so a
 // lane's 16 bytes are contiguous; padded taps load from g_zero16).
-template <int BM, bool CONV>
-__global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
+// NST = 2: two LDS stages, three workgroups per CU, loads issued one K step
+// ahead, two barriers per step. NST = 3: three stages, two workgroups per CU,
+// loads issued two steps ahead and one barrier per step (the barrier that
+// makes step k visible also retires every wave's reads of step k - 1, whose
+// stage the loads of step k + 2 then refill).
+template <int BM, bool CONV, int NST>
+__global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
   constexpr int WTM = BM / 64;                 // 32-row blocks per wave
   constexpr int BSTAGE = (BM + W2N) * W2K;     // bf16 per LDS stage
+  constexpr int LPS = BM / 64 + W2N / 64;      // loads per wave per K step
   static_assert(BM == 256 || BM == 192, "tile rows");
-  static_assert(4 * 32 * W2_SS * 4 <= 2 * BSTAGE * 2, "w2 epilogue stages fit the LDS stages");
+  static_assert(NST == 2 || NST == 3, "LDS stages");
+  static_assert(4 * 32 * W2_SS * 4 <= NST * BSTAGE * 2, "w2 epilogue stages fit the LDS stages");
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
   int m0, n0;
   if (!f2_tile<BM>(p, m0, n0)) return;
-  __shared__ __attribute__((aligned(16))) __bf16 lds[2 * BSTAGE];
+  __shared__ __attribute__((aligned(16))) __bf16 lds[NST * BSTAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1215,19 +1228,38 @@ __global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
   floatx16 c00 = {}, c01 = {}, c10 = {}, c11 = {}, c20 = {}, c21 = {}, c30 = {}, c31 = {};
   int buf = 0;
   GS_W2_ISSUE(0, 0)
+  if (NST == 3 && W2K < K) GS_W2_ISSUE(1, W2K)
   for (int k0 = 0; k0 < K; k0 += W2K) {
-    // step k0 in stage buf, step k0 + W2K streaming into the other stage:
-    // each wave waits for its own BM / 64 + 2 loads of step k0, the barrier
-    // makes all of them visible; the fragment reads drain before the barrier
-    // that lets the stage be refilled
-    if (k0 + W2K < K) {
-      GS_W2_ISSUE(buf ^ 1, k0 + W2K)
-      if constexpr (BM == 256)
-        asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory");
+    if constexpr (NST == 2) {
+      // step k0 in stage buf, step k0 + W2K streaming into the other stage:
+      // each wave waits for its own LPS loads of step k0, the barrier makes
+      // all of them visible; the fragment reads drain before the barrier
+      // that lets the stage be refilled
+      if (k0 + W2K < K) {
+        GS_W2_ISSUE(buf ^ 1, k0 + W2K)
+        if constexpr (BM == 256)
+          asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      }
     } else {
-      asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      // steps k0 and k0 + W2K in flight: wait for this wave's loads of step
+      // k0 (the LPS loads of step k0 + W2K may stay outstanding) and for its
+      // reads of step k0 - W2K; after the barrier every wave's loads of step
+      // k0 are visible and no wave reads the stage of step k0 - W2K, which
+      // the loads of step k0 + 2 W2K refill
+      static_assert(LPS == 6 || LPS == 5, "vmcnt immediates below");
+      if (k0 + W2K < K) {
+        if constexpr (LPS == 6)
+          asm volatile("s_waitcnt vmcnt(6) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        else
+          asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+      if (k0 + 2 * W2K < K) GS_W2_ISSUE(buf == 0 ? 2 : buf - 1, k0 + 2 * W2K)
     }
     const __bf16* as = lds + buf * BSTAGE;
     const __bf16* bs = as + BM * W2K;
@@ -1252,9 +1284,15 @@ __global__ __launch_bounds__(256, 3) void gemm_bf16_w2_kernel(GemmBatch batch) {
         c31 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a3, b1, c31, 0, 0, 0);
       }
     }
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    buf ^= 1;
+    if constexpr (NST == 2) {
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      buf ^= 1;
+    } else {
+      buf = buf == 2 ? 0 : buf + 1;
+    }
   }
+  // the epilogue stages overlay the LDS stages: every wave's last reads first
+  if constexpr (NST == 3) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #undef GS_W2_ISSUE
   // WTM 32-row block rows per wave through the staged epilogue (the wave's
   // 32 x 68-float stage; the LDS stages are free after the last barrier)
@@ -1863,10 +1901,11 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   if (bf16 && (aload == A_PLAIN_H || aload == A_CONV_H) && !a_relu && b.ksplit == 1) {
     const bool conv = aload == A_CONV_H;
     const int bm = conv ? 192 : 256;
-    int wt = 0, wtot = 0;
+    int wt = 0, wtot = 0, kmin = b.g[0].K;
     bool ok = true;
     for (int i = 0; i < b.ngroups; ++i) {
       const GemmArgs& g = b.g[i];
+      kmin = std::min(kmin, g.K);
       const int t = ((g.M + bm - 1) / bm) * ((g.N + W2N - 1) / W2N);
       wt = std::max(wt, t);
       wtot += t;
@@ -1877,16 +1916,21 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     if (ok && wtot >= 512) {
       hipEvent_t ev = prof_start(s);
       if (conv)
-        hipLaunchKernelGGL((gemm_bf16_w2_kernel<192, true>), dim3(wt, 1, b.ngroups), dim3(256), 0,
-                           s, b);
+        hipLaunchKernelGGL((gemm_bf16_w2_kernel<192, true, 2>), dim3(wt, 1, b.ngroups), dim3(256),
+                           0, s, b);
+      else if (kmin >= kW2ThreeStageMinK)
+        hipLaunchKernelGGL((gemm_bf16_w2_kernel<256, false, 3>), dim3(wt, 1, b.ngroups), dim3(256),
+                           0, s, b);
       else
-        hipLaunchKernelGGL((gemm_bf16_w2_kernel<256, false>), dim3(wt, 1, b.ngroups), dim3(256), 0,
-                           s, b);
+        hipLaunchKernelGGL((gemm_bf16_w2_kernel<256, false, 2>), dim3(wt, 1, b.ngroups), dim3(256),
+                           0, s, b);
       GS_CHECK_HIP(hipGetLastError());
       if (ev)
         prof_stop(s, ev,
                   gemm_prof_name(conv ? "gemm_bf16_w2_kernel<192,A_CONV_H>"
-                                      : "gemm_bf16_w2_kernel<A_PLAIN_H>", b).c_str(),
+                                 : kmin >= kW2ThreeStageMinK ? "gemm_bf16_w2_kernel<A_PLAIN_H,3-stage>"
+                                                             : "gemm_bf16_w2_kernel<A_PLAIN_H>",
+                                 b).c_str(),
                   flops, bytes);
       return post_layernorm(b, s);
     }

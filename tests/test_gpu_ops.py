@@ -91,10 +91,11 @@ def test_linear_bf16_variant(M, K, N):
 
 @pytest.mark.parametrize("M,K,N,epi", [(8200, 1024, 3000, "gelu"), (8200, 1024, 3000, "residual"),
                                        (8192, 768, 2304, "nobias"), (16384, 2048, 1024, "residual"),
-                                       (16400, 3072, 1000, "gelu")])
+                                       (16400, 3072, 1000, "gelu"), (8200, 7168, 2000, "residual")])
 def test_linear_bf16_large_launches(M, K, N, epi):
-    """The bf16 variant on launches large enough for the 256 x 128 and 256 x 256
-    kernels (ragged M and N, the three epilogues), against an fp64 product of
+    """The bf16 variant on launches large enough for the 256 x 128 kernel in
+    its two- and three-stage forms (K >= 6144 takes the latter; ragged M and
+    N, the three epilogues), against an fp64 product of
     the bf16-rounded operands: the kernels round x and W to bf16 and
     accumulate in fp32, so the error bound is the fp32 accumulation's."""
     case(f"linear bf16 large M={M} K={K} N={N} {epi}")
