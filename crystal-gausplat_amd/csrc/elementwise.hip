@@ -100,49 +100,117 @@ __global__ void unfold_kernel(const float* __restrict__ img, int32_t B, int32_t 
 // No FMA contraction: a fused sh*oy - y0 moves the lerp weight by an ulp of
 // the source coordinate; this kernel is HBM-bound, so it keeps the plain
 // operation sequence of the CPU formula.
+// One workgroup covers `px` consecutive pixels of one output row, so the
+// row's source rows and vertical weights are uniform. Where C / 4 <= 256,
+// thread t keeps channel group t % (C / 4) and walks a run of kUpsRun
+// consecutive output pixels: neighbouring outputs share source columns (the
+// scale is about one half), so the previous pixel's two source columns stay
+// in registers and a run of 8 loads about 5 columns instead of 16 (four
+// 16-byte loads per 16-byte output held the kernel near half of the HBM
+// bandwidth on L1 traffic). Wider rows step over flat element indices.
+constexpr int kUpsRun = 8;
 template <bool OUT_BF16>
 __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict__ x,
                                                          int32_t H, int32_t W, int32_t C,
-                                                         int32_t blocks_per_row,
+                                                         int32_t blocks_per_row, int32_t px,
                                                          float* __restrict__ y) {
 #pragma clang fp contract(off)
-  // One workgroup covers 256 consecutive float4s of one output row, so the
-  // row's source rows and weights are uniform and only the column is divided
-  // out per thread.
   const int Ho = 2 * H, Wo = 2 * W, C4 = C >> 2;
   const int row = (int)(blockIdx.x / (uint32_t)blocks_per_row);  // b * Ho + oy
-  const int e = (int)(blockIdx.x - (uint32_t)row * blocks_per_row) * 256 + threadIdx.x;
-  if (e >= Wo * C4) return;
-  const int ox = e / C4;
-  const int c = (e - ox * C4) * 4;
+  const int ox0 = (int)(blockIdx.x - (uint32_t)row * blocks_per_row) * px;
+  const int ox1 = min(ox0 + px, Wo);
   const int b = row / Ho;
   const int oy = row - b * Ho;
   const float sh = (float)(H - 1) / (float)(Ho - 1);
   const float sw = (float)(W - 1) / (float)(Wo - 1);
-  const float fy = sh * (float)oy, fx = sw * (float)ox;
-  const int y0 = (int)fy, x0 = (int)fx;
-  const int y1 = y0 + (y0 < H - 1 ? 1 : 0), x1 = x0 + (x0 < W - 1 ? 1 : 0);
+  const float fy = sh * (float)oy;
+  const int y0 = (int)fy;
+  const int y1 = y0 + (y0 < H - 1 ? 1 : 0);
   const float ly = fy - (float)y0, hy = 1.0f - ly;
-  const float lx = fx - (float)x0, hx = 1.0f - lx;
-  const float* base = x + (int64_t)b * H * W * C + c;
-  const fx4 a = *(const fx4*)(base + ((int64_t)y0 * W + x0) * C);
-  const fx4 bq = *(const fx4*)(base + ((int64_t)y0 * W + x1) * C);
-  const fx4 cq = *(const fx4*)(base + ((int64_t)y1 * W + x0) * C);
-  const fx4 d = *(const fx4*)(base + ((int64_t)y1 * W + x1) * C);
-  fx4 o;
-  o.x = hy * (hx * a.x + lx * bq.x) + ly * (hx * cq.x + lx * d.x);
-  o.y = hy * (hx * a.y + lx * bq.y) + ly * (hx * cq.y + lx * d.y);
-  o.z = hy * (hx * a.z + lx * bq.z) + ly * (hx * cq.z + lx * d.z);
-  o.w = hy * (hx * a.w + lx * bq.w) + ly * (hx * cq.w + lx * d.w);
-  // the output (4x the input) is streamed out with non-temporal stores so it
-  // does not displace the source rows that neighbouring output rows re-read
-  const int64_t oi = ((int64_t)row * Wo * C4 + e) * 4;
-  if constexpr (OUT_BF16) {  // round to nearest even, the conversion the bf16 GEMMs apply
-    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-    const bf16x4_t h = {(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
-    __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, h), (uint64_t*)((__bf16*)y + oi));
+  const float* r0 = x + ((int64_t)b * H + y0) * W * C;
+  const float* r1 = x + ((int64_t)b * H + y1) * W * C;
+  float* yrow = y + (int64_t)row * Wo * C;
+  // the bilinear blend of the four source values
+  auto blend = [&](const fx4& a, const fx4& bq, const fx4& cq, const fx4& d, float lx, float hx) {
+    fx4 o;
+    o.x = hy * (hx * a.x + lx * bq.x) + ly * (hx * cq.x + lx * d.x);
+    o.y = hy * (hx * a.y + lx * bq.y) + ly * (hx * cq.y + lx * d.y);
+    o.z = hy * (hx * a.z + lx * bq.z) + ly * (hx * cq.z + lx * d.z);
+    o.w = hy * (hx * a.w + lx * bq.w) + ly * (hx * cq.w + lx * d.w);
+    return o;
+  };
+  // output pixel ox, channels 4 cg .. 4 cg + 3; the output (4x the input) is
+  // streamed out with non-temporal stores so it does not displace the source
+  // rows that neighbouring output rows re-read
+  auto store = [&](int ox, int cg, const fx4& o) {
+    const int64_t oi = (int64_t)ox * C + 4 * cg;
+    if constexpr (OUT_BF16) {  // round to nearest even, the conversion the bf16 GEMMs apply
+      typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+      const bf16x4_t h = {(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
+      __builtin_nontemporal_store(__builtin_bit_cast(uint64_t, h),
+                                  (uint64_t*)((__bf16*)y + (int64_t)row * Wo * C + oi));
+    } else {
+      __builtin_nontemporal_store(o, (fx4*)(yrow + oi));
+    }
+  };
+  auto one = [&](int ox, int cg) {
+    const float fx = sw * (float)ox;
+    const int x0 = (int)fx;
+    const int x1 = x0 + (x0 < W - 1 ? 1 : 0);
+    const float lx = fx - (float)x0, hx = 1.0f - lx;
+    const int64_t c0 = (int64_t)x0 * C + 4 * cg, c1 = (int64_t)x1 * C + 4 * cg;
+    store(ox, cg, blend(*(const fx4*)(r0 + c0), *(const fx4*)(r0 + c1), *(const fx4*)(r1 + c0),
+                        *(const fx4*)(r1 + c1), lx, hx));
+  };
+  if (C4 <= 256) {
+    const int ppi = 256 / C4;  // pixel runs per workgroup
+    const int pp = (int)threadIdx.x / C4, cg = (int)threadIdx.x - pp * C4;
+    if (pp >= ppi) return;
+    const int xs = ox0 + pp * kUpsRun, xe = min(xs + kUpsRun, ox1);
+    // the previous pixel's source columns p0 (values pa, pc in rows y0, y1)
+    // and p1 (pb, pd); x0 repeats on every other pixel at this scale
+    int p0 = -1, p1 = -1;
+    fx4 pa = {}, pb = {}, pc = {}, pd = {};
+    for (int ox = xs; ox < xe; ++ox) {
+      const float fx = sw * (float)ox;
+      const int x0 = (int)fx;
+      const int x1 = x0 + (x0 < W - 1 ? 1 : 0);
+      const float lx = fx - (float)x0, hx = 1.0f - lx;
+      fx4 a, bq, cq, d;
+      if (x0 == p0) {
+        a = pa;
+        cq = pc;
+      } else if (x0 == p1) {
+        a = pb;
+        cq = pd;
+      } else {
+        a = *(const fx4*)(r0 + (int64_t)x0 * C + 4 * cg);
+        cq = *(const fx4*)(r1 + (int64_t)x0 * C + 4 * cg);
+      }
+      if (x1 == x0) {
+        bq = a;
+        d = cq;
+      } else if (x1 == p1) {
+        bq = pb;
+        d = pd;
+      } else {
+        bq = *(const fx4*)(r0 + (int64_t)x1 * C + 4 * cg);
+        d = *(const fx4*)(r1 + (int64_t)x1 * C + 4 * cg);
+      }
+      p0 = x0;
+      p1 = x1;
+      pa = a;
+      pc = cq;
+      pb = bq;
+      pd = d;
+      store(ox, cg, blend(a, bq, cq, d, lx, hx));
+    }
   } else {
-    __builtin_nontemporal_store(o, (fx4*)(y + oi));
+    const int n = (ox1 - ox0) * C4;
+    for (int e = (int)threadIdx.x; e < n; e += 256) {
+      const int q = e / C4;
+      one(ox0 + q, e - q * C4);
+    }
   }
 }
 
@@ -309,17 +377,20 @@ int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   GS_REQUIRE(aligned16(x) && aligned16(y), "upsample2x: operands must be 16-byte aligned");
   GS_REQUIRE((int64_t)2 * W * (C / 4) <= INT32_MAX && (int64_t)2 * B * H <= INT32_MAX,
              "upsample2x: too many elements");
-  const int32_t blocks_per_row = (int32_t)nblocks((int64_t)2 * W * (C / 4), 256);
+  // pixels per workgroup: 256 / (C / 4) runs of kUpsRun pixels, or eight
+  // pixels of wider rows
+  const int32_t px = C / 4 <= 256 ? kUpsRun * (256 / (C / 4)) : 8;
+  const int32_t blocks_per_row = (int32_t)nblocks((int64_t)2 * W, px);
   const int64_t nblk = (int64_t)2 * B * H * blocks_per_row;
   GS_REQUIRE(nblk < INT32_MAX, "upsample2x: too many elements");
   if (nblk == 0) return 0;
   hipEvent_t ev = prof_start(s);
   if (out_bf16)
     hipLaunchKernelGGL(upsample2x_kernel<true>, dim3((uint32_t)nblk), dim3(256), 0, s, x, H, W, C,
-                       blocks_per_row, y);
+                       blocks_per_row, px, y);
   else
     hipLaunchKernelGGL(upsample2x_kernel<false>, dim3((uint32_t)nblk), dim3(256), 0, s, x, H, W, C,
-                       blocks_per_row, y);
+                       blocks_per_row, px, y);
   GS_CHECK_HIP(hipGetLastError());
   prof_stop(s, ev, "upsample2x_kernel", 0.0, (double)B * H * W * C * (4.0 + (out_bf16 ? 8.0 : 16.0)));
   return 0;

@@ -566,8 +566,12 @@ def test_op_scratch_is_per_stream():
         np.testing.assert_array_equal(host(oc)[:n], rc)
 
 
-@pytest.mark.parametrize("B,H,W,C", [(1, 96, 128, 256), (2, 5, 7, 8)])
+@pytest.mark.parametrize("B,H,W,C", [(1, 96, 128, 256), (2, 5, 7, 8), (2, 48, 64, 128),
+                                     (1, 3, 37, 12), (1, 1, 1, 4), (1, 3, 5, 2048)])
 def test_upsample_parity(B, H, W, C):
+    """Channel widths of one and of several workgroup steps, a width that
+    leaves threads idle (C / 4 = 3), a 1 x 1 input and rows wider than a
+    workgroup (C / 4 > 256)."""
     case(f"upsample2x {B}x{H}x{W}x{C}")
     x = rnd(B, H, W, C)
     y = empty(B, 2 * H, 2 * W, C)
