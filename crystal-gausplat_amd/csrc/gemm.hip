@@ -203,7 +203,12 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmArgs& p, const floatx1
               ((__bf16*)p.C)[(int64_t)row * p.ldc + col] = (__bf16)v;
             } else {
               p.C[(int64_t)row * p.ldc + col] = v;
-              if (flags & EPI_DUAL) p.C2[(int64_t)row * p.ldc + col] = v;
+              if (flags & EPI_DUAL) {
+                if (flags & EPI_DUAL_RELU_H)
+                  ((__bf16*)p.C2)[(int64_t)row * p.ldc + col] = (__bf16)fmaxf(v, 0.f);
+                else
+                  p.C2[(int64_t)row * p.ldc + col] = v;
+              }
             }
           }
         }
@@ -220,6 +225,19 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& p, const floatx16&
     gemm_epilogue_t<true>(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
   else
     gemm_epilogue_t<false>(p, acc00, acc01, acc10, acc11, m0, n0, wm, wn, l32, hl);
+}
+
+// EPI_DUAL's second store of four consecutive columns at element offset off:
+// the value, or with EPI_DUAL_RELU_H bf16(max(v, 0)) (C2 then holds bf16).
+__device__ __forceinline__ void dual_store(const GemmArgs& p, int flags, int64_t off, fx4 v) {
+  if (flags & EPI_DUAL_RELU_H) {
+    typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+    const fx4 r = relu4(v);
+    const bf16x4_t h = {(__bf16)r.x, (__bf16)r.y, (__bf16)r.z, (__bf16)r.w};
+    *(bf16x4_t*)((__bf16*)p.C2 + off) = h;
+  } else {
+    *(fx4*)(p.C2 + off) = v;
+  }
 }
 
 // Split-K range of workgroup row blockIdx.y: the K steps (of `unit` elements)
@@ -306,7 +324,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce(GemmBatch batch) {
     return;
   }
   *(fx4*)(p.C + (int64_t)row * p.ldc + c0) = v;
-  if (flags & EPI_DUAL) *(fx4*)(p.C2 + (int64_t)row * p.ldc + c0) = v;
+  if (flags & EPI_DUAL) dual_store(p, flags, (int64_t)row * p.ldc + c0, v);
 }
 
 // gemm_splitk_reduce for launches with EPI_LNOUT: one wavefront per output row
@@ -1101,7 +1119,7 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
         *(bf16x4_t*)((__bf16*)p.C + (int64_t)row * p.ldc + col) = h;
       } else {
         *(fx4*)(p.C + (int64_t)row * p.ldc + col) = v;
-        if (flags & EPI_DUAL) *(fx4*)(p.C2 + (int64_t)row * p.ldc + col) = v;
+        if (flags & EPI_DUAL) dual_store(p, flags, (int64_t)row * p.ldc + col, v);
       }
     }
   }
@@ -1694,6 +1712,8 @@ int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16) {
                "gemm: bad rope epilogue");
   if (a.flags & EPI_DUAL)
     GS_REQUIRE(a.C2 != nullptr && !(a.flags & EPI_SCATTER), "gemm: bad dual store");
+  if (a.flags & EPI_DUAL_RELU_H)
+    GS_REQUIRE(a.flags & EPI_DUAL, "gemm: the ReLU'd bf16 copy is a form of the dual store");
   if (a.flags & EPI_ROPE)
     GS_REQUIRE(!(a.flags & (EPI_RES1 | EPI_RES2)) && a.M < (1 << 22) && a.tok_per_img > 0 &&
                    a.grid_w > 0,

@@ -183,6 +183,7 @@ struct Ctx {
   // DPT / descriptor workspaces, one slot per head of a grouped launch
   float *t0[2], *act[2][4], *L[2][4], *u[2], *s[2], *t[2], *up[2], *rA[2], *rB[2], *hd0[2],
       *hup[2], *hd2[2], *lf[2];
+  float* Lh[2][4];  // bf16 mode: bf16(max(L, 0)), the inputs of the RCU conv1s that read L
   float *rope_cos, *rope_sin, *ref_cos, *ref_sin;
   int ref_maxpos = 0;
   int last_B = 0;
@@ -684,7 +685,7 @@ int conv(Ctx& c, const Heads& hs, const std::string& suffix, const float* const 
          int H, int W_, int Cin, int Cout, int k, int stride, int pad, bool bias,
          float* const y[2], int flags, bool relu_in, hipStream_t s,
          const float* const r1[2] = nullptr, const float* const r2[2] = nullptr,
-         bool in_bf16 = false) {
+         bool in_bf16 = false, float* const yh[2] = nullptr) {
   const int Ho = (H + 2 * pad - k) / stride + 1, Wo = (W_ + 2 * pad - k) / stride + 1;
   GemmBatch b;
   b.ngroups = hs.n;
@@ -709,6 +710,10 @@ int conv(Ctx& c, const Heads& hs, const std::string& suffix, const float* const 
       a.flags |= EPI_RES2;
       a.R2 = r2[v];
       a.ldr2 = Cout;
+    }
+    if (yh) {  // also bf16(max(y, 0)) for an RCU conv1 that reads it
+      a.flags |= EPI_DUAL | EPI_DUAL_RELU_H;
+      a.C2 = yh[v];
     }
     b.g[v] = a;
   }
@@ -745,25 +750,43 @@ int convt(Ctx& c, const Heads& hs, const std::string& suffix, const float* const
 // and of the upsample's input traffic. Differences are fp32 rounding only.
 // bf16 mode: each RCU's conv1 output feeds only its conv2, so it is written in
 // bf16 (the rounding conv2's A load would apply) and conv2 reads it so; with
-// out_bf16 the final upsample does the same for a single bf16 consumer.
+// out_bf16 the final upsample does the same for a single bf16 consumer. Each
+// RCU conv1 reads bf16(max(x, 0)) of its input, written beside x by x's
+// producer (x0h / x1h for x0 / x1; RCU1's conv2 writes that of the sum into
+// c.t, free until RCU2's conv2 overwrites it).
 int fusion(Ctx& c, const Heads& hs, const std::string& suffix, const float* const x0[2],
            const float* const x1[2], int B, int H, int W_, float* const out[2], hipStream_t s,
-           bool out_bf16 = false) {
+           bool out_bf16 = false, const float* const x0h[2] = nullptr,
+           const float* const x1h[2] = nullptr) {
   const int F = c.cfg.dpt_feat;
   const bool hb = c.cfg.precision == 1;
   const int ub = hb ? EPI_BF16OUT : 0;
   const float* sum[2] = {x0[0], x0[1]};
+  const float* sumh[2] = {x0h ? x0h[0] : nullptr, x0h ? x0h[1] : nullptr};
   if (x1) {
-    RC(conv(c, hs, suffix + ".resConfUnit1.conv1", x1, B, H, W_, F, F, 3, 1, 1, true, c.u,
-            EPI_RELU | ub, true, s));
+    GS_REQUIRE(!hb || x1h, "fusion: the bf16 mode needs the ReLU'd bf16 copy of x1");
+    if (hb)
+      RC(conv(c, hs, suffix + ".resConfUnit1.conv1", x1h, B, H, W_, F, F, 3, 1, 1, true, c.u,
+              EPI_RELU | ub, false, s, nullptr, nullptr, true));
+    else
+      RC(conv(c, hs, suffix + ".resConfUnit1.conv1", x1, B, H, W_, F, F, 3, 1, 1, true, c.u,
+              EPI_RELU, true, s));
     const float* uin[2] = {c.u[0], c.u[1]};
     RC(conv(c, hs, suffix + ".resConfUnit1.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.s, 0,
-            false, s, x1, x0, hb));
+            false, s, x1, x0, hb, hb ? c.t : nullptr));
     sum[0] = c.s[0];
     sum[1] = c.s[1];
+    sumh[0] = c.t[0];
+    sumh[1] = c.t[1];
   }
-  RC(conv(c, hs, suffix + ".resConfUnit2.conv1", sum, B, H, W_, F, F, 3, 1, 1, true, c.u,
-          EPI_RELU | ub, true, s));
+  if (hb) {
+    GS_REQUIRE(sumh[0] && sumh[1], "fusion: the bf16 mode needs the ReLU'd bf16 copy of x0");
+    RC(conv(c, hs, suffix + ".resConfUnit2.conv1", sumh, B, H, W_, F, F, 3, 1, 1, true, c.u,
+            EPI_RELU | ub, false, s, nullptr, nullptr, true));
+  } else {
+    RC(conv(c, hs, suffix + ".resConfUnit2.conv1", sum, B, H, W_, F, F, 3, 1, 1, true, c.u,
+            EPI_RELU, true, s));
+  }
   const float* uin[2] = {c.u[0], c.u[1]};
   RC(conv(c, hs, suffix + ".resConfUnit2.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.t, 0, false,
           s, sum, nullptr, hb));
@@ -799,20 +822,25 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
   for (int i = 0; i < 4; ++i) {
     for (int v = 0; v < 2; ++v) L[i][v] = c.L[v][i];
     const float* ain[2] = {act[i][0], act[i][1]};
+    float* Lh[2] = {c.Lh[0][i], c.Lh[1][i]};
     RC(conv(c, hs, ".dpt.scratch.layer" + std::to_string(i + 1) + "_rn", ain, B, ah[i], aw[i], d[i],
-            F, 3, 1, 1, false, L[i], 0, false, s));
+            F, 3, 1, 1, false, L[i], 0, false, s, nullptr, nullptr, false,
+            f.precision == 1 ? Lh : nullptr));
   }
+  const float* Lhc[4][2];
+  for (int i = 0; i < 4; ++i)
+    for (int v = 0; v < 2; ++v) Lhc[i][v] = c.Lh[v][i];
   const std::string rp = ".dpt.scratch.refinenet";
   const float* Lc[4][2];
   for (int i = 0; i < 4; ++i)
     for (int v = 0; v < 2; ++v) Lc[i][v] = L[i][v];
   const float* rAc[2] = {c.rA[0], c.rA[1]};
   const float* rBc[2] = {c.rB[0], c.rB[1]};
-  RC(fusion(c, hs, rp + "4", Lc[3], nullptr, B, ah[3], aw[3], c.rA, s));
-  RC(fusion(c, hs, rp + "3", rAc, Lc[2], B, ah[2], aw[2], c.rB, s));
-  RC(fusion(c, hs, rp + "2", rBc, Lc[1], B, ah[1], aw[1], c.rA, s));
+  RC(fusion(c, hs, rp + "4", Lc[3], nullptr, B, ah[3], aw[3], c.rA, s, false, Lhc[3]));
+  RC(fusion(c, hs, rp + "3", rAc, Lc[2], B, ah[2], aw[2], c.rB, s, false, nullptr, Lhc[2]));
+  RC(fusion(c, hs, rp + "2", rBc, Lc[1], B, ah[1], aw[1], c.rA, s, false, nullptr, Lhc[1]));
   // refinenet1's output feeds only head.0: bf16 in the bf16 mode
-  RC(fusion(c, hs, rp + "1", rAc, Lc[0], B, ah[0], aw[0], c.rB, s, true));
+  RC(fusion(c, hs, rp + "1", rAc, Lc[0], B, ah[0], aw[0], c.rB, s, true, nullptr, Lhc[0]));
   const int h1 = 2 * ah[0], w1 = 2 * aw[0];
   RC(conv(c, hs, ".dpt.head.0", rBc, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s,
           nullptr, nullptr, f.precision == 1));
@@ -1105,6 +1133,7 @@ int build_workspace(Ctx& c) {
       {&c.ref_cos, 512 * (De / f.enc_heads / 2)},
       {&c.ref_sin, 512 * (De / f.enc_heads / 2)},
   };
+  const int64_t hbuf = f.precision == 1 ? 1 : 0;  // bf16-mode-only buffers
   for (int v = 0; v < 2; ++v) {  // DPT / descriptor heads, B images each
     const std::vector<std::pair<float**, int64_t>> head = {
         {&c.t0[v], B * N * dmax},
@@ -1116,6 +1145,10 @@ int build_workspace(Ctx& c) {
         {&c.L[v][1], B * 4 * N * F},
         {&c.L[v][2], B * N * F},
         {&c.L[v][3], B * N / 4 * F},
+        {&c.Lh[v][0], hbuf * B * 8 * N * F},  // bf16: half the floats of L
+        {&c.Lh[v][1], hbuf * B * 2 * N * F},
+        {&c.Lh[v][2], hbuf * (B * N * F + 1) / 2},
+        {&c.Lh[v][3], hbuf * (B * N / 4 * F + 1) / 2},
         {&c.u[v], B * 16 * N * F},
         {&c.s[v], B * 16 * N * F},
         {&c.t[v], B * 16 * N * F},
