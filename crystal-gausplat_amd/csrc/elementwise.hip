@@ -19,18 +19,28 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnBatch bt) {
   if (row >= p.rows) return;
   const int D = p.D, nv = D >> 2;
   const fx4* xr = (const fx4*)(p.x + row * D);
-  fx4 v[NV];
-  float s = 0.f;
+  fx4 v[NV], g[NV], bb[NV];
+  // gamma and beta are loaded with the row: after the reductions (and the
+  // statistics store, which they may alias for the compiler) their latency
+  // would follow the row's instead of overlapping it
+  const bool out = p.y != nullptr;
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = lane + 64 * i;
     if (idx < nv) {
       v[i] = xr[idx];
-      s += v[i].x + v[i].y + v[i].z + v[i].w;
+      if (out) {
+        g[i] = ((const fx4*)p.gamma)[idx];
+        bb[i] = ((const fx4*)p.beta)[idx];
+      }
     } else {
       v[i] = mk4(0.f, 0.f, 0.f, 0.f);
     }
   }
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < nv) s += v[i].x + v[i].y + v[i].z + v[i].w;
   const float mean = wave_sum(s) / (float)D;
   float q = 0.f;
 #pragma unroll
@@ -47,20 +57,17 @@ __global__ __launch_bounds__(256) void layernorm_kernel(LnBatch bt) {
     p.stats[2 * row] = mean;
     p.stats[2 * row + 1] = inv;
   }
-  if (!p.y) return;
-  const fx4* g4 = (const fx4*)p.gamma;
-  const fx4* b4 = (const fx4*)p.beta;
+  if (!out) return;
   fx4* yr = (fx4*)(p.y + row * D);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = lane + 64 * i;
     if (idx < nv) {
-      const fx4 g = g4[idx], bb = b4[idx];
       fx4 o;
-      o.x = (v[i].x - mean) * inv * g.x + bb.x;
-      o.y = (v[i].y - mean) * inv * g.y + bb.y;
-      o.z = (v[i].z - mean) * inv * g.z + bb.z;
-      o.w = (v[i].w - mean) * inv * g.w + bb.w;
+      o.x = (v[i].x - mean) * inv * g[i].x + bb[i].x;
+      o.y = (v[i].y - mean) * inv * g[i].y + bb[i].y;
+      o.z = (v[i].z - mean) * inv * g[i].z + bb[i].z;
+      o.w = (v[i].w - mean) * inv * g[i].w + bb[i].w;
       if (p.y_bf16) {
         typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
         bf16x4_t h;
