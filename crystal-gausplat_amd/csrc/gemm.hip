@@ -197,7 +197,11 @@ __device__ __forceinline__ void gemm_epilogue_t(const GemmArgs& p, const floatx1
                 const int yy = rem / p.sc_gw, xx = rem - (rem / p.sc_gw) * p.sc_gw;
                 const int64_t oy = (int64_t)img * p.sc_gh * p.sc_r + yy * p.sc_r + sc_i;
                 const int64_t ox = (int64_t)xx * p.sc_r + sc_j;
-                p.C[(oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c] = v;
+                const int64_t si = (oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c;
+                if (flags & EPI_BF16OUT)
+                  ((__bf16*)p.C)[si] = (__bf16)v;
+                else
+                  p.C[si] = v;
               }
             } else if (flags & EPI_BF16OUT) {
               ((__bf16*)p.C)[(int64_t)row * p.ldc + col] = (__bf16)v;
@@ -1107,7 +1111,14 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
           const int yy = rem / p.sc_gw, xx = rem - yy * p.sc_gw;
           const int64_t oy = (int64_t)img * p.sc_gh * p.sc_r + yy * p.sc_r + sc_i;
           const int64_t ox = (int64_t)xx * p.sc_r + sc_j;
-          *(fx4*)(p.C + (oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c) = v;
+          const int64_t si = (oy * p.sc_gw * p.sc_r + ox) * p.sc_Cout + sc_c;
+          if (flags & EPI_BF16OUT) {
+            typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+            const bf16x4_t h = {(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+            *(bf16x4_t*)((__bf16*)p.C + si) = h;
+          } else {
+            *(fx4*)(p.C + si) = v;
+          }
         }
       } else if (flags & EPI_BF16OUT) {
         typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
@@ -1652,7 +1663,7 @@ bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 bool row_epi_ok(const GemmArgs& g) {
   if (g.flags & EPI_SCATTER)  // 4-column segments stay within one output pixel
     return g.sc_C % 4 == 0 && g.sc_Cout % 4 == 0 && g.N % 4 == 0 && aligned16(g.C) &&
-           !(g.flags & (EPI_RES1 | EPI_RES2 | EPI_ROPE | EPI_DUAL | EPI_BF16OUT));
+           !(g.flags & (EPI_RES1 | EPI_RES2 | EPI_ROPE | EPI_DUAL));
   if (g.N % 4 || g.ldc % 4 || !aligned16(g.C)) return false;
   if ((g.flags & EPI_RES1) && (g.ldr1 % 4 || !aligned16(g.R1))) return false;
   if ((g.flags & EPI_RES2) && (g.ldr2 % 4 || !aligned16(g.R2))) return false;
@@ -1719,8 +1730,8 @@ int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16) {
                    a.grid_w > 0,
                "gemm: RoPE excludes residual epilogues and needs M < 2^22");
   if (a.flags & EPI_BF16OUT)
-    GS_REQUIRE(!(a.flags & (EPI_SCATTER | EPI_DUAL)) && a.ldc % 4 == 0,
-               "gemm: bf16 output excludes scatter / dual stores");
+    GS_REQUIRE(!(a.flags & EPI_DUAL) && ((a.flags & EPI_SCATTER) || a.ldc % 4 == 0),
+               "gemm: bf16 output excludes dual stores");
   if (a.flags & EPI_LNOUT)
     GS_REQUIRE(!(a.flags & ~(EPI_BIAS | EPI_RES1 | EPI_RES2 | EPI_LNOUT)) && a.N % 4 == 0 &&
                    a.N <= 4096 && a.ldc == a.N && a.lnout && a.lnout_g && a.lnout_b &&

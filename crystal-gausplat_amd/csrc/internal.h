@@ -78,7 +78,7 @@ enum EpiFlags : int {
   EPI_ROPE = 32,     // RoPE on columns [0, rope_ncols)
   EPI_SCATTER = 64,  // sub-pixel scatter store (ConvT / pixel shuffle)
   EPI_DUAL = 128,    // also store the result to C2 (same ldc)
-  EPI_BF16OUT = 256, // C holds bf16 (ldc in elements); not with SCATTER / DUAL
+  EPI_BF16OUT = 256, // C holds bf16 (ldc in elements; with SCATTER the scattered store); not with DUAL
   EPI_LNOUT = 512,   // also the LayerNorm of every output row into lnout (see GemmArgs)
   EPI_DUAL_RELU_H = 1024,  // with EPI_DUAL: C2 holds bf16 and receives bf16(max(v, 0))
 };

@@ -718,21 +718,27 @@ int conv(Ctx& c, const Heads& hs, const std::string& suffix, const float* const 
     b.g[v] = a;
   }
   const bool pointwise = (k == 1 && stride == 1 && pad == 0);
-  // in_bf16: x holds bf16 (the bf16 mode's head upsample writes it so)
-  GS_REQUIRE(!in_bf16 || (!pointwise && !relu_in && c.cfg.precision == 1),
-             "conv: a bf16 input needs a 3x3 conv without ReLU prologue in the bf16 mode");
-  return gemm(c, b, pointwise ? A_PLAIN : (in_bf16 ? A_CONV_H : A_CONV), relu_in, s);
+  // in_bf16: x holds bf16 (its producer wrote it so in the bf16 mode)
+  GS_REQUIRE(!in_bf16 || (!relu_in && c.cfg.precision == 1),
+             "conv: a bf16 input needs a conv without ReLU prologue in the bf16 mode");
+  const int al = pointwise ? (in_bf16 ? A_PLAIN_H : A_PLAIN) : (in_bf16 ? A_CONV_H : A_CONV);
+  return gemm(c, b, al, relu_in, s);
 }
 
-// ConvTranspose (k == s) from [rows, Cin] token tensors on the gh x gw grid.
+// ConvTranspose (k == s) from [rows, Cin] token tensors on the gh x gw grid;
+// bf16 mode: in_bf16 / out_bf16 read / write bf16 rows.
 int convt(Ctx& c, const Heads& hs, const std::string& suffix, const float* const x[2], int imgs,
-          int Cin, int Cout, int k, float* const y[2], hipStream_t s) {
+          int Cin, int Cout, int k, float* const y[2], hipStream_t s, bool in_bf16 = false,
+          bool out_bf16 = false) {
+  GS_REQUIRE(!(in_bf16 || out_bf16) || c.cfg.precision == 1,
+             "convt: bf16 rows are the bf16 mode's");
   GemmBatch b;
   b.ngroups = hs.n;
   for (int v = 0; v < hs.n; ++v) {
     const std::string name = hs.pre(v) + suffix;
     GemmArgs a = lin(x[v], Cin, c.derived[name + ".weight"], c.derived[name + ".bias"], y[v], 0,
-                     (int64_t)imgs * c.N, k * k * Cout, Cin, EPI_SCATTER);
+                     (int64_t)imgs * c.N, k * k * Cout, Cin,
+                     EPI_SCATTER | (out_bf16 ? EPI_BF16OUT : 0));
     a.sc_r = k;
     a.sc_C = Cout;
     a.sc_Cout = Cout;
@@ -740,7 +746,7 @@ int convt(Ctx& c, const Heads& hs, const std::string& suffix, const float* const
     a.sc_gw = c.gw;
     b.g[v] = a;
   }
-  return gemm(c, b, A_PLAIN, false, s);
+  return gemm(c, b, in_bf16 ? A_PLAIN_H : A_PLAIN, false, s);
 }
 
 // FeatureFusionBlock: out = out_conv(up2(RCU2(x0 (+ RCU1(x1))))). The 1x1
@@ -788,10 +794,12 @@ int fusion(Ctx& c, const Heads& hs, const std::string& suffix, const float* cons
             EPI_RELU, true, s));
   }
   const float* uin[2] = {c.u[0], c.u[1]};
-  RC(conv(c, hs, suffix + ".resConfUnit2.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.t, 0, false,
+  // RCU2's output feeds only the 1x1 out_conv: bf16 in the bf16 mode
+  RC(conv(c, hs, suffix + ".resConfUnit2.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.t, ub, false,
           s, sum, nullptr, hb));
   const float* tin[2] = {c.t[0], c.t[1]};
-  RC(conv(c, hs, suffix + ".out_conv", tin, B, H, W_, F, F, 1, 1, 0, true, c.up, 0, false, s));
+  RC(conv(c, hs, suffix + ".out_conv", tin, B, H, W_, F, F, 1, 1, 0, true, c.up, 0, false, s,
+          nullptr, nullptr, hb));
   for (int v = 0; v < hs.n; ++v)
     RC(launch_upsample2x(c.up[v], B, H, W_, F, out[v], s, out_bf16 && hb));
   return 0;
@@ -809,14 +817,19 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
   float* act[4][2];
   for (int i = 0; i < 4; ++i)
     for (int v = 0; v < 2; ++v) act[i][v] = c.act[v][i];
-  // act_postprocess
-  RC(conv(c, hs, ap + "0.0", e, B, gh, gw, f.enc_dim, d[0], 1, 1, 0, true, c.t0, 0, false, s));
-  RC(convt(c, hs, ap + "0.1", t0c, B, d[0], d[0], 4, act[0], s));
-  RC(conv(c, hs, ap + "1.0", h6, B, gh, gw, f.dec_dim, d[1], 1, 1, 0, true, c.t0, 0, false, s));
-  RC(convt(c, hs, ap + "1.1", t0c, B, d[1], d[1], 2, act[1], s));
-  RC(conv(c, hs, ap + "2.0", h9, B, gh, gw, f.dec_dim, d[2], 1, 1, 0, true, act[2], 0, false, s));
-  RC(conv(c, hs, ap + "3.0", dfin, B, gh, gw, f.dec_dim, d[3], 1, 1, 0, true, c.t0, 0, false, s));
-  RC(conv(c, hs, ap + "3.1", t0c, B, gh, gw, d[3], d[3], 3, 2, 1, true, act[3], 0, false, s));
+  // act_postprocess. bf16 mode: every output here feeds a single bf16 GEMM
+  // (the next act_postprocess step or a layer_rn conv), so it is written in
+  // bf16 and read so
+  const bool hb = f.precision == 1;
+  const int ub = hb ? EPI_BF16OUT : 0;
+  RC(conv(c, hs, ap + "0.0", e, B, gh, gw, f.enc_dim, d[0], 1, 1, 0, true, c.t0, ub, false, s));
+  RC(convt(c, hs, ap + "0.1", t0c, B, d[0], d[0], 4, act[0], s, hb, hb));
+  RC(conv(c, hs, ap + "1.0", h6, B, gh, gw, f.dec_dim, d[1], 1, 1, 0, true, c.t0, ub, false, s));
+  RC(convt(c, hs, ap + "1.1", t0c, B, d[1], d[1], 2, act[1], s, hb, hb));
+  RC(conv(c, hs, ap + "2.0", h9, B, gh, gw, f.dec_dim, d[2], 1, 1, 0, true, act[2], ub, false, s));
+  RC(conv(c, hs, ap + "3.0", dfin, B, gh, gw, f.dec_dim, d[3], 1, 1, 0, true, c.t0, ub, false, s));
+  RC(conv(c, hs, ap + "3.1", t0c, B, gh, gw, d[3], d[3], 3, 2, 1, true, act[3], ub, false, s,
+          nullptr, nullptr, hb));
   const int ah[4] = {4 * gh, 2 * gh, gh, gh / 2}, aw[4] = {4 * gw, 2 * gw, gw, gw / 2};
   float* L[4][2];
   for (int i = 0; i < 4; ++i) {
@@ -824,8 +837,7 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
     const float* ain[2] = {act[i][0], act[i][1]};
     float* Lh[2] = {c.Lh[0][i], c.Lh[1][i]};
     RC(conv(c, hs, ".dpt.scratch.layer" + std::to_string(i + 1) + "_rn", ain, B, ah[i], aw[i], d[i],
-            F, 3, 1, 1, false, L[i], 0, false, s, nullptr, nullptr, false,
-            f.precision == 1 ? Lh : nullptr));
+            F, 3, 1, 1, false, L[i], 0, false, s, nullptr, nullptr, hb, hb ? Lh : nullptr));
   }
   const float* Lhc[4][2];
   for (int i = 0; i < 4; ++i)
@@ -843,10 +855,9 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
   RC(fusion(c, hs, rp + "1", rAc, Lc[0], B, ah[0], aw[0], c.rB, s, true, nullptr, Lhc[0]));
   const int h1 = 2 * ah[0], w1 = 2 * aw[0];
   RC(conv(c, hs, ".dpt.head.0", rBc, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s,
-          nullptr, nullptr, f.precision == 1));
+          nullptr, nullptr, hb));
   // bf16 mode: the full-resolution upsample feeds only the next conv, so it is
   // written in bf16 (the rounding that conv's A load would apply) and read so
-  const bool hb = f.precision == 1;
   for (int v = 0; v < hs.n; ++v)
     RC(launch_upsample2x(c.hd0[v], B, h1, w1, F / 2, c.hup[v], s, hb));
   const float* hupc[2] = {c.hup[0], c.hup[1]};
