@@ -272,7 +272,9 @@ __global__ void rope_ref_token_kernel(const float* __restrict__ x, float* __rest
 // MASt3R confidence mapping) or, SIGMOID, the reference's own 1 / (1 + exp(-x)).
 constexpr int kHeadOutIter = 8;  // groups of 32 pixels per workgroup
 
-template <bool SIGMOID>
+// INH: x holds bf16 (the bf16 mode's head.2 writes its ReLU output so); a
+// lane's 16-byte chunks then hold 8 channels.
+template <bool SIGMOID, bool INH>
 __global__ __launch_bounds__(256) void head_out_kernel(const float* __restrict__ x, int64_t P,
                                                        int32_t Cin, const float* __restrict__ w,
                                                        const float* __restrict__ b,
@@ -293,16 +295,29 @@ __global__ __launch_bounds__(256) void head_out_kernel(const float* __restrict__
   for (int it = 0; it < kHeadOutIter; ++it) {
     const int64_t px = ((int64_t)blockIdx.x * kHeadOutIter + it) * 32 + (threadIdx.x >> 3);
     if (px >= P) break;  // uniform within each group of eight lanes
-    const fx4* xr = (const fx4*)(x + px * Cin);
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll 4
-    for (int c4 = sub; c4 < n4; c4 += 8) {
-      const fx4 v = xr[c4];
+    auto dot4 = [&](const fx4& v, int c4) {
       const fx4 q0 = w0[c4], q1 = w1[c4], q2 = w2[c4], q3 = w3[c4];
       a0 += v.x * q0.x + v.y * q0.y + v.z * q0.z + v.w * q0.w;
       a1 += v.x * q1.x + v.y * q1.y + v.z * q1.z + v.w * q1.w;
       a2 += v.x * q2.x + v.y * q2.y + v.z * q2.z + v.w * q2.w;
       a3 += v.x * q3.x + v.y * q3.y + v.z * q3.z + v.w * q3.w;
+    };
+    if constexpr (INH) {
+      typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+      const u32x4_t* xr = (const u32x4_t*)((const __bf16*)x + px * Cin);
+      auto lo = [](uint32_t u) { return __uint_as_float(u << 16); };
+      auto hi = [](uint32_t u) { return __uint_as_float(u & 0xffff0000u); };
+#pragma unroll 2
+      for (int c8 = sub; c8 < (n4 >> 1); c8 += 8) {
+        const u32x4_t u = xr[c8];
+        dot4(mk4(lo(u.x), hi(u.x), lo(u.y), hi(u.y)), 2 * c8);
+        dot4(mk4(lo(u.z), hi(u.z), lo(u.w), hi(u.w)), 2 * c8 + 1);
+      }
+    } else {
+      const fx4* xr = (const fx4*)(x + px * Cin);
+#pragma unroll 4
+      for (int c4 = sub; c4 < n4; c4 += 8) dot4(xr[c4], c4);
     }
 #pragma unroll
     for (int o = 1; o < 8; o <<= 1) {  // xor 1, 2, 4 stay inside the group
@@ -432,20 +447,26 @@ int launch_rope_ref_token(const float* x, float* y, int32_t B, int32_t gh, int32
 }
 
 int launch_head_out(const float* x, int64_t P, int32_t Cin, const float* w, const float* b,
-                    float* pts, float* conf, bool sigmoid, hipStream_t s) {
+                    float* pts, float* conf, bool sigmoid, hipStream_t s, bool in_bf16) {
   GS_REQUIRE(Cin % 4 == 0 && Cin <= 4096, "head_out: need Cin % 4 == 0");
+  GS_REQUIRE(!in_bf16 || Cin % 8 == 0, "head_out: bf16 input needs Cin % 8 == 0");
   GS_REQUIRE(aligned16(x), "head_out: input must be 16-byte aligned");
   GS_REQUIRE(grid_fits(P, 32 * kHeadOutIter), "head_out: bad pixel count");
   if (P == 0) return 0;
   hipEvent_t ev = prof_start(s);
-  if (sigmoid)
-    hipLaunchKernelGGL(head_out_kernel<true>, dim3(nblocks(P, 32 * kHeadOutIter)), dim3(256),
-                       4 * Cin * sizeof(float), s, x, P, Cin, w, b, pts, conf);
+  const dim3 grid(nblocks(P, 32 * kHeadOutIter)), block(256);
+  const size_t lds = 4 * Cin * sizeof(float);
+  if (sigmoid && in_bf16)
+    hipLaunchKernelGGL((head_out_kernel<true, true>), grid, block, lds, s, x, P, Cin, w, b, pts, conf);
+  else if (sigmoid)
+    hipLaunchKernelGGL((head_out_kernel<true, false>), grid, block, lds, s, x, P, Cin, w, b, pts, conf);
+  else if (in_bf16)
+    hipLaunchKernelGGL((head_out_kernel<false, true>), grid, block, lds, s, x, P, Cin, w, b, pts, conf);
   else
-    hipLaunchKernelGGL(head_out_kernel<false>, dim3(nblocks(P, 32 * kHeadOutIter)), dim3(256),
-                       4 * Cin * sizeof(float), s, x, P, Cin, w, b, pts, conf);
+    hipLaunchKernelGGL((head_out_kernel<false, false>), grid, block, lds, s, x, P, Cin, w, b, pts, conf);
   GS_CHECK_HIP(hipGetLastError());
-  prof_stop(s, ev, "head_out_kernel", 8.0 * (double)P * Cin, 4.0 * (double)P * (Cin + 4));
+  prof_stop(s, ev, "head_out_kernel", 8.0 * (double)P * Cin,
+            (in_bf16 ? 2.0 : 4.0) * (double)P * Cin + 16.0 * (double)P);
   return 0;
 }
 

@@ -218,7 +218,7 @@ int launch_rope_ref_token(const float* x, float* y, int32_t B, int32_t gh,
                           const float* sin_t, int32_t max_pos, hipStream_t s);
 // conv 1x1 Cin->4 + split: pts [P,3] = y[0..2], conf [P] = 1 + exp(y[3]).
 int launch_head_out(const float* x, int64_t P, int32_t Cin, const float* w, const float* b,
-                    float* pts, float* conf, bool sigmoid, hipStream_t s);
+                    float* pts, float* conf, bool sigmoid, hipStream_t s, bool in_bf16 = false);
 
 // Weight re-layouts (device): OIHW -> OHWI; ConvTranspose [Cin,Cout,k,k] ->
 // [(i*k+j)*Cout + oc][Cin] with the bias expanded to k*k*Cout columns.

@@ -861,12 +861,13 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
   for (int v = 0; v < hs.n; ++v)
     RC(launch_upsample2x(c.hd0[v], B, h1, w1, F / 2, c.hup[v], s, hb));
   const float* hupc[2] = {c.hup[0], c.hup[1]};
+  // head.2's ReLU output feeds only head.4 (head_out): bf16 in the bf16 mode
   RC(conv(c, hs, ".dpt.head.2", hupc, B, 2 * h1, 2 * w1, F / 2, f.head_mid, 3, 1, 1, true, c.hd2,
-          EPI_RELU, false, s, nullptr, nullptr, hb));
+          EPI_RELU | (hb ? EPI_BF16OUT : 0), false, s, nullptr, nullptr, hb));
   for (int v = 0; v < hs.n; ++v)
     RC(launch_head_out(c.hd2[v], (int64_t)B * 4 * h1 * w1, f.head_mid,
                        W(c, hs.pre(v) + ".dpt.head.4.weight"), W(c, hs.pre(v) + ".dpt.head.4.bias"),
-                       pts[v], conf[v], false, s));
+                       pts[v], conf[v], false, s, hb));
   return 0;
 }
 
