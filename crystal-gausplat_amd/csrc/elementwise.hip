@@ -116,7 +116,8 @@ __global__ void unfold_kernel(const float* __restrict__ img, int32_t B, int32_t 
 // 16-byte loads per 16-byte output held the kernel near half of the HBM
 // bandwidth on L1 traffic). Wider rows step over flat element indices.
 constexpr int kUpsRun = 8;
-template <bool OUT_BF16>
+// IN_BF16 / OUT_BF16: x / y hold bf16 (element offsets are unchanged).
+template <bool IN_BF16, bool OUT_BF16>
 __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict__ x,
                                                          int32_t H, int32_t W, int32_t C,
                                                          int32_t blocks_per_row, int32_t px,
@@ -134,8 +135,19 @@ __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict
   const int y0 = (int)fy;
   const int y1 = y0 + (y0 < H - 1 ? 1 : 0);
   const float ly = fy - (float)y0, hy = 1.0f - ly;
-  const float* r0 = x + ((int64_t)b * H + y0) * W * C;
-  const float* r1 = x + ((int64_t)b * H + y1) * W * C;
+  const int64_t o0 = ((int64_t)b * H + y0) * W * C, o1 = ((int64_t)b * H + y1) * W * C;
+  // four channels of source row r (0: y0, 1: y1) at element offset off
+  auto ld = [&](int r, int64_t off) -> fx4 {
+    const int64_t e = (r ? o1 : o0) + off;
+    if constexpr (IN_BF16) {
+      const uint64_t u = *(const uint64_t*)((const __bf16*)x + e);
+      const uint32_t w0 = (uint32_t)u, w1 = (uint32_t)(u >> 32);
+      return mk4(__uint_as_float(w0 << 16), __uint_as_float(w0 & 0xffff0000u),
+                 __uint_as_float(w1 << 16), __uint_as_float(w1 & 0xffff0000u));
+    } else {
+      return *(const fx4*)(x + e);
+    }
+  };
   float* yrow = y + (int64_t)row * Wo * C;
   // the bilinear blend of the four source values
   auto blend = [&](const fx4& a, const fx4& bq, const fx4& cq, const fx4& d, float lx, float hx) {
@@ -166,8 +178,7 @@ __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict
     const int x1 = x0 + (x0 < W - 1 ? 1 : 0);
     const float lx = fx - (float)x0, hx = 1.0f - lx;
     const int64_t c0 = (int64_t)x0 * C + 4 * cg, c1 = (int64_t)x1 * C + 4 * cg;
-    store(ox, cg, blend(*(const fx4*)(r0 + c0), *(const fx4*)(r0 + c1), *(const fx4*)(r1 + c0),
-                        *(const fx4*)(r1 + c1), lx, hx));
+    store(ox, cg, blend(ld(0, c0), ld(0, c1), ld(1, c0), ld(1, c1), lx, hx));
   };
   if (C4 <= 256) {
     const int ppi = 256 / C4;  // pixel runs per workgroup
@@ -191,8 +202,8 @@ __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict
         a = pb;
         cq = pd;
       } else {
-        a = *(const fx4*)(r0 + (int64_t)x0 * C + 4 * cg);
-        cq = *(const fx4*)(r1 + (int64_t)x0 * C + 4 * cg);
+        a = ld(0, (int64_t)x0 * C + 4 * cg);
+        cq = ld(1, (int64_t)x0 * C + 4 * cg);
       }
       if (x1 == x0) {
         bq = a;
@@ -201,8 +212,8 @@ __global__ __launch_bounds__(256) void upsample2x_kernel(const float* __restrict
         bq = pb;
         d = pd;
       } else {
-        bq = *(const fx4*)(r0 + (int64_t)x1 * C + 4 * cg);
-        d = *(const fx4*)(r1 + (int64_t)x1 * C + 4 * cg);
+        bq = ld(0, (int64_t)x1 * C + 4 * cg);
+        d = ld(1, (int64_t)x1 * C + 4 * cg);
       }
       p0 = x0;
       p1 = x1;
@@ -394,7 +405,7 @@ int launch_unfold(const float* img, int32_t B, int32_t H, int32_t W, int32_t p,
 }
 
 int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C,
-                      float* y, hipStream_t s, bool out_bf16) {
+                      float* y, hipStream_t s, bool out_bf16, bool in_bf16) {
   GS_REQUIRE(C > 0 && C % 4 == 0 && H > 0 && W > 0 && B >= 0, "upsample2x: need C % 4 == 0");
   GS_REQUIRE(aligned16(x) && aligned16(y), "upsample2x: operands must be 16-byte aligned");
   GS_REQUIRE((int64_t)2 * W * (C / 4) <= INT32_MAX && (int64_t)2 * B * H <= INT32_MAX,
@@ -407,14 +418,22 @@ int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   GS_REQUIRE(nblk < INT32_MAX, "upsample2x: too many elements");
   if (nblk == 0) return 0;
   hipEvent_t ev = prof_start(s);
-  if (out_bf16)
-    hipLaunchKernelGGL(upsample2x_kernel<true>, dim3((uint32_t)nblk), dim3(256), 0, s, x, H, W, C,
+  const dim3 grid((uint32_t)nblk), block(256);
+  if (in_bf16 && out_bf16)
+    hipLaunchKernelGGL((upsample2x_kernel<true, true>), grid, block, 0, s, x, H, W, C, blocks_per_row,
+                       px, y);
+  else if (in_bf16)
+    hipLaunchKernelGGL((upsample2x_kernel<true, false>), grid, block, 0, s, x, H, W, C,
+                       blocks_per_row, px, y);
+  else if (out_bf16)
+    hipLaunchKernelGGL((upsample2x_kernel<false, true>), grid, block, 0, s, x, H, W, C,
                        blocks_per_row, px, y);
   else
-    hipLaunchKernelGGL(upsample2x_kernel<false>, dim3((uint32_t)nblk), dim3(256), 0, s, x, H, W, C,
+    hipLaunchKernelGGL((upsample2x_kernel<false, false>), grid, block, 0, s, x, H, W, C,
                        blocks_per_row, px, y);
   GS_CHECK_HIP(hipGetLastError());
-  prof_stop(s, ev, "upsample2x_kernel", 0.0, (double)B * H * W * C * (4.0 + (out_bf16 ? 8.0 : 16.0)));
+  prof_stop(s, ev, "upsample2x_kernel", 0.0,
+            (double)B * H * W * C * ((in_bf16 ? 2.0 : 4.0) + (out_bf16 ? 8.0 : 16.0)));
   return 0;
 }
 

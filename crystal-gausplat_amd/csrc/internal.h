@@ -208,7 +208,8 @@ int launch_unfold(const float* img, int32_t B, int32_t H, int32_t W, int32_t p,
                   float* out, hipStream_t s);
 // out_bf16: y holds bf16 (for a bf16 conv that reads it, A_CONV_H)
 int launch_upsample2x(const float* x, int32_t B, int32_t H, int32_t W,
-                      int32_t C, float* y, hipStream_t s, bool out_bf16 = false);
+                      int32_t C, float* y, hipStream_t s, bool out_bf16 = false,
+                      bool in_bf16 = false);
 int launch_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld,
                   int32_t grid_w, const float* cos_t, const float* sin_t,
                   hipStream_t s);

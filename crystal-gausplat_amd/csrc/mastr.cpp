@@ -798,10 +798,13 @@ int fusion(Ctx& c, const Heads& hs, const std::string& suffix, const float* cons
   RC(conv(c, hs, suffix + ".resConfUnit2.conv2", uin, B, H, W_, F, F, 3, 1, 1, true, c.t, ub, false,
           s, sum, nullptr, hb));
   const float* tin[2] = {c.t[0], c.t[1]};
-  RC(conv(c, hs, suffix + ".out_conv", tin, B, H, W_, F, F, 1, 1, 0, true, c.up, 0, false, s,
-          nullptr, nullptr, hb));
+  // a bf16 output (single bf16 consumer): out_conv's rows, which feed only
+  // the upsample, are bf16 too
+  const bool ob = out_bf16 && hb;
+  RC(conv(c, hs, suffix + ".out_conv", tin, B, H, W_, F, F, 1, 1, 0, true, c.up,
+          ob ? EPI_BF16OUT : 0, false, s, nullptr, nullptr, hb));
   for (int v = 0; v < hs.n; ++v)
-    RC(launch_upsample2x(c.up[v], B, H, W_, F, out[v], s, out_bf16 && hb));
+    RC(launch_upsample2x(c.up[v], B, H, W_, F, out[v], s, ob, ob));
   return 0;
 }
 
@@ -854,12 +857,13 @@ int dpt_heads(Ctx& c, const Heads& hs, const float* const e[2], const float* con
   // refinenet1's output feeds only head.0: bf16 in the bf16 mode
   RC(fusion(c, hs, rp + "1", rAc, Lc[0], B, ah[0], aw[0], c.rB, s, true, nullptr, Lhc[0]));
   const int h1 = 2 * ah[0], w1 = 2 * aw[0];
-  RC(conv(c, hs, ".dpt.head.0", rBc, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0, 0, false, s,
-          nullptr, nullptr, hb));
-  // bf16 mode: the full-resolution upsample feeds only the next conv, so it is
-  // written in bf16 (the rounding that conv's A load would apply) and read so
+  // bf16 mode: head.0's output feeds only the upsample, and the
+  // full-resolution upsample feeds only the next conv, so both are written in
+  // bf16 (the rounding that conv's A load would apply) and read so
+  RC(conv(c, hs, ".dpt.head.0", rBc, B, h1, w1, F, F / 2, 3, 1, 1, true, c.hd0,
+          hb ? EPI_BF16OUT : 0, false, s, nullptr, nullptr, hb));
   for (int v = 0; v < hs.n; ++v)
-    RC(launch_upsample2x(c.hd0[v], B, h1, w1, F / 2, c.hup[v], s, hb));
+    RC(launch_upsample2x(c.hd0[v], B, h1, w1, F / 2, c.hup[v], s, hb, hb));
   const float* hupc[2] = {c.hup[0], c.hup[1]};
   // head.2's ReLU output feeds only head.4 (head_out): bf16 in the bf16 mode
   RC(conv(c, hs, ".dpt.head.2", hupc, B, 2 * h1, 2 * w1, F / 2, f.head_mid, 3, 1, 1, true, c.hd2,
