@@ -10,76 +10,90 @@ namespace {
 
 // LayerNorm#forward_cpu (src/nn/layernorm.cr:192-240): two-pass mean /
 // variance, inv_std = 1/sqrt(var + eps), y = (x - mean)*inv_std*gamma + beta.
-// One wavefront per row, the row held in registers (D <= 256*NV).
+// One wavefront per row, the row held in registers (D <= 256*NV). The grid
+// is capped at the resident workgroups, so each wave steps over rows: gamma
+// and beta are loaded once per wave, and the next row's load is in flight
+// while the current row is reduced and stored.
+constexpr int kLnBlocks = 1280;  // workgroups per group: the 5 per CU that 95 VGPRs leave resident
 template <int NV>
 __global__ __launch_bounds__(256) void layernorm_kernel(LnBatch bt) {
   const LnArgs& p = bt.g[blockIdx.y];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * 4 + wave;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  int64_t row = (int64_t)blockIdx.x * 4 + wave;
   if (row >= p.rows) return;
   const int D = p.D, nv = D >> 2;
-  const fx4* xr = (const fx4*)(p.x + row * D);
-  fx4 v[NV], g[NV], bb[NV];
-  // gamma and beta are loaded with the row: after the reductions (and the
-  // statistics store, which they may alias for the compiler) their latency
-  // would follow the row's instead of overlapping it
   const bool out = p.y != nullptr;
+  fx4 v[NV], g[NV], bb[NV];
+  auto load_row = [&](int64_t r, fx4* dst) {
+    const fx4* xr = (const fx4*)(p.x + r * D);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int idx = lane + 64 * i;
+      dst[i] = idx < nv ? xr[idx] : mk4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  load_row(row, v);
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     const int idx = lane + 64 * i;
-    if (idx < nv) {
-      v[i] = xr[idx];
-      if (out) {
-        g[i] = ((const fx4*)p.gamma)[idx];
-        bb[i] = ((const fx4*)p.beta)[idx];
-      }
-    } else {
-      v[i] = mk4(0.f, 0.f, 0.f, 0.f);
+    if (out && idx < nv) {
+      g[i] = ((const fx4*)p.gamma)[idx];
+      bb[i] = ((const fx4*)p.beta)[idx];
     }
   }
-  float s = 0.f;
+  for (;;) {
+    const int64_t next = row + stride;
+    fx4 vn[NV];
+    if (next < p.rows) load_row(next, vn);
+    float s = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (lane + 64 * i < nv) s += v[i].x + v[i].y + v[i].z + v[i].w;
-  const float mean = wave_sum(s) / (float)D;
-  float q = 0.f;
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < nv) s += v[i].x + v[i].y + v[i].z + v[i].w;
+    const float mean = wave_sum(s) / (float)D;
+    float q = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int idx = lane + 64 * i;
-    if (idx < nv) {
-      const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
-      q += a * a + b * b + c * c + d * d;
-    }
-  }
-  const float var = wave_sum(q) / (float)D;
-  const float inv = 1.0f / sqrtf(var + p.eps);
-  if (p.stats && lane == 0) {  // for GEMMs that apply the normalisation on load
-    p.stats[2 * row] = mean;
-    p.stats[2 * row + 1] = inv;
-  }
-  if (!out) return;
-  fx4* yr = (fx4*)(p.y + row * D);
-#pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int idx = lane + 64 * i;
-    if (idx < nv) {
-      fx4 o;
-      o.x = (v[i].x - mean) * inv * g[i].x + bb[i].x;
-      o.y = (v[i].y - mean) * inv * g[i].y + bb[i].y;
-      o.z = (v[i].z - mean) * inv * g[i].z + bb[i].z;
-      o.w = (v[i].w - mean) * inv * g[i].w + bb[i].w;
-      if (p.y_bf16) {
-        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
-        bf16x4_t h;
-        h.x = (__bf16)o.x;
-        h.y = (__bf16)o.y;
-        h.z = (__bf16)o.z;
-        h.w = (__bf16)o.w;
-        ((bf16x4_t*)((__bf16*)p.y + row * D))[idx] = h;
-      } else {
-        yr[idx] = o;
+    for (int i = 0; i < NV; ++i) {
+      if (lane + 64 * i < nv) {
+        const float a = v[i].x - mean, b = v[i].y - mean, c = v[i].z - mean, d = v[i].w - mean;
+        q += a * a + b * b + c * c + d * d;
       }
     }
+    const float var = wave_sum(q) / (float)D;
+    const float inv = 1.0f / sqrtf(var + p.eps);
+    if (p.stats && lane == 0) {  // for GEMMs that apply the normalisation on load
+      p.stats[2 * row] = mean;
+      p.stats[2 * row + 1] = inv;
+    }
+    if (out) {
+      fx4* yr = (fx4*)(p.y + row * D);
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int idx = lane + 64 * i;
+        if (idx < nv) {
+          fx4 o;
+          o.x = (v[i].x - mean) * inv * g[i].x + bb[i].x;
+          o.y = (v[i].y - mean) * inv * g[i].y + bb[i].y;
+          o.z = (v[i].z - mean) * inv * g[i].z + bb[i].z;
+          o.w = (v[i].w - mean) * inv * g[i].w + bb[i].w;
+          if (p.y_bf16) {
+            typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+            bf16x4_t h;
+            h.x = (__bf16)o.x;
+            h.y = (__bf16)o.y;
+            h.z = (__bf16)o.z;
+            h.w = (__bf16)o.w;
+            ((bf16x4_t*)((__bf16*)p.y + row * D))[idx] = h;
+          } else {
+            yr[idx] = o;
+          }
+        }
+      }
+    }
+    if (next >= p.rows) break;
+    row = next;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = vn[i];
   }
 }
 
@@ -369,7 +383,7 @@ int launch_layernorm(const LnBatch& bt, hipStream_t s) {
   }
   GS_REQUIRE(D > 0 && D % 4 == 0 && D <= 4096, "layernorm: need 0 < D <= 4096, D % 4 == 0");
   if (max_rows == 0) return 0;
-  dim3 grid(nblocks(max_rows, 4), bt.ngroups), block(256);
+  dim3 grid(std::min(nblocks(max_rows, 4), (unsigned)kLnBlocks), bt.ngroups), block(256);
   hipEvent_t ev = prof_start(s);
   if (D <= 1024)
     hipLaunchKernelGGL(layernorm_kernel<4>, grid, block, 0, s, bt);
