@@ -279,10 +279,28 @@ __device__ __forceinline__ void store_partial(const GemmArgs& p, const floatx16&
 // gemm_epilogue in the same operation order (bias, RoPE, GELU / ReLU,
 // residuals, store, dual store). One thread per 4 consecutive columns; RoPE
 // reads the partner columns (col ^ 16) the same way. N % 4 == 0, no scatter.
+// The loads go out four (then two) at a time before their adds (a load-add
+// loop waits for each partial in turn); the adds keep the split order.
 __device__ __forceinline__ fx4 splitk_sum(const GemmArgs& p, int S, int64_t off) {
   const int64_t plane = (int64_t)p.M * p.N;
-  fx4 v = *(const fx4*)(p.part + off);
-  for (int s = 1; s < S; ++s) v = v + *(const fx4*)(p.part + s * plane + off);
+  const float* q = p.part + off;
+  fx4 v = *(const fx4*)q;
+  int s = 1;
+  for (; s + 3 < S; s += 4) {
+    const fx4 a = *(const fx4*)(q + s * plane), b = *(const fx4*)(q + (s + 1) * plane);
+    const fx4 c = *(const fx4*)(q + (s + 2) * plane), d = *(const fx4*)(q + (s + 3) * plane);
+    v = v + a;
+    v = v + b;
+    v = v + c;
+    v = v + d;
+  }
+  if (s + 1 < S) {
+    const fx4 a = *(const fx4*)(q + s * plane), b = *(const fx4*)(q + (s + 1) * plane);
+    v = v + a;
+    v = v + b;
+    s += 2;
+  }
+  if (s < S) v = v + *(const fx4*)(q + s * plane);
   return v;
 }
 
