@@ -1045,6 +1045,14 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
   const float bv0 = (flags & EPI_BIAS) ? p.bias[min(col0 + l32, N - 1)] : 0.f;
   const float bv1 = (flags & EPI_BIAS) ? p.bias[min(col0 + 32 + l32, N - 1)] : 0.f;
   const bool rope = ROPE && col0 < p.rope_ncols;
+  // With the tokens per image and the grid width multiples of 4, the four
+  // rows 4k .. 4k + 3 of accumulator registers 4g .. 4g + 3 lie in one image
+  // and grid row: their position is decoded once (the first row's, x + j for
+  // row j) and the y-axis cos / sin are read once. Rows at or past M are not
+  // stored; their group decodes the last group start below M.
+  const bool grp4 = ROPE && ((p.tok_per_img | p.grid_w) & 3) == 0;
+  int gty = 0, gtx = 0;
+  float gcy = 0.f, gsy = 0.f;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     float v0 = q0[r], v1 = q1[r];
@@ -1054,12 +1062,33 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
     }
     if (rope) {
       // the row's grid position, frequency l32 % 16
-      const int row = min(row0 + 8 * (r >> 2) + 4 * hl + (r & 3), M - 1);
-      int tok, tx;
-      divmod_small(row, p.tok_per_img, rtok, tok);
-      const int ty = divmod_small(tok, p.grid_w, rgw, tx);
-      const int iy = ty * 16 + (l32 & 15), ix = tx * 16 + (l32 & 15);
-      const float cy = p.rope_cos[iy], sy = p.rope_sin[iy];
+      int ty, tx;
+      float cy, sy;
+      if (grp4) {
+        if ((r & 3) == 0) {
+          const int rg = min(row0 + 8 * (r >> 2) + 4 * hl, (M - 1) & ~3);
+          int tok;
+          divmod_small(rg, p.tok_per_img, rtok, tok);
+          gty = divmod_small(tok, p.grid_w, rgw, gtx);
+          const int iy = gty * 16 + (l32 & 15);
+          gcy = p.rope_cos[iy];
+          gsy = p.rope_sin[iy];
+        }
+        ty = gty;
+        tx = gtx + (r & 3);
+        cy = gcy;
+        sy = gsy;
+      } else {
+        const int row = min(row0 + 8 * (r >> 2) + 4 * hl + (r & 3), M - 1);
+        int tok;
+        divmod_small(row, p.tok_per_img, rtok, tok);
+        ty = divmod_small(tok, p.grid_w, rgw, tx);
+        const int iy = ty * 16 + (l32 & 15);
+        cy = p.rope_cos[iy];
+        sy = p.rope_sin[iy];
+      }
+      (void)ty;
+      const int ix = tx * 16 + (l32 & 15);
       const float cx = p.rope_cos[ix], sx = p.rope_sin[ix];
       const float p0 = __shfl_xor(v0, 16), p1 = __shfl_xor(v1, 16);
       v0 = (l32 < 16) ? (v0 * cy - p0 * sy) : (v0 * cy + p0 * sy);
