@@ -86,54 +86,65 @@ def cpu_model():
 
 
 def cpu_baseline():
-    """Reference CPU path stand-in: the oracle with the reference's literal
-    loops (linear i-j-k, attention scores/softmax/PV), one thread, on a bounded
-    sample -- one config-0 ViT-L block (768 tokens) -- extrapolated to a
-    384x512 pair by algorithmic FLOPs."""
+    """Reference CPU path stand-in, timed on the host: the oracle's literal
+    reference loops (Linear i-j-k, attention scores / softmax / PV, conv
+    kh-kw-ic) on one full config-2 pair (384x512, seed-0 weights and images)
+    on all host threads -- the measured figure -- and one config-0 ViT-L block
+    on 1 thread and on all threads; the block's thread ratio extrapolates the
+    measured pair to one thread (labelled as extrapolated)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
 
     import gsplat_hip as G
     import pyoracle as O
 
-    cfg = G.default_config(enc_depth=1, dec_depth=1, dpt_hooks=[0, 1, 1, 1])
-    w = {}
-    for i, (n, s, k) in enumerate(G.weight_inventory(cfg)):
-        if n.startswith("enc_blocks.0."):
-            w[n] = G.weight_values(cfg, i, int(np.prod(s))).reshape(s)
-    x = G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)
+    cfg = G.default_config()
+    w = G.seeded_weights(cfg, 0)
+    n = 3 * 384 * 512
+    i1 = G.seed_uniform(0, "view1", n).reshape(1, 3, 384, 512)
+    i2 = G.seed_uniform(0, "view2", n).reshape(1, 3, 384, 512)
     O.set_naive(True)
     O.set_threads(0)
     threads_all = O.lib().orc_get_threads()
+    print(f"[cpu] one 384x512 pair through the literal loops on {threads_all} threads",
+          file=sys.stderr, flush=True)
+    t0 = time.perf_counter()
+    out = O.mastr_pair(cfg.as_dict(), w, i1, i2)
+    dt_pair = time.perf_counter() - t0
+    assert all(np.isfinite(v).all() for v in out.values())
+    print(f"[cpu] pair: {dt_pair:.1f} s", file=sys.stderr, flush=True)
+    x = G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)
     t0 = time.perf_counter()
     y_all = O.encoder_block(cfg.as_dict(), w, "enc_blocks.0", x, 24, 32)
     dt_all = time.perf_counter() - t0
     O.set_threads(1)
     t0 = time.perf_counter()
     y_one = O.encoder_block(cfg.as_dict(), w, "enc_blocks.0", x, 24, 32)
-    dt = time.perf_counter() - t0
+    dt_one = time.perf_counter() - t0
     O.set_naive(False)
     O.set_threads(0)
     assert np.array_equal(y_one, y_all)  # threads split output rows only: same bits
-    ratio = PAIR_GFLOP_384x512 / BLOCK_GFLOP
-    s_per_pair = dt * ratio
+    thread_ratio = dt_one / dt_all
+    s_pair_1t = dt_pair * thread_ratio
     return {
-        "value": 1.0 / s_per_pair,
+        "value": 1.0 / dt_pair,
         "unit": "pairs/s",
-        "cores": 1,
+        "cores": threads_all,
         "kind": "port",
-        "value_all_cores": 1.0 / (dt_all * ratio),
-        "cores_all": threads_all,
+        "measured_s_per_pair": round(dt_pair, 2),
+        "value_1_thread_extrapolated": 1.0 / s_pair_1t,
+        "s_per_pair_1_thread_extrapolated": round(s_pair_1t, 1),
         "cpu": cpu_model(),
         "logical_cpus": os.cpu_count(),
-        "extrapolation": f"measured config-0 block x {ratio:.1f} (2037.2 / 21.74 GFLOP) to one "
-                         "384x512 pair",
-        "sample": (f"one config-0 ViT-L block (768 tokens, 21.74 GFLOP) through the oracle's "
-                   f"literal reference loops: {dt:.2f} s on 1 thread, {dt_all:.3f} s on "
-                   f"{threads_all} threads (bit-identical); extrapolated x{ratio:.1f} by FLOPs "
-                   f"to one 384x512 pair ({s_per_pair:.0f} s/pair on 1 thread, "
-                   f"{dt_all * ratio:.1f} s/pair on {threads_all}); host CPU: {cpu_model()}, "
-                   f"{os.cpu_count()} logical CPUs"),
+        "extrapolation": f"1-thread figure only: the measured {threads_all}-thread pair x the "
+                         f"config-0 block's measured 1-thread / {threads_all}-thread time ratio "
+                         f"({dt_one:.2f} s / {dt_all:.3f} s = {thread_ratio:.2f})",
+        "sample": (f"one full config-2 pair (two 3x384x512 U(-1,1) images, seed-0 N(0,0.02) "
+                   f"weights: ViT-L encoder x2, ViT-B decoder, 2 DPT heads, 2 descriptor heads, "
+                   f"2037.2 GFLOP) through the oracle's literal reference loops: {dt_pair:.1f} s "
+                   f"measured on {threads_all} threads; one config-0 ViT-L block (21.74 GFLOP): "
+                   f"{dt_one:.2f} s on 1 thread, {dt_all:.3f} s on {threads_all} threads "
+                   f"(bit-identical); host CPU: {cpu_model()}, {os.cpu_count()} logical CPUs"),
     }
 
 
@@ -440,12 +451,9 @@ def secondary(args):
         cfg = G.default_config()
         m = G.Mastr(cfg, 1)
         m.init_seeded(0)
-        if args.workload == "block":
-            x0 = torch.from_numpy(G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)).cuda()
-            x = torch.empty_like(x0)
-            def fn():
-                x.copy_(x0)
-                m.encoder_block(0, x, 1, stream=stream)
+        if args.workload == "block":  # applied in place, step after step
+            x = torch.from_numpy(G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)).cuda()
+            fn = lambda: m.encoder_block(0, x, 1, stream=stream)
             gflop, what = BLOCK_GFLOP, "config 0: one ViT-L block, 768 tokens, batch 1"
         else:
             img = torch.from_numpy(G.seed_uniform(0, "view1", 3 * 384 * 512).reshape(1, 3, 384, 512)).cuda()
@@ -536,14 +544,70 @@ def secondary(args):
     return out
 
 
-def fp32x6_variant(args, B, H, W):
-    """The same workload in precision 2 (fp32 GEMMs, convolutions and attention
-    on bf16 matrix cores through exact three-term splits), timed
-    the same way. Reported beside the fp32 headline, never as `value`."""
+# Algorithmic work of one 512x512 pair (GFLOP), same FLOP model.
+PAIR_GFLOP_512x512 = 2806.4
+ENCODER_GFLOP = 523.0
+PREC_NAME = {0: "fp32", 1: "bf16", 2: "fp32x6"}
+PREC_DTYPE = {0: "f32", 1: "bf16-in/f32-acc", 2: "f32 (bf16x6 split products, f32 acc)"}
+# the MFMA ceiling each precision's flops are counted against
+PREC_PEAK = {0: MFMA_FP32_PEAK_TFLOPS, 1: MFMA_BF16_PEAK_TFLOPS, 2: MFMA_X6_PEAK_TFLOPS}
+
+
+def _event_timed(fn, steps, warmup):
+    """Seconds per step: W warm-up steps, then K steps between two HIP events
+    on the current (launch) stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / 1e3 / steps
+
+
+def _profiled(fn, steps):
+    """Per-kernel launch records (the library's own HIP event pairs) over
+    `steps` further steps."""
     import torch
 
     import gsplat_hip as G
-    cfg = G.default_config(img_h=H, img_w=W, precision=2)
+    G.profile_begin()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return G.profile_end()
+
+
+def _mfma_summary(prof, steps):
+    """GEMM+attention fraction of the MFMA peak (each kernel against its own
+    precision's ceiling) and the dominant kernel's rate."""
+    mm = [(k, v) for k, v in prof.items() if k.startswith(("gemm", "attn"))]
+    fl = sum(v["flops"] for k, v in mm)
+    cap = sum(v["ms"] * 1e-3 * kernel_peak(k) * 1e12 for k, v in mm)
+    dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
+    tf = dom["flops"] / (dom["ms"] * 1e-3) / 1e12 if dom["flops"] else 0.0
+    return {"gemm_attn_frac_mfma_peak": round(fl / cap, 4) if cap else None,
+            "dominant_kernel": dom_name,
+            "dominant_launches_per_step": dom["launches"] // steps,
+            "dominant_tflops": round(tf, 2),
+            "dominant_frac": round(tf / kernel_peak(dom_name), 4)}
+
+
+def pair_variant(args, config, precision, pairs=None):
+    """A pair workload besides the headline, timed the same way (W warm-up
+    steps, then K steps between events on the launch stream, inputs resident
+    in HBM, outputs left there), then K instrumented steps for the per-kernel
+    figures. Reported in `variants`, never as `value`."""
+    import torch
+
+    import gsplat_hip as G
+    wl = CONFIGS[config]
+    B, H, W = pairs or wl["pairs"], wl["img_h"], wl["img_w"]
+    cfg = G.default_config(img_h=H, img_w=W, precision=precision)
     m = G.Mastr(cfg, B)
     m.init_seeded(0)
     n = B * 3 * H * W
@@ -552,22 +616,65 @@ def fp32x6_variant(args, B, H, W):
     outs = [torch.empty(B, H, W, c, device="cuda") for c in (3, 1, cfg.desc_dim) * 2]
     stream = torch.cuda.current_stream().cuda_stream
     step = lambda: m.pair(img1, img2, B, *outs, stream=stream)
-    sec = _timed(step, args.steps, args.warmup)
-    G.profile_begin()
-    step()
-    torch.cuda.synchronize()
-    prof = G.profile_end()
+    sec = _event_timed(step, args.steps, args.warmup)
+    prof = _profiled(step, args.steps)
     m.close()
-    dom_name, dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
-    tf = dom["flops"] / (dom["ms"] * 1e-3) / 1e12
-    return {"value": round(B / sec, 3), "ms_per_step": round(sec * 1e3, 3),
-            "dtype": "f32 (bf16x6 split products, f32 acc)",
-            "precision_note": "error against an fp64 product at or below the fp32 MFMA "
-                              "kernel's (tests/test_gpu_ops.py::"
-                              "test_linear_f32x6_accuracy_vs_fp64); pair outputs at the fp32 "
-                              "parity bar (test_gpu_model.py::test_tiny_pair_f32x6_parity)",
-            "dominant_kernel": dom_name, "dominant_tflops_fp32_equivalent": round(tf, 2),
-            "dominant_frac_of_bf16_peak_div6": round(tf / MFMA_X6_PEAK_TFLOPS, 4)}
+    del m, img1, img2, outs
+    torch.cuda.empty_cache()
+    gflop = (PAIR_GFLOP_384x512 if H * W == 384 * 512 else PAIR_GFLOP_512x512) * B
+    peak = PREC_PEAK[precision]
+    return {"workload": f"config {config}: {B} pair{'s' if B > 1 else ''} at 3x{H}x{W}, "
+                        f"{PREC_NAME[precision]}",
+            "value": round(B / sec, 3), "unit": "pairs/s", "ms_per_step": round(sec * 1e3, 3),
+            "steps": args.steps, "warmup": args.warmup, "dtype": PREC_DTYPE[precision],
+            "wall_tflops": round(gflop / sec / 1e3, 2),
+            "wall_frac_of_peak": round(gflop / sec / 1e3 / peak, 4), "peak_tflops": peak,
+            **_mfma_summary(prof, args.steps)}
+
+
+def batch1_variant(args, which):
+    """Config 0 (one ViT-L block on 768 tokens, applied in place step after
+    step) or config 1 (the ViT-L encoder on one 384x512 image): wall time per
+    step and its fraction of the fp32 MFMA peak. These launches are small, so
+    more steps are timed (10x K for the block, 2x K for the encoder)."""
+    import torch
+
+    import gsplat_hip as G
+    cfg = G.default_config()
+    m = G.Mastr(cfg, 1)
+    m.init_seeded(0)
+    stream = torch.cuda.current_stream().cuda_stream
+    if which == "block":
+        x = torch.from_numpy(G.seed_normal(0, "tokens", 768 * 1024).reshape(1, 768, 1024)).cuda()
+        fn = lambda: m.encoder_block(0, x, 1, stream=stream)
+        gflop, steps = BLOCK_GFLOP, 10 * args.steps
+        what = "config 0: one ViT-L encoder block, 768 tokens (24x32 grid), batch 1, fp32"
+    else:
+        img = torch.from_numpy(G.seed_uniform(0, "view1", 3 * 384 * 512).reshape(1, 3, 384, 512)).cuda()
+        enc = torch.empty(1, 768, 1024, device="cuda")
+        fn = lambda: m.encoder(img, 1, enc, stream=stream)
+        gflop, steps = ENCODER_GFLOP, 2 * args.steps
+        what = "config 1: ViT-L encoder (patch embed, 24 blocks, enc_norm), one 3x384x512 image, fp32"
+    sec = _event_timed(fn, steps, args.warmup)
+    prof = _profiled(fn, steps)
+    m.close()
+    return {"workload": what, "value": round(sec * 1e3, 4), "unit": "ms", "higher_is_better": False,
+            "steps": steps, "warmup": args.warmup, "dtype": "f32",
+            "wall_tflops": round(gflop / sec / 1e3, 2),
+            "wall_frac_of_peak": round(gflop / sec / 1e3 / MFMA_FP32_PEAK_TFLOPS, 4),
+            "peak_tflops": MFMA_FP32_PEAK_TFLOPS, **_mfma_summary(prof, steps)}
+
+
+def fp32x6_variant(args, B, H, W):
+    """The headline workload in precision 2 (fp32 GEMMs, convolutions and
+    attention on bf16 matrix cores through exact three-term splits), timed
+    the same way. Reported beside the fp32 headline, never as `value`."""
+    v = pair_variant(args, 3 if H * W == 384 * 512 else 4, 2, pairs=B)
+    v["precision_note"] = ("error against an fp64 product at or below the fp32 MFMA kernel's "
+                           "(tests/test_gpu_ops.py::test_linear_f32x6_accuracy_vs_fp64); pairs 0 "
+                           "and 15 of this workload at the fp32 parity bar against the oracle "
+                           "(tests/test_gpu_model.py::test_config3_16_pairs[2])")
+    return v
 
 
 def main():
@@ -772,8 +879,19 @@ def main():
             tf = v["flops"] / (v["ms"] * 1e-3) / 1e12 if v["flops"] else 0.0
             print(f"{v['ms']:9.3f} ms {v['launches']:4d}x {tf:7.1f} TF/s  {k}", file=sys.stderr)
     m.close()
+    del m, img1, img2, outs
+    torch.cuda.empty_cache()
     if args.precision == "fp32" and not (args.graph or args.e2e or args.no_variants):
-        out["variants"] = {"fp32x6": fp32x6_variant(args, B, H, W)}
+        # the other configurations of the baseline, each timed the same way
+        # in this run: the fp32x6 form of this workload, config 4 in the
+        # bf16 variant at its own size, and the batch-1 configs 0 / 1 / 2
+        out["variants"] = {
+            "fp32x6": fp32x6_variant(args, B, H, W),
+            "config4_bf16": pair_variant(args, 4, 1),
+            "config2_fp32": pair_variant(args, 2, 0),
+            "config1_fp32": batch1_variant(args, "encoder"),
+            "config0_fp32": batch1_variant(args, "block"),
+        }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

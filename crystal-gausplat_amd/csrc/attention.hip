@@ -357,10 +357,12 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
 
   floatx16 o0 = {}, o1 = {};
   float m_run = -INFINITY, l_run = 0.f;
-  // rank-one operands of the reference subtraction: k slot 0 of the lanes
-  // with hl == 0 holds 1 (key side) and -m_run (query side)
+  // rank-one operands of the reference subtraction: k slots 0 and 1 of the
+  // lanes with hl == 0 hold 1 (key side) and the two bf16 terms -m_hi, -m_lo
+  // of -m_run (query side)
   bf16x8 ones_k0 = {}, negm_k0 = {};
   ones_k0[0] = hl == 0 ? (__bf16)1.0f : (__bf16)0.0f;
+  ones_k0[1] = ones_k0[0];
 
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
   fx4 rk[4], rv[4];     // fp32 inputs: 4 values each
@@ -432,11 +434,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
     for (int sub = 0; sub < KT / 32; ++sub) {
       const int sb = kbase + sub * 32;
       if (sb >= Nkv) break;
-      // Scores relative to the running reference m_run, which is kept
-      // bf16-exact: a fifth MFMA adds the rank-one product ones x (-m_run)
-      // (k slot 0 of the halves with hl == 0), so the exponentials take the
-      // accumulators as they are and the VALU, which bounds this kernel,
-      // does no subtraction.
+      // Scores relative to the running reference m_run = m_hi + m_lo, a sum
+      // of two bf16 values: a fifth MFMA adds the rank-one product
+      // ones x (-m_hi, -m_lo) (k slots 0 and 1 of the halves with hl == 0),
+      // so the exponentials take the accumulators as they are and the VALU,
+      // which bounds this kernel, does no subtraction. Two terms keep m_run
+      // within 2^-16 of the running maximum at any magnitude (one bf16 term
+      // would miss it by up to half a bf16 ulp: 128 at |m| = 2^15, enough to
+      // overflow exp2).
       floatx16 s = {};
       const __bf16* kr = &Ks[sub * 32 + l32][hl * 8];
 #pragma unroll
@@ -457,13 +462,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
       mb = fmaxf(mb, __shfl_xor(mb, 32));  // block maximum relative to m_run (0 at first)
       // Lazy rescaling: the reference maximum m_run only moves (and O, l
       // are rescaled) when some query of the wave sees a score more than
-      // 2^8 above it, so exp2(s - m_run) <= 2^8 (and a bf16 rounding) and
-      // the rescale multiplies are skipped for most blocks (the first block
+      // 2^8 above it, so exp2(s - m_run) <= 2^8 (to m_run's 2^-16 relative
+      // residual) and the rescale multiplies are skipped for most blocks (the first block
       // always moves it from -inf). O / l is unchanged by the choice of
       // reference.
       if (__any(m_run == -INFINITY || mb > 8.0f)) {
         const float m_base = m_run == -INFINITY ? 0.f : m_run;
-        const float m_new = (float)(__bf16)fmaxf(m_run, m_base + mb);
+        const float m_t = fmaxf(m_run, m_base + mb);
+        const __bf16 m_hi = (__bf16)m_t;
+        const __bf16 m_lo = (__bf16)(m_t - (float)m_hi);
+        const float m_new = (float)m_hi + (float)m_lo;
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
         l_run *= alpha;
 #pragma unroll
@@ -475,7 +483,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_bf16_kernel(AttnBatch batch, 
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[r] -= shift;
         m_run = m_new;
-        negm_k0[0] = hl == 0 ? (__bf16)(-m_new) : (__bf16)0.0f;
+        negm_k0[0] = hl == 0 ? -m_hi : (__bf16)0.0f;
+        negm_k0[1] = hl == 0 ? -m_lo : (__bf16)0.0f;
       }
       float ps = 0.f;
 #pragma unroll
@@ -734,6 +743,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_x6_kernel(AttnBatch batch, in
 bool aligned16(const void* ptr) { return ((uintptr_t)ptr & 15) == 0; }
 
 }  // namespace
+
+int64_t attention_split_elems(const AttnBatch& bt, int prec) {
+  const AttnArgs& a0 = bt.g[0];
+  if (prec == 1 || a0.B <= 0 || a0.H <= 0 || a0.Nq <= 0 || a0.Nkv < 2 * KT) return 0;
+  const int64_t units = (int64_t)a0.H * a0.B * bt.ngroups;
+  const int64_t qtiles = (a0.Nq + QT - 1) / QT;
+  if (bt.kv_split == 0 && units * qtiles >= 3 * kAttnCUs) return 0;
+  const int64_t ranges = (a0.Nkv + KT - 1) / KT;  // the most a split uses
+  return units * a0.Nq * ranges * 66;
+}
 
 int launch_attention(const AttnBatch& bt, hipStream_t s, int prec) {
   const bool bf16 = prec == 1, x6 = prec == 2;

@@ -438,7 +438,7 @@ __global__ __launch_bounds__(256) void gemm_splitk_reduce_ln(GemmBatch batch) {
         /* padded taps read A[lc4..] (in bounds) and are zeroed by GS_FIX_A */           \
         const int kk = k0_ / p.cCin;                                                     \
         const int ic0 = k0_ - kk * p.cCin;                                               \
-        const int kh = kk / p.ck, kw = kk - kh * p.ck;                                   \
+        const int kh = kk / p.ckw, kw = kk - kh * p.ckw;                                   \
         const int64_t toff = ((int64_t)kh * p.cW + kw) * p.cCin + ic0;                   \
         const int ih = ohs[i] + kh, iw = ows[i] + kw;                                    \
         const bool ok = aval[i] && (unsigned)ih < (unsigned)p.cH && (unsigned)iw < (unsigned)p.cW; \
@@ -882,7 +882,7 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16_kernel(GemmBatch batch) {
       const __bf16* Ah = (const __bf16*)p.A;                                     \
       const int kk = (K0) / p.cCin;                                              \
       const int ic0 = (K0) - kk * p.cCin;                                        \
-      const int kh = kk / p.ck, kw = kk - kh * p.ck;                             \
+      const int kh = kk / p.ckw, kw = kk - kh * p.ckw;                             \
       const int64_t toff = ((int64_t)kh * p.cW + kw) * p.cCin + ic0;             \
       _Pragma("unroll") for (int i = 0; i < 4; ++i) {                            \
         const int ih = ohs[i] + kh, iw = ows[i] + kw;                            \
@@ -1029,7 +1029,10 @@ static_assert(4 * 32 * W2_SS * 4 <= 2 * W2_STAGE * 2, "w2 epilogue stages fit th
 // accumulators, then through the wave's LDS stage (32 rows of W2_SS floats) so
 // that residuals are read and outputs written as 16-byte row segments (16
 // lanes per 64-column row). Same per-element operations and order as
-// gemm_epilogue_t; no scatter form (checked on the host). Measured in the
+// gemm_epilogue_t. The scatter form (ConvT / pixel shuffle) stores 4-column
+// segments, each inside one output pixel: the host admits it only with
+// sc_C % 4 == 0, sc_Cout % 4 == 0 and no residual, RoPE or dual store
+// (row_epi_ok). Measured in the
 // model: the per-element form of the shared epilogue (64-bit addresses, 4-byte
 // accesses) took this kernel from ~1100 TFLOP/s (main loop) to 360-565.
 template <bool ROPE>
@@ -1285,7 +1288,7 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
       tic += W2K;                                                                            \
       if (tic == p.cCin) {                                                                   \
         tic = 0;                                                                             \
-        if (++tkw == p.ck) {                                                                 \
+        if (++tkw == p.ckw) {                                                                 \
           tkw = 0;                                                                           \
           ++tkh;                                                                             \
         }                                                                                    \
@@ -1464,7 +1467,7 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
       tic += FK;                                                                             \
       if (tic == p.cCin) {                                                                   \
         tic = 0;                                                                             \
-        if (++tkw == p.ck) {                                                                 \
+        if (++tkw == p.ckw) {                                                                 \
           tkw = 0;                                                                           \
           ++tkh;                                                                             \
         }                                                                                    \
@@ -1752,9 +1755,10 @@ int check_gemm(const GemmArgs& a, int aload, int blayout, bool bf16) {
                "gemm: bad concat operand");
   if (aload == A_CONV || aload == A_CONV_H) {
     GS_REQUIRE(a.cCin % BK == 0, "conv: Cin must be a multiple of 32");
-    GS_REQUIRE(a.K == a.ck * a.ck * a.cCin, "conv: K != k*k*Cin");
+    GS_REQUIRE(a.ck > 0 && a.ckw > 0 && a.cs > 0 && a.cp >= 0, "conv: bad kernel geometry");
+    GS_REQUIRE(a.K == a.ck * a.ckw * a.cCin, "conv: K != kh*kw*Cin");
     GS_REQUIRE(a.cHo == (a.cH + 2 * a.cp - a.ck) / a.cs + 1 &&
-                   a.cWo == (a.cW + 2 * a.cp - a.ck) / a.cs + 1,
+                   a.cWo == (a.cW + 2 * a.cp - a.ckw) / a.cs + 1,
                "conv: output grid mismatch");
     GS_REQUIRE(a.M % (a.cHo * a.cWo) == 0, "conv: M must be images*Ho*Wo");
   }

@@ -89,10 +89,10 @@ struct GemmArgs {
   const float* A2;  // concat second source
   int64_t lda2;
   int32_t K1;       // concat split (multiple of 32)
-  // implicit convolution (A_CONV): input [Bimg, cH, cW, cCin], kernel ck,
-  // stride cs, pad cp, output grid cHo x cWo; K = ck*ck*cCin, k index =
-  // (kh*ck + kw)*cCin + ic
-  int32_t cH, cW, cCin, ck, cs, cp, cHo, cWo;
+  // implicit convolution (A_CONV): input [Bimg, cH, cW, cCin], kernel
+  // ck (rows) x ckw (columns), stride cs, pad cp, output grid cHo x cWo;
+  // K = ck*ckw*cCin, k index = (kh*ckw + kw)*cCin + ic
+  int32_t cH, cW, cCin, ck, cs, cp, cHo, cWo, ckw;
   const float* B;   // NT: B[n*ldb + k]; NN: B[k*ldb + n]
   const void* Bh;   // bf16 copy of B (NT layout, same ldb) for the bf16 kernels;
                     // for the bf16x6 kernel with bh_plane > 0: plane 0 of the
@@ -184,6 +184,9 @@ struct AttnBatch {
 // prec: 0 fp32 MFMA, 1 bf16-input, 2 bf16x6 split products (fp32 accuracy;
 // launches that split the keys use the fp32 kernel)
 int launch_attention(const AttnBatch& b, hipStream_t s, int prec = 0);
+// Scratch (floats) that lets launch_attention split the keys of this launch
+// as far as its cost model may choose; 0 when the launch never splits.
+int64_t attention_split_elems(const AttnBatch& b, int prec = 0);
 
 // ---- LayerNorm -----------------------------------------------------------------
 struct LnArgs {
@@ -257,16 +260,17 @@ int launch_collect_points(const float* pts, const float* conf, int64_t n, float 
 int launch_fill_i64(int64_t* p, int64_t n, int64_t v, hipStream_t s);
 
 // General-shape kernels of the op-level entry points (general.hip): attention
-// for any head_dim in [1, 128] and any strides / alignment; LayerNorm of any
+// for any head_dim >= 1 and any strides / alignment; LayerNorm of any
 // width and alignment; a zero-padded, possibly transposing copy
 // dst[r*cp + c] = c < cols ? src[r*s_row + c*s_col] : 0; and a convolution
-// weight (OIHW layout 0 / OHWI layout 1) to OHWI with Cin padded to cp.
+// weight (OIHW layout 0 / OHWI layout 1) of kh x kw taps to OHWI with Cin
+// padded to cp.
 int launch_attention_general(const AttnArgs& a, int32_t hd, hipStream_t s);
 int launch_layernorm_rows(const LnArgs& a, hipStream_t s);
 int launch_stage(const float* src, int64_t rows, int64_t cols, int64_t s_row, int64_t s_col,
                  float* dst, int64_t cp, hipStream_t s);
-int launch_conv_weight_stage(const float* w, int32_t Cout, int32_t Cin, int32_t k, int32_t layout,
-                             int32_t cp, float* out, hipStream_t s);
+int launch_conv_weight_stage(const float* w, int32_t Cout, int32_t Cin, int32_t kh, int32_t kw,
+                             int32_t layout, int32_t cp, float* out, hipStream_t s);
 
 // Configuration of a MASt3R context created by gs_hip_mastr_create.
 const ::gs_mastr_config* mastr_ctx_config(void* ctx);

@@ -697,6 +697,7 @@ int conv(Ctx& c, const Heads& hs, const std::string& suffix, const float* const 
     a.cW = W_;
     a.cCin = Cin;
     a.ck = k;
+    a.ckw = k;
     a.cs = stride;
     a.cp = pad;
     a.cHo = Ho;

@@ -45,21 +45,26 @@ int64_t round_up(int64_t v, int64_t m) { return (v + m - 1) / m * m; }
 // Split-K / key-split partials of an op-level call whose launch would leave
 // most CUs idle (fewer than ~432 workgroups): up to 16 partial tiles per
 // output, capped at 64 MB (the launchers pick a smaller split that fits).
+// A split keeps at least 4 K steps of 32 per range, so K below 256 never
+// splits and reserves nothing.
 constexpr int64_t kOpSplitCapBytes = (int64_t)64 << 20;
-int64_t gemm_split_bytes(int64_t M, int64_t N, int ngroups = 1) {
+int64_t gemm_split_bytes(int64_t M, int64_t N, int64_t K, int ngroups = 1) {
   const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128) * ngroups;
-  if (tiles >= 432) return 0;
+  if (tiles >= 432 || K / 32 < 8) return 0;
   return std::min<int64_t>(16 * M * N * 4 * ngroups, kOpSplitCapBytes);
 }
 
-// RoPE tables [512][16] per base, uploaded once.
+// RoPE tables [512][16] per (device, base), uploaded once per device.
 std::mutex g_rope_mu;
-std::map<float, std::pair<float*, float*>> g_rope;
+std::map<std::pair<int, float>, std::pair<float*, float*>> g_rope;
 constexpr int kRopeMaxPos = 512;
 
 int rope_tables(float base, const float** c, const float** s) {
+  int dev = 0;
+  GS_CHECK_HIP(hipGetDevice(&dev));
   std::lock_guard<std::mutex> lk(g_rope_mu);
-  auto it = g_rope.find(base);
+  const std::pair<int, float> key(dev, base);
+  auto it = g_rope.find(key);
   if (it == g_rope.end()) {
     std::vector<float> hc(kRopeMaxPos * 16), hs(kRopeMaxPos * 16);
     rope_table_host(kRopeMaxPos, base, hc.data(), hs.data());
@@ -69,7 +74,7 @@ int rope_tables(float base, const float** c, const float** s) {
     GS_CHECK_HIP(hipMalloc(&ds, hs.size() * sizeof(float)));
     GS_CHECK_HIP(hipMemcpy(dc, hc.data(), hc.size() * sizeof(float), hipMemcpyHostToDevice));
     GS_CHECK_HIP(hipMemcpy(ds, hs.data(), hs.size() * sizeof(float), hipMemcpyHostToDevice));
-    it = g_rope.emplace(base, std::make_pair(dc, ds)).first;
+    it = g_rope.emplace(key, std::make_pair(dc, ds)).first;
   }
   *c = it->second.first;
   *s = it->second.second;
@@ -123,7 +128,7 @@ int32_t gs_hip_linear(const float* x, const float* w, const float* b, float* y, 
   const int64_t xh_bytes = bf16 ? M * Kp * 2 : 0;
   const int64_t off_b = round_up(a_bytes, 256), off_h = round_up(off_b + b_bytes, 256);
   const int64_t off_xh = round_up(off_h + h_bytes, 256);
-  const int64_t off_p = round_up(off_xh + xh_bytes, 256), p_bytes = gemm_split_bytes(M, N);
+  const int64_t off_p = round_up(off_xh + xh_bytes, 256), p_bytes = gemm_split_bytes(M, N, Kp);
   StreamScratch ws;
   if (off_p + p_bytes > 0) {
     int rc = ws.alloc((size_t)(off_p + p_bytes), s);
@@ -203,38 +208,51 @@ int32_t gs_hip_layernorm(const float* x, const float* gamma, const float* beta, 
   return launch_layernorm_rows(a, pick(stream));
 }
 
-int32_t gs_hip_attention(const float* q, const float* k, const float* v, float* o, int32_t B,
-                         int32_t H, int32_t Nq, int32_t Nkv, int32_t head_dim, float scale,
-                         int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
-                         int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, int64_t o_sb,
-                         int64_t o_sh, int64_t o_sn, void* stream) {
+int32_t gs_hip_attention_prec(const float* q, const float* k, const float* v, float* o,
+                              int32_t B, int32_t H, int32_t Nq, int32_t Nkv, int32_t head_dim,
+                              float scale, int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb,
+                              int64_t k_sh, int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                              int64_t o_sb, int64_t o_sh, int64_t o_sn, int32_t precision,
+                              void* stream) {
   if (ensure_device()) return -2;
-  GS_REQUIRE(head_dim >= 1 && head_dim <= 128, "attention: head_dim must be in [1, 128]");
+  GS_REQUIRE(head_dim >= 1, "attention: head_dim must be >= 1");
+  GS_REQUIRE(precision >= 0 && precision <= 2, "attention: precision must be 0, 1 or 2");
   const AttnArgs a{q,    k,    v,    o,    q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb,
                    v_sh, v_sn, o_sb, o_sh, o_sn, B,    H,    Nq,   Nkv,  scale};
-  // head_dim 64 with 16-byte aligned rows runs on the MFMA flash kernel; other
-  // head dims and layouts on the general kernel (one wavefront per query)
+  // head_dim 64 with 16-byte aligned rows runs on the MFMA flash kernels;
+  // other head dims and layouts on the general fp32 kernel (one wavefront per
+  // query), which the bf16 variants do not have
   bool mfma = head_dim == 64 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   const int64_t st[12] = {q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn};
   for (int j = 0; j < 12; ++j) mfma = mfma && st[j] % 4 == 0;
+  GS_REQUIRE(mfma || precision == 0,
+             "attention: the bf16 and bf16x6 variants need head_dim 64 and 16-byte aligned rows "
+             "(pointers and strides multiples of 4 floats)");
   if (!mfma) return launch_attention_general(a, head_dim, pick(stream));
   AttnBatch bt;
   bt.g[0] = a;
   bt.ngroups = 1;
-  // launches of fewer than ~432 workgroups split the keys into ranges merged
-  // in order; their partial states (64 outputs + max + sum per query and
-  // range) live in stream-ordered scratch
-  const int64_t units = (int64_t)B * H, qtiles = (Nq + 127) / 128;
+  // launches that leave most CUs idle split the keys into ranges merged in
+  // order; their partial states live in stream-ordered scratch sized by the
+  // launcher's own rule (zero when this launch cannot split)
   StreamScratch ws;
-  if (units * qtiles < 432 && Nkv >= 128 && B > 0 && H > 0 && Nq > 0) {
-    const int64_t ranges = std::min<int64_t>((Nkv + 63) / 64, (432 + units * qtiles - 1) / (units * qtiles));
-    const int64_t elems = std::min<int64_t>(units * Nq * ranges * 66, kOpSplitCapBytes / 4) / 4 * 4;
+  const int64_t elems = std::min<int64_t>(attention_split_elems(bt, precision), kOpSplitCapBytes / 4) / 4 * 4;
+  if (elems > 0) {
     int rc = ws.alloc((size_t)elems * 4, pick(stream));
     if (rc) return rc;
     bt.part_ws = (float*)ws.get();
     bt.part_ws_elems = elems;
   }
-  return launch_attention(bt, pick(stream));
+  return launch_attention(bt, pick(stream), precision);
+}
+
+int32_t gs_hip_attention(const float* q, const float* k, const float* v, float* o, int32_t B,
+                         int32_t H, int32_t Nq, int32_t Nkv, int32_t head_dim, float scale,
+                         int64_t q_sb, int64_t q_sh, int64_t q_sn, int64_t k_sb, int64_t k_sh,
+                         int64_t k_sn, int64_t v_sb, int64_t v_sh, int64_t v_sn, int64_t o_sb,
+                         int64_t o_sh, int64_t o_sn, void* stream) {
+  return gs_hip_attention_prec(q, k, v, o, B, H, Nq, Nkv, head_dim, scale, q_sb, q_sh, q_sn, k_sb,
+                               k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn, 0, stream);
 }
 
 int32_t gs_hip_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld, int32_t grid_w,
@@ -250,19 +268,20 @@ int32_t gs_hip_rope2d(float* t, int32_t B, int32_t N, int32_t H, int64_t ld, int
   return launch_rope2d(t, B, N, H, ld, grid_w, c, s, pick(stream));
 }
 
-int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t Cin,
-                      const float* w, const float* b, float* y, int32_t Cout, int32_t k,
-                      int32_t stride, int32_t pad, int32_t w_layout, int32_t flags,
-                      const float* residual, void* stream) {
+int32_t gs_hip_conv2d_hw(const float* x, int32_t B, int32_t H, int32_t W, int32_t Cin,
+                         const float* w, const float* b, float* y, int32_t Cout, int32_t kh,
+                         int32_t kw, int32_t stride, int32_t pad, int32_t w_layout, int32_t flags,
+                         const float* residual, void* stream) {
   if (ensure_device()) return -2;
   GS_REQUIRE(w_layout == 0 || w_layout == 1, "conv2d: w_layout must be 0 or 1");
-  GS_REQUIRE(k > 0 && stride > 0 && pad >= 0 && B >= 0 && H > 0 && W > 0 && Cin > 0 && Cout > 0,
+  GS_REQUIRE(kh > 0 && kw > 0 && stride > 0 && pad >= 0 && B >= 0 && H > 0 && W > 0 && Cin > 0 &&
+                 Cout > 0,
              "conv2d: bad geometry");
   GS_REQUIRE(x && w && y, "conv2d: null operand");
   GS_REQUIRE((flags & ~(GS_CONV_RELU_IN | GS_CONV_RELU_OUT | GS_CONV_F32X6)) == 0,
              "conv2d: unknown flag");
-  const int32_t Ho = (H + 2 * pad - k) / stride + 1, Wo = (W + 2 * pad - k) / stride + 1;
-  GS_REQUIRE(H + 2 * pad >= k && W + 2 * pad >= k && Ho > 0 && Wo > 0, "conv2d: empty output");
+  GS_REQUIRE(H + 2 * pad >= kh && W + 2 * pad >= kw, "conv2d: empty output");
+  const int32_t Ho = (H + 2 * pad - kh) / stride + 1, Wo = (W + 2 * pad - kw) / stride + 1;
   GS_REQUIRE((int64_t)B * Ho * Wo <= INT32_MAX, "conv2d: too many output pixels");
   GS_REQUIRE((int64_t)B * H * W <= INT32_MAX, "conv2d: too many input pixels");
   if (B == 0) return 0;
@@ -273,11 +292,11 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   // other channel counts run on copies zero-padded to a multiple of 32.
   const int32_t Cp = (int32_t)round_up(Cin, 32);
   const bool stage_x = Cp != Cin || !aligned16(x);
-  const bool stage_w = Cp != Cin || !aligned16(w) || (w_layout == 0 && k > 1);
+  const bool stage_w = Cp != Cin || !aligned16(w) || (w_layout == 0 && kh * kw > 1);
   const int64_t x_bytes = stage_x ? (int64_t)B * H * W * Cp * 4 : 0;
-  const int64_t w_bytes = stage_w ? (int64_t)Cout * k * k * Cp * 4 : 0;
+  const int64_t w_bytes = stage_w ? (int64_t)Cout * kh * kw * Cp * 4 : 0;
   const int64_t off_w = round_up(x_bytes, 256), off_p = round_up(off_w + w_bytes, 256);
-  const int64_t p_bytes = gemm_split_bytes((int64_t)B * Ho * Wo, Cout);
+  const int64_t p_bytes = gemm_split_bytes((int64_t)B * Ho * Wo, Cout, (int64_t)kh * kw * Cp);
   StreamScratch ws;
   if (off_p + p_bytes > 0) {
     int rc = ws.alloc((size_t)(off_p + p_bytes), s);
@@ -293,24 +312,25 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   }
   if (stage_w) {
     float* wsb = (float*)(ws.get() + off_w);
-    int rc = launch_conv_weight_stage(w, Cout, Cin, k, w_layout, Cp, wsb, s);
+    int rc = launch_conv_weight_stage(w, Cout, Cin, kh, kw, w_layout, Cp, wsb, s);
     if (rc) return rc;
     wk = wsb;
   }
   GemmArgs a = blank_args();
-  const bool pointwise = (k == 1 && stride == 1 && pad == 0);
+  const bool pointwise = (kh == 1 && kw == 1 && stride == 1 && pad == 0);
   a.A = xk;
   a.lda = Cp;
   a.cH = H;
   a.cW = W;
   a.cCin = Cp;
-  a.ck = k;
+  a.ck = kh;
+  a.ckw = kw;
   a.cs = stride;
   a.cp = pad;
   a.cHo = Ho;
   a.cWo = Wo;
   a.B = wk;
-  a.ldb = (int64_t)k * k * Cp;
+  a.ldb = (int64_t)kh * kw * Cp;
   a.C = y;
   a.ldc = Cout;
   a.bias = b;
@@ -318,7 +338,7 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
   a.ldr1 = Cout;
   a.M = (int32_t)((int64_t)B * Ho * Wo);
   a.N = Cout;
-  a.K = k * k * Cp;
+  a.K = kh * kw * Cp;
   a.flags = (b ? EPI_BIAS : 0) | ((flags & GS_CONV_RELU_OUT) ? EPI_RELU : 0) |
             (residual ? EPI_RES1 : 0);
   GemmBatch bt;
@@ -330,6 +350,14 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t C
     bt.part_ws_elems = p_bytes / 4;
   }
   return launch_gemm(bt, pointwise ? A_PLAIN : A_CONV, B_NT, (flags & GS_CONV_RELU_IN) != 0, s);
+}
+
+int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t Cin,
+                      const float* w, const float* b, float* y, int32_t Cout, int32_t k,
+                      int32_t stride, int32_t pad, int32_t w_layout, int32_t flags,
+                      const float* residual, void* stream) {
+  return gs_hip_conv2d_hw(x, B, H, W, Cin, w, b, y, Cout, k, k, stride, pad, w_layout, flags,
+                          residual, stream);
 }
 
 int32_t gs_hip_conv_transpose(const float* x, int32_t B, int32_t H, int32_t W, int32_t Cin,

@@ -292,6 +292,7 @@ extern "C" int32_t gs_hip_collect_points_noalloc(const float* pts, const float* 
                                                  float threshold, float* out_pts,
                                                  float* out_conf, int64_t capacity,
                                                  int64_t* count, void* stream) {
+  if (gs::ensure_device()) return -2;
   GS_REQUIRE(n >= 0 && n <= gs::kNoAllocMaxPoints,
              "collect_points_noalloc: n must be in [0, 2^27] (134217728 points)");
   int64_t* sc = nullptr;

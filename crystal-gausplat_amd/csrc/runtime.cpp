@@ -117,6 +117,16 @@ int32_t gs_init_device(void) {
     strncpy(g_name, prop.name, sizeof(g_name) - 1);
     g_name[sizeof(g_name) - 1] = 0;
   }
+  // Op-level calls take their scratch from the device's default memory pool
+  // (hipMallocAsync / hipFreeAsync). With the pool's default release
+  // threshold of 0 every synchronisation hands the memory back to the driver,
+  // so a caller that synchronises after each op would pay a fresh allocation
+  // on every call; keep up to 256 MB cached in the pool instead.
+  hipMemPool_t pool;
+  if (hipDeviceGetDefaultMemPool(&pool, g_device) == hipSuccess) {
+    uint64_t keep = (uint64_t)256 << 20;
+    (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+  }
   // Default-priority, non-blocking stream.
   if (hipStreamCreateWithFlags(&g_stream, hipStreamNonBlocking) != hipSuccess) {
     set_error("gs_init_device: stream creation failed");

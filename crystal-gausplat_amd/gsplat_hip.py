@@ -74,11 +74,17 @@ _SIGS = [
     ("gs_hip_layernorm", C.c_int32, [vp, vp, vp, vp, C.c_int64, C.c_int32, C.c_float, vp]),
     ("gs_hip_attention", C.c_int32, [vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                      C.c_int32, C.c_float] + [C.c_int64] * 12 + [vp]),
+    ("gs_hip_attention_prec", C.c_int32, [vp, vp, vp, vp, C.c_int32, C.c_int32, C.c_int32,
+                                          C.c_int32, C.c_int32, C.c_float] + [C.c_int64] * 12 +
+     [C.c_int32, vp]),
     ("gs_hip_rope2d", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int64, C.c_int32,
                                   C.c_float, vp]),
     ("gs_hip_conv2d", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp, vp,
                                   C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                   C.c_int32, vp, vp]),
+    ("gs_hip_conv2d_hw", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp, vp,
+                                     C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                     C.c_int32, C.c_int32, vp, vp]),
     ("gs_hip_conv_transpose", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp,
                                           vp, C.c_int32, C.c_int32, vp]),
     ("gs_hip_upsample2x", C.c_int32, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp]),
@@ -218,13 +224,22 @@ def weight_values(cfg, i, n, seed=0, bias_std=0.0, ln_std=0.0):
 
 
 def seeded_weights(cfg, seed=0, bias_std=0.0, ln_std=0.0):
-    """dict name -> float32 numpy array (shaped) of the seeded weights."""
+    """dict name -> float32 numpy array (shaped) of the seeded weights. The
+    generator is counter-based (each tensor depends only on its name and the
+    seed), so the tensors are generated on a few host threads (the ctypes
+    call releases the GIL) with the same values as one at a time."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+
     import numpy as np
-    w = {}
-    for i, (name, shape, kind) in enumerate(weight_inventory(cfg)):
-        n = int(np.prod(shape))
-        w[name] = weight_values(cfg, i, n, seed, bias_std, ln_std).reshape(shape)
-    return w
+    inv = weight_inventory(cfg)
+
+    def one(i):
+        name, shape, kind = inv[i]
+        return name, weight_values(cfg, i, int(np.prod(shape)), seed, bias_std,
+                                   ln_std).reshape(shape)
+    with ThreadPoolExecutor(max_workers=max(1, min(8, os.cpu_count() or 1))) as ex:
+        return dict(ex.map(one, range(len(inv))))
 
 
 def seed_normal(seed, name, n, mean=0.0, std=1.0):

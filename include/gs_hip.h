@@ -143,11 +143,12 @@ int32_t gs_hip_layernorm(const float* x, const float* gamma, const float* beta,
 
 /* NN::GPUOps.fused_attention (src/nn/gpu_ops.cr:200-227) generalised to
  * cross-attention with Nq != Nkv (the CPU path's semantics,
- * src/nn/attention.cr:215-325). head_dim in [1, 128] (the reference takes any;
- * its own spec runs 16, spec/nn/attention_spec.cr:49-58): head_dim 64 with
- * 16-byte aligned rows (pointers and strides multiples of 4 floats) runs on
- * the MFMA flash kernel, anything else on a general kernel (one wavefront
- * per query, K / V tiles in LDS, expf softmax). Element (b,h,n,d) of q
+ * src/nn/attention.cr:215-325). Any head_dim >= 1, as the reference (its own
+ * spec runs 16, spec/nn/attention_spec.cr:49-58): head_dim 64 with 16-byte
+ * aligned rows (pointers and strides multiples of 4 floats) runs on the MFMA
+ * flash kernel, anything else on a general kernel (one wavefront per query,
+ * K / V tiles in LDS, expf softmax; head dims beyond 128 in chunks of 128,
+ * accumulated in the output row). Element (b,h,n,d) of q
  * is at q[b*q_sb + h*q_sh + n*q_sn + d]; likewise for k, v, o. The
  * reference layout [B,H,N,64] is q_sb = H*N*64, q_sh = N*64, q_sn = 64;
  * token-major [B,N,H*64] is q_sb = N*H*64, q_sh = 64, q_sn = H*64. */
@@ -159,6 +160,22 @@ int32_t gs_hip_attention(const float* q, const float* k, const float* v,
                          int64_t v_sb, int64_t v_sh, int64_t v_sn,
                          int64_t o_sb, int64_t o_sh, int64_t o_sn,
                          void* stream);
+
+/* gs_hip_attention with a choice of arithmetic, as gs_hip_linear's epilogue
+ * flags choose it for the linears: precision 0 = fp32 MFMA (gs_hip_attention
+ * itself); 1 = the bf16-input / fp32-accumulate variant (q, k, v and the
+ * softmax probabilities rounded to bf16; the north star's optional bf16
+ * path); 2 = fp32 through bf16x6 split products (fp32-level accuracy;
+ * launches that split the keys run the fp32 kernel). Precisions 1 and 2 need
+ * head_dim 64 and 16-byte aligned rows. */
+int32_t gs_hip_attention_prec(const float* q, const float* k, const float* v,
+                              float* o, int32_t B, int32_t H, int32_t Nq,
+                              int32_t Nkv, int32_t head_dim, float scale,
+                              int64_t q_sb, int64_t q_sh, int64_t q_sn,
+                              int64_t k_sb, int64_t k_sh, int64_t k_sn,
+                              int64_t v_sb, int64_t v_sh, int64_t v_sn,
+                              int64_t o_sb, int64_t o_sh, int64_t o_sn,
+                              int32_t precision, void* stream);
 
 /* 2D RoPE in place on t [B, N, ld], columns [0, H*64): per 64-wide head,
  * dims [0,32) rotate by the token's row y and [32,64) by its column x
@@ -184,6 +201,18 @@ int32_t gs_hip_conv2d(const float* x, int32_t B, int32_t H, int32_t W,
                       int32_t Cout, int32_t k, int32_t stride, int32_t pad,
                       int32_t w_layout, int32_t flags, const float* residual,
                       void* stream);
+
+/* gs_hip_conv2d with a kh x kw kernel: conv2d_forward reads kernel_h and
+ * kernel_w from the weight's shape separately (src/nn/gpu_ops.cr:491-495),
+ * with one stride and one padding for both axes. w OIHW [Cout,Cin,kh,kw]
+ * (w_layout 0) or OHWI [Cout,kh,kw,Cin] (w_layout 1); output
+ * Ho = (H + 2 pad - kh) / stride + 1, Wo = (W + 2 pad - kw) / stride + 1.
+ * gs_hip_conv2d(..., k, ...) is gs_hip_conv2d_hw(..., k, k, ...). */
+int32_t gs_hip_conv2d_hw(const float* x, int32_t B, int32_t H, int32_t W,
+                         int32_t Cin, const float* w, const float* b, float* y,
+                         int32_t Cout, int32_t kh, int32_t kw, int32_t stride,
+                         int32_t pad, int32_t w_layout, int32_t flags,
+                         const float* residual, void* stream);
 
 /* ConvTranspose2d with kernel == stride (no padding), NHWC, weight in the
  * PyTorch layout [Cin, Cout, k, k]. Cin % 32 == 0, Cout % 32 == 0. */

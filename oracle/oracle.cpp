@@ -41,7 +41,9 @@
  *   orc_unfold          src/nn/vit.cr:38-83 ((c,i,j) patch order). Pinned:
  *                       equals torch unfold / a 16x16 stride-16 conv.
  *   orc_conv2d          src/mastr/decoder_v2.cr:281-344 (NHWC x OIHW, sum order
- *                       kh, kw, ic, OOB taps skipped, bias added after).
+ *                       kh, kw, ic, OOB taps skipped, bias added after);
+ *                       orc_conv2d_hw takes kh x kw kernels as the GPU
+ *                       conv2d_forward does (nn.metal:1098-1164, same order).
  *                       Pinned: 6-loop naive variant (bit-equal), 1x1 conv ==
  *                       linear, delta kernel identity, torch conv2d.
  *   orc_conv_transpose  no reference kernel (ConvTranspose k == s of the DPT
@@ -88,7 +90,10 @@
  *                       (1 memory = the other view's decoder_embed output,
  *                       fixed; 2 norm_y dropped; 3 no RoPE on the
  *                       cross-attention q / k; 4 local-feature concat
- *                       dec | enc; 5 norm2 / norm3 roles swapped) so the
+ *                       dec | enc; 5 norm2 / norm3 roles swapped; 6 the
+ *                       DPT hooks after layers dpt_hooks[1] and dpt_hooks[2]
+ *                       swapped; 7 each DPT head fed the other view's hooks;
+ *                       8 the last DPT hook taken before dec_norm) so the
  *                       tests can show that each pin above fails on it.
  */
 #include "oracle.h"
@@ -443,25 +448,29 @@ extern "C" void orc_unfold(const float* img, int32_t B, int32_t C, int32_t H,
                   img[(((int64_t)b * C + c) * H + y * p + i) * W + x * p + j];
 }
 
-extern "C" void orc_conv2d_naive(const float* x, int32_t B, int32_t H, int32_t W,
-                                 int32_t Cin, const float* w, const float* b,
-                                 int32_t Cout, int32_t k, int32_t stride,
-                                 int32_t pad, float* y) {
-  const int32_t Ho = (H + 2 * pad - k) / stride + 1;
-  const int32_t Wo = (W + 2 * pad - k) / stride + 1;
+/* kh x kw kernel: the reference's GPU conv2d_forward takes kernel_h and
+ * kernel_w separately with the CPU path's (kh, kw, ic) order
+ * (src/metal/kernels/nn.metal:1098-1164); the CPU path itself
+ * (src/mastr/decoder_v2.cr:281-344) is the square case. */
+extern "C" void orc_conv2d_hw_naive(const float* x, int32_t B, int32_t H, int32_t W,
+                                    int32_t Cin, const float* w, const float* b,
+                                    int32_t Cout, int32_t KH, int32_t KW, int32_t stride,
+                                    int32_t pad, float* y) {
+  const int32_t Ho = (H + 2 * pad - KH) / stride + 1;
+  const int32_t Wo = (W + 2 * pad - KW) / stride + 1;
 #pragma omp parallel for schedule(static) collapse(2)
   for (int32_t bb = 0; bb < B; ++bb)
     for (int32_t oh = 0; oh < Ho; ++oh)
       for (int32_t ow = 0; ow < Wo; ++ow)
         for (int32_t oc = 0; oc < Cout; ++oc) {
           float sum = 0.0f;
-          for (int32_t kh = 0; kh < k; ++kh)
-            for (int32_t kw = 0; kw < k; ++kw) {
+          for (int32_t kh = 0; kh < KH; ++kh)
+            for (int32_t kw = 0; kw < KW; ++kw) {
               const int32_t ih = oh * stride + kh - pad, iw = ow * stride + kw - pad;
               if (ih < 0 || ih >= H || iw < 0 || iw >= W) continue;
               for (int32_t ic = 0; ic < Cin; ++ic)
                 sum += x[(((int64_t)bb * H + ih) * W + iw) * Cin + ic] *
-                       w[(((int64_t)oc * Cin + ic) * k + kh) * k + kw];
+                       w[(((int64_t)oc * Cin + ic) * KH + kh) * KW + kw];
             }
           float* r = &y[(((int64_t)bb * Ho + oh) * Wo + ow) * Cout + oc];
           *r = sum;
@@ -469,23 +478,30 @@ extern "C" void orc_conv2d_naive(const float* x, int32_t B, int32_t H, int32_t W
         }
 }
 
+extern "C" void orc_conv2d_naive(const float* x, int32_t B, int32_t H, int32_t W,
+                                 int32_t Cin, const float* w, const float* b,
+                                 int32_t Cout, int32_t k, int32_t stride,
+                                 int32_t pad, float* y) {
+  orc_conv2d_hw_naive(x, B, H, W, Cin, w, b, Cout, k, k, stride, pad, y);
+}
+
 /* Same per-element sequence as orc_conv2d_naive, vectorised across output
  * channels and blocked over output pixels. */
-extern "C" void orc_conv2d(const float* x, int32_t B, int32_t H, int32_t W,
-                           int32_t Cin, const float* w, const float* b,
-                           int32_t Cout, int32_t k, int32_t stride, int32_t pad,
-                           float* y) {
-  const int32_t Ho = (H + 2 * pad - k) / stride + 1;
-  const int32_t Wo = (W + 2 * pad - k) / stride + 1;
+extern "C" void orc_conv2d_hw(const float* x, int32_t B, int32_t H, int32_t W,
+                              int32_t Cin, const float* w, const float* b,
+                              int32_t Cout, int32_t KH, int32_t KW, int32_t stride,
+                              int32_t pad, float* y) {
+  const int32_t Ho = (H + 2 * pad - KH) / stride + 1;
+  const int32_t Wo = (W + 2 * pad - KW) / stride + 1;
   /* wt[kh][kw][ic][oc] */
-  std::vector<float> wt((size_t)k * k * Cin * Cout);
+  std::vector<float> wt((size_t)KH * KW * Cin * Cout);
 #pragma omp parallel for schedule(static)
   for (int32_t oc = 0; oc < Cout; ++oc)
     for (int32_t ic = 0; ic < Cin; ++ic)
-      for (int32_t kh = 0; kh < k; ++kh)
-        for (int32_t kw = 0; kw < k; ++kw)
-          wt[(((size_t)kh * k + kw) * Cin + ic) * Cout + oc] =
-              w[(((size_t)oc * Cin + ic) * k + kh) * k + kw];
+      for (int32_t kh = 0; kh < KH; ++kh)
+        for (int32_t kw = 0; kw < KW; ++kw)
+          wt[(((size_t)kh * KW + kw) * Cin + ic) * Cout + oc] =
+              w[(((size_t)oc * Cin + ic) * KH + kh) * KW + kw];
   const int PB = 16, CB = 64;
   const int64_t npix = (int64_t)B * Ho * Wo;
   const int64_t npb = (npix + PB - 1) / PB;
@@ -506,9 +522,9 @@ extern "C" void orc_conv2d(const float* x, int32_t B, int32_t H, int32_t W,
         pbb[q] = (int32_t)(pix / ((int64_t)Wo * Ho));
         for (int c = 0; c < CB; ++c) acc[q][c] = 0.0f;
       }
-      for (int32_t kh = 0; kh < k; ++kh)
-        for (int32_t kw = 0; kw < k; ++kw) {
-          const float* wk = &wt[(((size_t)kh * k + kw) * Cin) * Cout + oc0];
+      for (int32_t kh = 0; kh < KH; ++kh)
+        for (int32_t kw = 0; kw < KW; ++kw) {
+          const float* wk = &wt[(((size_t)kh * KW + kw) * Cin) * Cout + oc0];
           for (int q = 0; q < np; ++q) {
             const int32_t ih = poh[q] * stride + kh - pad;
             const int32_t iw = pow_[q] * stride + kw - pad;
@@ -531,6 +547,13 @@ extern "C" void orc_conv2d(const float* x, int32_t B, int32_t H, int32_t W,
       }
     }
   }
+}
+
+extern "C" void orc_conv2d(const float* x, int32_t B, int32_t H, int32_t W,
+                           int32_t Cin, const float* w, const float* b,
+                           int32_t Cout, int32_t k, int32_t stride, int32_t pad,
+                           float* y) {
+  orc_conv2d_hw(x, B, H, W, Cin, w, b, Cout, k, k, stride, pad, y);
 }
 
 extern "C" void orc_conv_transpose(const float* x, int32_t B, int32_t H,
@@ -1003,6 +1026,16 @@ void pair(const Ctx& c, const float* img1, const float* img2, int32_t B,
   if (!pts1 && !pts2 && !desc1 && !desc2) return;
   const float* h1[4] = {e1.data(), hook1[1].data(), hook1[2].data(), f1.data()};
   const float* h2[4] = {e2.data(), hook2[1].data(), hook2[2].data(), f2.data()};
+  if (g_mut == 6) { /* planted: the two intermediate decoder hooks swapped */
+    std::swap(h1[1], h1[2]);
+    std::swap(h2[1], h2[2]);
+  }
+  if (g_mut == 8) { /* planted: last hook before dec_norm */
+    h1[3] = d1.data();
+    h2[3] = d2.data();
+  }
+  if (g_mut == 7) /* planted: each head fed the other view's hooks */
+    for (int i = 0; i < 4; ++i) std::swap(h1[i], h2[i]);
   if (cf->composite == 1) {
     if (pts1) dpt_ref_head(c, "downstream_head1", f1.data(), B, gh, gw, pts1, conf1);
     if (pts2) dpt_ref_head(c, "downstream_head2", f2.data(), B, gh, gw, pts2, conf2);

@@ -86,6 +86,15 @@ void orc_conv2d(const float* x, int32_t B, int32_t H, int32_t W, int32_t Cin,
 void orc_conv2d_naive(const float* x, int32_t B, int32_t H, int32_t W,
                       int32_t Cin, const float* w, const float* b, int32_t Cout,
                       int32_t k, int32_t stride, int32_t pad, float* y);
+/* kh x kw kernels: OIHW w [Cout,Cin,kh,kw], Ho = (H+2pad-kh)/stride+1,
+ * Wo = (W+2pad-kw)/stride+1; orc_conv2d is the kh == kw == k case. */
+void orc_conv2d_hw(const float* x, int32_t B, int32_t H, int32_t W, int32_t Cin,
+                   const float* w, const float* b, int32_t Cout, int32_t kh,
+                   int32_t kw, int32_t stride, int32_t pad, float* y);
+void orc_conv2d_hw_naive(const float* x, int32_t B, int32_t H, int32_t W,
+                         int32_t Cin, const float* w, const float* b,
+                         int32_t Cout, int32_t kh, int32_t kw, int32_t stride,
+                         int32_t pad, float* y);
 /* ConvTranspose2d with kernel == stride, no padding. w [Cin,Cout,k,k]. */
 void orc_conv_transpose(const float* x, int32_t B, int32_t H, int32_t W,
                         int32_t Cin, const float* w, const float* b,

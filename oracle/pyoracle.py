@@ -61,6 +61,10 @@ _SIGS = [
                           C.c_int32, C.c_int32, C.c_int32, vp]),
     ("orc_conv2d_naive", None, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp, C.c_int32,
                                 C.c_int32, C.c_int32, C.c_int32, vp]),
+    ("orc_conv2d_hw", None, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp, C.c_int32,
+                             C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]),
+    ("orc_conv2d_hw_naive", None, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp,
+                                   C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]),
     ("orc_conv_transpose", None, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp, vp,
                                   C.c_int32, C.c_int32, vp]),
     ("orc_upsample2x", None, [vp, C.c_int32, C.c_int32, C.c_int32, C.c_int32, vp]),
@@ -87,6 +91,7 @@ _SIGS = [
 
 # Planted composition mistakes of orc_set_mutation (tests only).
 MUT_MEMORY_FIXED, MUT_NO_NORM_Y, MUT_NO_CROSS_ROPE, MUT_CONCAT_SWAP, MUT_NORM_ROLES = 1, 2, 3, 4, 5
+MUT_HOOKS_SWAPPED, MUT_HEADS_CROSSED, MUT_HOOK3_PRE_NORM = 6, 7, 8
 
 _lib = None
 
@@ -200,16 +205,20 @@ def unfold(img, p):
 
 
 def conv2d(x, w, b=None, stride=1, pad=0, naive=False):
-    """x NHWC, w OIHW."""
+    """x NHWC, w OIHW [Cout, Cin, kh, kw] (kh != kw allowed)."""
     x, w = f32(x), f32(w)
     B, H, W, Cin = x.shape
-    Cout, _, k, _ = w.shape
-    Ho = (H + 2 * pad - k) // stride + 1
-    Wo = (W + 2 * pad - k) // stride + 1
+    Cout, _, kh, kw = w.shape
+    Ho = (H + 2 * pad - kh) // stride + 1
+    Wo = (W + 2 * pad - kw) // stride + 1
     y = np.empty((B, Ho, Wo, Cout), np.float32)
-    fn = lib().orc_conv2d_naive if naive else lib().orc_conv2d
-    fn(_p(x), B, H, W, Cin, _p(w), _p(f32(b) if b is not None else None), Cout, k, stride, pad,
-       _p(y))
+    bp = _p(f32(b) if b is not None else None)
+    if kh == kw:
+        fn = lib().orc_conv2d_naive if naive else lib().orc_conv2d
+        fn(_p(x), B, H, W, Cin, _p(w), bp, Cout, kh, stride, pad, _p(y))
+    else:
+        fn = lib().orc_conv2d_hw_naive if naive else lib().orc_conv2d_hw
+        fn(_p(x), B, H, W, Cin, _p(w), bp, Cout, kh, kw, stride, pad, _p(y))
     return y
 
 

@@ -305,12 +305,16 @@ def test_config4_batch_invariance_32_pairs():
     m.close()
 
 
-def test_config3_16_pairs():
+@pytest.mark.parametrize("precision", [0, 2])
+def test_config3_16_pairs(precision):
     """Config 3, the benchmark workload: 16 pairs at 384x512 in one launch
-    sequence, fp32. Pairs 0 and 15 against the oracle at the fp32 bar
-    (1e-3 relative + 1e-4 absolute per element); a rerun is bit-identical."""
-    case("config3 16 pairs")
-    cfg = G.default_config()
+    sequence, fp32 (precision 0) and fp32 through bf16x6 split products
+    (precision 2, the bench line's fp32x6 variant). Pairs 0 and 15 against
+    the oracle at the fp32 bar (1e-3 relative + 1e-4 absolute per element);
+    a rerun is bit-identical. The oracle outputs are cached across the two
+    precisions (same weights, same images)."""
+    case(f"config3 16 pairs precision {precision}")
+    cfg = G.default_config(precision=precision)
     B = 16
     n = 3 * 384 * 512
     i1 = G.seed_uniform(0, "view1", B * n).reshape(B, 3, 384, 512)
@@ -327,7 +331,8 @@ def test_config3_16_pairs():
     w = weights_for(cfg)
     for b in (0, B - 1):
         ref = oracle_pair(cfg, w, i1[b:b + 1], i2[b:b + 1])
-        check_pair({k: v[b:b + 1] for k, v in full.items()}, ref, f"config3 pair {b}")
+        check_pair({k: v[b:b + 1] for k, v in full.items()}, ref,
+                   f"config3 precision {precision} pair {b}")
 
 
 def test_config4_bf16_32_pairs():

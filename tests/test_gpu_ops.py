@@ -313,10 +313,17 @@ def test_attention_bhnd_layout_and_large_scores():
 def test_attention_rejects_bad_head_dim():
     case("attention validation")
     x = empty(64)
-    for hd in (0, 129):
+    for hd in (0, -3):
         rc = L().gs_hip_attention(p(x), p(x), p(x), p(x), 1, 1, 1, 1, hd, 0.1, *([0] * 12),
                                   stream())
         assert rc != 0 and b"head_dim" in L().gs_hip_last_error()
+    # the bf16 variants exist for the MFMA shapes only (head_dim 64, aligned rows)
+    rc = L().gs_hip_attention_prec(p(x), p(x), p(x), p(x), 1, 1, 1, 1, 32, 0.1, *([32] * 12), 1,
+                                   stream())
+    assert rc != 0 and b"head_dim 64" in L().gs_hip_last_error()
+    rc = L().gs_hip_attention_prec(p(x), p(x), p(x), p(x), 1, 1, 1, 1, 64, 0.1, *([64] * 12), 3,
+                                   stream())
+    assert rc != 0 and b"precision" in L().gs_hip_last_error()
 
 
 # GPUOps.fused_attention takes any head_dim (src/nn/gpu_ops.cr:200-227); the
@@ -328,7 +335,10 @@ def test_attention_rejects_bad_head_dim():
 @pytest.mark.parametrize("B,H,Nq,Nkv,hd,layout", [
     (2, 4, 8, 8, 16, "tok"), (1, 2, 4, 6, 16, "tok"), (2, 4, 32, 32, 16, "tok"),
     (1, 3, 100, 77, 32, "tok"), (2, 2, 70, 70, 128, "tok"), (2, 2, 33, 65, 80, "bhnd"),
-    (1, 2, 45, 200, 1, "bhnd"), (2, 3, 50, 40, 64, "odd")])
+    (1, 2, 45, 200, 1, "bhnd"), (2, 3, 50, 40, 64, "odd"),
+    # head dims beyond 128: chunks of 128, the last one ragged
+    (1, 2, 37, 70, 129, "tok"), (2, 1, 20, 33, 200, "bhnd"), (1, 2, 9, 40, 256, "odd"),
+    (1, 1, 5, 64, 1000, "tok")])
 def test_attention_any_head_dim(B, H, Nq, Nkv, hd, layout):
     case(f"attention any head_dim B={B} H={H} Nq={Nq} Nkv={Nkv} hd={hd} {layout}")
     scale = float(np.float32(1.0 / np.sqrt(hd)))
@@ -356,6 +366,74 @@ def test_attention_any_head_dim(B, H, Nq, Nkv, hd, layout):
         got = got[:B * Nq * D].reshape(B, Nq, D)[..., :H * hd].reshape(B, Nq, H, hd)
         got = got.transpose(0, 2, 1, 3)
     assert_close(got, ref, name="attention any head_dim")
+
+
+def bf16_round(a):
+    """float32 -> nearest bf16 (ties to even), returned as float32."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    r = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return r.astype(np.uint32).view(np.float32)
+
+
+def attn_prec_call(q, k, v, B, H, N, Nkv, prec, scale=0.125):
+    """[B, H, N, 64] operands through gs_hip_attention_prec."""
+    o = empty(B, H, N, 64)
+    st = lambda n: (H * n * 64, n * 64, 64)
+    G.check(L().gs_hip_attention_prec(p(dev(q)), p(dev(k)), p(dev(v)), p(o), B, H, N, Nkv, 64,
+                                      scale, *st(N), *st(Nkv), *st(Nkv), *st(N), prec, stream()))
+    return host(o)
+
+
+@pytest.mark.parametrize("B,H,N,Nkv", [(2, 4, 300, 257), (4, 16, 768, 768)])
+def test_attention_precision_variants(B, H, N, Nkv):
+    """gs_hip_attention_prec: the bf16-input variant against the fp32 oracle
+    at the bf16 bar (2e-2 norm-wise), the bf16x6 variant at the fp32 bar."""
+    case(f"attention precision variants B={B} H={H} N={N} Nkv={Nkv}")
+    q, k, v = rnd(B, H, N, 64, scale=1.5), rnd(B, H, Nkv, 64, scale=1.5), rnd(B, H, Nkv, 64)
+    ref = O.sdpa(q, k, v, 0.125)
+    got1 = attn_prec_call(q, k, v, B, H, N, Nkv, 1)
+    rel, worst, p999 = assert_close_bf16(got1, ref, name="attention bf16")
+    print(f"attention bf16: rel {rel:.2e} worst {worst:.2e} p99.9 elementwise {p999:.2e}")
+    assert rel > 1e-5  # it really ran in bf16
+    assert_close(attn_prec_call(q, k, v, B, H, N, Nkv, 2), ref, name="attention bf16x6")
+    np.testing.assert_array_equal(attn_prec_call(q, k, v, B, H, N, Nkv, 0),
+                                  attn_prec_call(q, k, v, B, H, N, Nkv, 0))
+
+
+@pytest.mark.parametrize("kind", ["random", "all_negative"])
+def test_attention_bf16_huge_logits(kind):
+    """The bf16 flash kernel with scores of order 2^16 in its log2 domain,
+    where one bf16 term for the running maximum would be off by up to 256
+    and overflow (or underflow) exp2. The output is finite and matches a
+    float64 softmax of the same bf16-rounded operands (q pre-scaled by
+    scale * log2(e) before rounding, as the kernel does), at the bf16 bar."""
+    case(f"attention bf16 huge logits {kind}")
+    B, H, N, Nkv = 1, 2, 128, 192
+    rng = np.random.default_rng(7)
+    if kind == "random":
+        q = (rng.standard_normal((B, H, N, 64)) * 128).astype(np.float32)
+        k = (rng.standard_normal((B, H, Nkv, 64)) * 128).astype(np.float32)
+    else:  # every score near -2^16: keys opposite to a shared query direction
+        u = rng.standard_normal(64)
+        u /= np.linalg.norm(u)
+        q = np.broadcast_to(u * 700.0, (B, H, N, 64)).astype(np.float32)
+        q = q + rng.standard_normal((B, H, N, 64)).astype(np.float32)
+        k = np.broadcast_to(-u * 700.0, (B, H, Nkv, 64)).astype(np.float32)
+        k = k + rng.standard_normal((B, H, Nkv, 64)).astype(np.float32) * 2
+    v = rng.standard_normal((B, H, Nkv, 64)).astype(np.float32)
+    qs = np.float32(0.125 * 1.4426950408889634)
+    q2 = bf16_round(q * qs).astype(np.float64)
+    k2, v2 = bf16_round(k).astype(np.float64), bf16_round(v).astype(np.float64)
+    s2 = q2 @ k2.transpose(0, 1, 3, 2)
+    mx = s2.max(-1, keepdims=True)
+    assert np.abs(mx).max() > 2.0 ** 15  # the regime this test is for
+    pr = np.exp2(s2 - mx)
+    ref = (pr @ v2) / pr.sum(-1, keepdims=True)
+    got = attn_prec_call(q, k, v, B, H, N, Nkv, 1)
+    assert np.isfinite(got).all(), "non-finite bf16 attention output"
+    rel, worst, _ = assert_close_bf16(got, ref, name=f"attention bf16 huge logits {kind}")
+    print(f"attention bf16 huge logits {kind}: |m| max {np.abs(mx).max():.0f}, rel {rel:.2e}, "
+          f"worst {worst:.2e}")
 
 
 @pytest.mark.parametrize("B,N,Nkv,E,H", [(2, 8, 8, 64, 4), (1, 4, 6, 32, 2)])
@@ -514,6 +592,32 @@ def test_conv2d_any_channels(B, H, W, Cin, Cout, k, s, pd, layout, flags, res):
     G.check(L().gs_hip_conv2d(p(dev(x)), B, H, W, Cin, p(dev(wk)), p(dev(b)), p(y), Cout, k, s, pd,
                               layout, flags, p(dev(r)) if res else None, stream()))
     assert_close(host(y), ref, name="conv2d any Cin")
+
+
+# conv2d_forward reads kernel_h and kernel_w separately (src/nn/gpu_ops.cr:
+# 491-495): kh x kw kernels through gs_hip_conv2d_hw, on the register-staged
+# conv kernel, the bf16x6 kernel and (the last case: 768 tiles of 192 rows)
+# the direct-to-LDS conv kernel.
+@pytest.mark.parametrize("B,H,W,Cin,Cout,kh,kw,s,pd,layout,flags", [
+    (2, 9, 11, 32, 40, 1, 3, 1, 1, 0, 0),
+    (1, 12, 10, 64, 32, 3, 1, 2, 1, 1, G.CONV_RELU_OUT),
+    (2, 7, 13, 20, 16, 2, 5, 1, 2, 0, G.CONV_RELU_IN),
+    (1, 10, 10, 32, 64, 5, 2, 3, 0, 0, G.CONV_F32X6),
+    (1, 192, 382, 32, 256, 3, 1, 1, 1, 0, 0)])
+def test_conv2d_nonsquare_kernel(B, H, W, Cin, Cout, kh, kw, s, pd, layout, flags):
+    case(f"conv2d_hw B={B} {H}x{W} {Cin}->{Cout} k={kh}x{kw} s={s} p={pd} layout={layout} "
+         f"flags={flags}")
+    x, w, b = rnd(B, H, W, Cin), rnd(Cout, Cin, kh, kw, scale=0.1), rnd(Cout, scale=0.1)
+    Ho, Wo = (H + 2 * pd - kh) // s + 1, (W + 2 * pd - kw) // s + 1
+    ref = O.conv2d(np.maximum(x, 0) if flags & G.CONV_RELU_IN else x, w, b, s, pd)
+    if flags & G.CONV_RELU_OUT:
+        ref = np.maximum(ref, 0)
+    assert ref.shape == (B, Ho, Wo, Cout)
+    wk = w if layout == 0 else np.ascontiguousarray(w.transpose(0, 2, 3, 1))
+    y = empty(B, Ho, Wo, Cout)
+    G.check(L().gs_hip_conv2d_hw(p(dev(x)), B, H, W, Cin, p(dev(wk)), p(dev(b)), p(y), Cout, kh,
+                                 kw, s, pd, layout, flags, None, stream()))
+    assert_close(host(y), ref, name="conv2d_hw")
 
 
 def test_op_scratch_is_per_stream():

@@ -228,6 +228,20 @@ def test_conv_blocked_equals_reference_loop_and_torch(k, s, p):
     np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("kh,kw,s,p", [(1, 3, 1, 1), (3, 1, 2, 1), (2, 5, 1, 2), (5, 2, 3, 0)])
+def test_conv_nonsquare_kernel_reference_loop_and_torch(kh, kw, s, p):
+    """kh x kw kernels (the GPU conv2d_forward reads kernel_h and kernel_w
+    separately): blocked == literal loop bit for bit, and torch conv2d; a
+    transposed kernel (kw x kh) changes the output grid or the values."""
+    x, w, b = rnd(2, 9, 11, 32), rnd(24, 32, kh, kw, scale=0.1), rnd(24)
+    y = O.conv2d(x, w, b, s, p)
+    np.testing.assert_array_equal(y, O.conv2d(x, w, b, s, p, naive=True))
+    ref = F.conv2d(torch.from_numpy(x).permute(0, 3, 1, 2), torch.from_numpy(w),
+                   torch.from_numpy(b), stride=s, padding=p).permute(0, 2, 3, 1).numpy()
+    assert y.shape == ref.shape
+    np.testing.assert_allclose(y, ref, rtol=1e-4, atol=1e-5)
+
+
 def test_conv_1x1_is_linear_and_delta_kernel_is_identity():
     x, w, b = rnd(1, 5, 7, 32), rnd(24, 32, 1, 1), rnd(24)
     np.testing.assert_array_equal(O.conv2d(x, w, b),
@@ -347,24 +361,30 @@ def torch_decoder_block(x, mem, w, p, H, gw, eps, rope=True):
     return x + lin(m, p + ".mlp.fc2")
 
 
-def torch_decoder(e1, e2, w, cfg, gw):
+def torch_decoder(e1, e2, w, cfg, gw, states=False):
     """MASt3RDecoder#forward_pair (src/mastr/decoder_v2.cr:170-191) from torch
     ops: decoder_embed, then per layer l chain 1 (dec_blocks) and chain 2
     (dec_blocks2). composite 0: each chain's cross-attention memory is the
     other chain's state before layer l; composite 1: its own view's
-    decoder_embed output, fixed (176-184). Returns dec_norm of both."""
+    decoder_embed output, fixed (176-184). Returns dec_norm of both; with
+    states=True also each chain's state after every layer (index l = after
+    l layers, so index 0 is the decoder_embed output)."""
     comp = cfg.get("composite", 0)
     eps, H = cfg["ln_eps"], cfg["dec_heads"]
     rope = cfg["rope_mode"] == 1
     ln, lin = _mods(w, eps)
     d1, d2 = lin(torch.from_numpy(e1), "decoder_embed"), lin(torch.from_numpy(e2), "decoder_embed")
     m1, m2 = d1, d2
+    s1, s2 = [d1.numpy()], [d2.numpy()]
     for l in range(cfg["dec_depth"]):
         if comp == 0:
             m1, m2 = d2, d1
         d1, d2 = (torch_decoder_block(d1, m1, w, f"dec_blocks.{l}", H, gw, eps, rope),
                   torch_decoder_block(d2, m2, w, f"dec_blocks2.{l}", H, gw, eps, rope))
-    return ln(d1, "dec_norm").numpy(), ln(d2, "dec_norm").numpy()
+        s1.append(d1.numpy())
+        s2.append(d2.numpy())
+    n1, n2 = ln(d1, "dec_norm").numpy(), ln(d2, "dec_norm").numpy()
+    return (n1, n2, s1, s2) if states else (n1, n2)
 
 
 def local_features_f64(enc, dec, w, pre, gh, gw, r, C):
@@ -500,6 +520,65 @@ def test_decoder_block_pin_catches_planted_mistakes(tiny_cfg, tiny_weights, mut)
     assert max_excess(y, ref, COMP_RTOL, COMP_ATOL) > 10.0
     assert max_excess(O.decoder_block(tiny_cfg, tiny_weights, "dec_blocks.1", x, mem, gh, gw),
                       ref, COMP_RTOL, COMP_ATOL) <= 1.0  # switch is off again
+
+
+def _dpt_routing_excess(cfg, w, i1, i2, mut=0):
+    """Largest tolerance excess of the pair's full-DPT outputs (pts, conf of
+    both views, with mistake mut planted in the pair only) against each
+    view's head run standalone on hooks assembled outside the oracle's pair:
+    [the view's encoder output, its chain's torch state after layers
+    dpt_hooks[1] and dpt_hooks[2], dec_norm of its chain's last state]
+    (hook set of MASt3R's DPT adapter, src/mastr/decoder_v2.cr:502-530 for
+    the head entry). The standalone head is the float64-golden-pinned
+    O.dpt_head."""
+    gh, gw = cfg["img_h"] // cfg["patch"], cfg["img_w"] // cfg["patch"]
+    hk = cfg["dpt_hooks"]
+    e1, e2, _, _ = O.mastr_pair_taps(cfg, w, i1, i2)
+    n1, n2, s1, s2 = torch_decoder(e1, e2, w, cfg, gw, states=True)
+    with O.mutation(mut):
+        out = O.mastr_pair(cfg, w, i1, i2, desc=False)
+    worst = 0.0
+    for v, e, st, n in ((1, e1, s1, n1), (2, e2, s2, n2)):
+        hooks = [e, st[hk[1]], st[hk[2]], n]
+        pts, conf = O.dpt_head(cfg, w, f"downstream_head{v}", hooks, gh, gw)
+        worst = max(worst, max_excess(out[f"pts{v}"], pts, COMP_RTOL, COMP_ATOL),
+                    max_excess(out[f"conf{v}"], conf, COMP_RTOL, COMP_ATOL))
+    return worst
+
+
+@pytest.fixture(scope="module")
+def routing_weights(tiny_weights):
+    """The tiny weights with every DPT-head weight rescaled to unit gain
+    (std 1/sqrt(fan_in) instead of 0.02), so a change in any hook reaches
+    pts / conf at full size rather than damped below the biases. Fan-in of
+    a conv [out, in, kh, kw] is in*kh*kw; of a ConvTranspose with kernel =
+    stride [in, out, k, k] it is in (one tap per output pixel)."""
+    w = dict(tiny_weights)
+    for n, a in tiny_weights.items():
+        if ".dpt." in n and n.endswith(".weight"):
+            convt = ".act_postprocess." in n and n.endswith(".1.weight") and a.shape[2] == a.shape[3] \
+                and a.shape[2] in (2, 4)
+            fan = a.shape[0] if convt else int(np.prod(a.shape[1:]))
+            w[n] = (a / (0.02 * np.sqrt(fan))).astype(np.float32)
+    return w
+
+
+def test_pair_dpt_hook_routing(tiny_cfg, routing_weights):
+    """Inside the pair, each view's full DPT head reads its own view's
+    encoder output, its own chain's states after layers dpt_hooks[1] and
+    dpt_hooks[2], and dec_norm of its own chain's final state (non-trivial
+    LayerNorm affine, distinct weights per chain and per head)."""
+    i1, i2 = _tiny_imgs(1, 4)
+    assert _dpt_routing_excess(tiny_cfg, routing_weights, i1, i2) <= 1.0
+
+
+@pytest.mark.parametrize("mut", [O.MUT_HOOKS_SWAPPED, O.MUT_HEADS_CROSSED, O.MUT_HOOK3_PRE_NORM])
+def test_pair_dpt_hook_routing_catches_planted_mistakes(tiny_cfg, routing_weights, mut):
+    """The routing pin fails, by more than ten times its tolerance, when the
+    two intermediate hooks are swapped, when each head is fed the other
+    view's hooks, or when the last hook is taken before dec_norm."""
+    i1, i2 = _tiny_imgs(1, 4)
+    assert _dpt_routing_excess(tiny_cfg, routing_weights, i1, i2, mut) > 10.0
 
 
 def test_decoder_pair_pin_catches_fixed_memory(tiny_cfg, tiny_weights):
