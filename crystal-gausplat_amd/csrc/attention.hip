@@ -108,21 +108,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnBatch batch, int32
   floatx16 o0 = {}, o1 = {};
   float m_run = -INFINITY, l_run = 0.f;
 
-  // Tile load assignment: key rows tid/16 + 4*NW*i, fx4 column tid%16.
+  // Tile load assignment: key rows tid/16 + 4*NW*i, fx4 column tid%16. The
+  // loads go through buffer resources whose base is the tile's first key row
+  // and whose size ends at key kend - 1's 64 values, so the lane offsets stay
+  // fixed across tiles and rows at or past kend read as zero (key rows are at
+  // least HD apart and each (image, head) span is below 2 GiB, checked on the
+  // host): no 64-bit address arithmetic and no range branches per tile.
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
   fx4 rk[KP], rv[KP];
-  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
+  uint32_t kvo[KP], vvo[KP];
+#pragma unroll
+  for (int i = 0; i < KP; ++i) {
+    kvo[i] = (uint32_t)(((int64_t)(lrow + 4 * NW * i) * p.k_sn + lc4) * 4);
+    vvo[i] = (uint32_t)(((int64_t)(lrow + 4 * NW * i) * p.v_sn + lc4) * 4);
+  }
+  const int64_t kspan = ((int64_t)(kend - 1) * p.k_sn + HD) * 4;
+  const int64_t vspan = ((int64_t)(kend - 1) * p.v_sn + HD) * 4;
   auto load_kv = [&](int kbase) {
+    const int64_t ko = (int64_t)kbase * p.k_sn, vo = (int64_t)kbase * p.v_sn;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(kb + ko), (short)0, (int)(kspan - 4 * ko), 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(vb + vo), (short)0, (int)(vspan - 4 * vo), 0x00020000);
 #pragma unroll
     for (int i = 0; i < KP; ++i) {
-      const int key = kbase + lrow + 4 * NW * i;
-      if (key < kend) {
-        rk[i] = *(const fx4*)(kb + (int64_t)key * p.k_sn + lc4);
-        rv[i] = *(const fx4*)(vb + (int64_t)key * p.v_sn + lc4);
-      } else {
-        rk[i] = zero4;
-        rv[i] = zero4;
-      }
+      rk[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo[i], 0, 0));
+      rv[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vvo[i], 0, 0));
     }
   };
 
@@ -606,19 +617,30 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_x6_kernel(AttnBatch batch, in
 
   const int lrow = tid >> 4, lc4 = (tid & 15) * 4;
   fx4 rk[4], rv[4];
-  const fx4 zero4 = mk4(0.f, 0.f, 0.f, 0.f);
   // K rows lrow + 16 i; V rows 4 lrow + i, so each thread holds four
-  // consecutive keys of V and writes its transpose with 8-byte stores
-#define GS_ATT_LOAD(KB)                                                         \
-  _Pragma("unroll") for (int i = 0; i < 4; ++i) {                               \
-    const int key = (KB) + lrow + 16 * i;                                       \
-    const int kc = min(key, Nkv - 1);                                           \
-    const fx4 kk = *(const fx4*)(kb + (int64_t)kc * p.k_sn + lc4);              \
-    rk[i] = key < Nkv ? kk : zero4;                                             \
-    const int vkey = (KB) + 4 * lrow + i;                                       \
-    const int vc = min(vkey, Nkv - 1);                                          \
-    const fx4 vv = *(const fx4*)(vb + (int64_t)vc * p.v_sn + lc4);              \
-    rv[i] = vkey < Nkv ? vv : zero4;                                            \
+  // consecutive keys of V and writes its transpose with 8-byte stores. The
+  // loads go through buffer resources based at the tile's first key row and
+  // ending at the last key's 64 values (as in attn_fwd_kernel): fixed lane
+  // offsets, rows at or past Nkv read as zero.
+  uint32_t kvo[4], vvo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    kvo[i] = (uint32_t)(((int64_t)(lrow + 16 * i) * p.k_sn + lc4) * 4);
+    vvo[i] = (uint32_t)(((int64_t)(4 * lrow + i) * p.v_sn + lc4) * 4);
+  }
+  const int64_t kspan = ((int64_t)(Nkv - 1) * p.k_sn + HD) * 4;
+  const int64_t vspan = ((int64_t)(Nkv - 1) * p.v_sn + HD) * 4;
+#define GS_ATT_LOAD(KB)                                                                      \
+  {                                                                                          \
+    const int64_t ko = (int64_t)(KB) * p.k_sn, vo = (int64_t)(KB) * p.v_sn;                  \
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(                    \
+        (void*)(kb + ko), (short)0, (int)(kspan - 4 * ko), 0x00020000);                      \
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(                    \
+        (void*)(vb + vo), (short)0, (int)(vspan - 4 * vo), 0x00020000);                      \
+    _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                          \
+      rk[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(krs, kvo[i], 0, 0)); \
+      rv[i] = __builtin_bit_cast(fx4, __builtin_amdgcn_raw_buffer_load_b128(vrs, vvo[i], 0, 0)); \
+    }                                                                                        \
   }
 // product of the three-term operands A[ta] x B[tb], smallest terms first
 #define GS_X6_MM(ACC, A, B)                                                           \
@@ -774,11 +796,10 @@ int launch_attention(const AttnBatch& bt, hipStream_t s, int prec) {
                             a.v_sb, a.v_sh, a.v_sn, a.o_sb, a.o_sh, a.o_sn};
     for (int j = 0; j < 12; ++j)
       GS_REQUIRE(st[j] % 4 == 0 && st[j] >= 0, "attention: strides must be multiples of 4");
-    if (bf16) {  // the bf16 kernel's buffer-resource loads (see the kernel)
-      GS_REQUIRE(a.k_sn >= HD && a.v_sn >= HD, "attention: bf16 kernel needs key rows >= 64 apart");
-      GS_REQUIRE(((int64_t)(a.Nkv - 1) * std::max(a.k_sn, a.v_sn) + HD) * 4 < ((int64_t)1 << 31),
-                 "attention: bf16 kernel needs each (image, head) K / V span below 2 GiB");
-    }
+    // the kernels' buffer-resource K / V loads (see the kernels)
+    GS_REQUIRE(a.k_sn >= HD && a.v_sn >= HD, "attention: the MFMA kernels need key rows >= 64 apart");
+    GS_REQUIRE(((int64_t)(a.Nkv - 1) * std::max(a.k_sn, a.v_sn) + HD) * 4 < ((int64_t)1 << 31),
+               "attention: the MFMA kernels need each (image, head) K / V span below 2 GiB");
   }
   GS_REQUIRE(a0.B > 0 && a0.H > 0 && a0.Nq > 0 && a0.Nkv > 0, "attention: bad sizes");
   GS_REQUIRE((int64_t)a0.B * bt.ngroups <= 65535 && a0.H <= 65535, "attention: grid too large");

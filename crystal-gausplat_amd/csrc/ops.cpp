@@ -225,6 +225,10 @@ int32_t gs_hip_attention_prec(const float* q, const float* k, const float* v, fl
   bool mfma = head_dim == 64 && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
   const int64_t st[12] = {q_sb, q_sh, q_sn, k_sb, k_sh, k_sn, v_sb, v_sh, v_sn, o_sb, o_sh, o_sn};
   for (int j = 0; j < 12; ++j) mfma = mfma && st[j] % 4 == 0;
+  // the MFMA kernels' buffer-resource K / V loads: key rows at least 64
+  // floats apart, each (image, head) K / V span below 2 GiB
+  mfma = mfma && k_sn >= 64 && v_sn >= 64 && Nkv > 0 &&
+         ((int64_t)(Nkv - 1) * std::max(k_sn, v_sn) + 64) * 4 < ((int64_t)1 << 31);
   GS_REQUIRE(mfma || precision == 0,
              "attention: the bf16 and bf16x6 variants need head_dim 64 and 16-byte aligned rows "
              "(pointers and strides multiples of 4 floats)");
