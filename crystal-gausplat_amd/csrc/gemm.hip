@@ -1022,6 +1022,12 @@ constexpr int W2_SS = 68;                    // epilogue stage row stride (float
 // three workgroups per CU (measured at config 3: the 576-tile decoder launches
 // run 105 TFLOP/s on it against 120 on the 128 x 128 kernels)
 constexpr int kF2MinTiles = 768;
+// Long-K launches of the fp32 256 x 128 kernel run as one launch per round of
+// workgroup slots (96 tiles per XCD: 32 CUs x 3 workgroups), so every round
+// starts together, as the first round of one launch does, and its tiles stream
+// their shared A / B panels through the XCD's L2 at the same K; across the later
+// rounds of one launch the tiles drift apart and each re-fetches its panels
+constexpr int kF2PhaseMinK = 6144, kF2PhaseTiles = 96;
 static_assert(4 * 32 * W2_SS * 4 <= 2 * W2_STAGE * 2, "w2 epilogue stages fit the LDS stages");
 
 // Epilogue of one 32 x 64 block row of a gemm_bf16_w2_kernel wave (q0: columns
@@ -1191,12 +1197,16 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
 }
 
 template <int BM>
-__device__ __forceinline__ bool f2_tile(const GemmArgs& p, int& m0, int& n0) {
+__device__ __forceinline__ bool f2_tile(const GemmBatch& batch, const GemmArgs& p, int& m0,
+                                        int& n0) {
   const int tiles_m = (p.M + BM - 1) / BM, tiles_n = (p.N + W2N - 1) / W2N;
   const int ntiles = tiles_m * tiles_n;
   int bid = blockIdx.x;
   const int nb = gridDim.x;
-  if ((nb & 7) == 0) bid = (bid & 7) * (nb >> 3) + (bid >> 3);
+  if (batch.tphase_q)
+    bid = (bid & 7) * batch.tphase_q + batch.tphase_base + (bid >> 3);
+  else if ((nb & 7) == 0)
+    bid = (bid & 7) * (nb >> 3) + (bid >> 3);
   if (bid >= ntiles) return false;
   const int per_group = GROUP_M * tiles_n;
   const int gid = bid / per_group;
@@ -1235,7 +1245,7 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
   int m0, n0;
-  if (!f2_tile<BM>(p, m0, n0)) return;
+  if (!f2_tile<BM>(batch, p, m0, n0)) return;
   __shared__ __attribute__((aligned(16))) __bf16 lds[NST * BSTAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1413,7 +1423,7 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
   int m0, n0;
-  if (!f2_tile<BM>(p, m0, n0)) return;
+  if (!f2_tile<BM>(batch, p, m0, n0)) return;
   __shared__ __attribute__((aligned(16))) float lds[2 * FSTAGE];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1729,6 +1739,7 @@ std::string gemm_prof_name(const char* base, const GemmBatch& b) {
          " groups=" + std::to_string(b.ngroups);
     if (g.flags & EPI_GELU) n += " gelu";
     if (b.ksplit > 1) n += " splitk=" + std::to_string(b.ksplit);
+    if (b.tphase_q) n += " per-round";
   }
   return n;
 }
@@ -2100,6 +2111,39 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
       if (ok && tot256 >= kF2MinTiles && !w2_conv) bm = 256;
       if (ok && tot192 >= kF2MinTiles && (bm == 0 || fill(tot192) > fill(tot256))) bm = 192;
       if (bm) {
+        bool phased = bm == 256;
+        for (int i = 0; i < b.ngroups; ++i) {
+          const GemmArgs& g = b.g[i];
+          const int t = ((g.M + 255) / 256) * ((g.N + W2N - 1) / W2N);
+          phased = phased && g.K >= kF2PhaseMinK && t % 8 == 0 && t > 8 * kF2PhaseTiles;
+        }
+        if (phased) {
+          // one group and one round of tiles per launch (each launch timed on
+          // its own, with its share of the group's flops and bytes)
+          for (int i = 0; i < b.ngroups; ++i) {
+            GemmBatch pb = b;
+            pb.g[0] = b.g[i];
+            pb.ngroups = 1;
+            const GemmArgs& g = b.g[i];
+            const int t = ((g.M + 255) / 256) * ((g.N + W2N - 1) / W2N);
+            pb.tphase_q = t / 8;
+            const double ea = 4.0, ec = (g.flags & EPI_BF16OUT) ? 2.0 : 4.0;
+            const double gfl = 2.0 * g.M * (double)g.N * g.K,
+                         gby = ea * g.M * (double)g.K + 4.0 * g.N * (double)g.K + ec * g.M * (double)g.N;
+            for (int base = 0; base < pb.tphase_q; base += kF2PhaseTiles) {
+              pb.tphase_base = base;
+              const int per = std::min(kF2PhaseTiles, pb.tphase_q - base);
+              hipEvent_t ev = prof_start(s);
+              hipLaunchKernelGGL((gemm_f32_w2_kernel<256, false>), dim3(8 * per, 1, 1), dim3(256),
+                                 0, s, pb);
+              GS_CHECK_HIP(hipGetLastError());
+              if (ev)
+                prof_stop(s, ev, gemm_prof_name("gemm_f32_w2_kernel<256>", pb).c_str(),
+                          gfl * 8 * per / t, gby * 8 * per / t);
+            }
+          }
+          return post_layernorm(b, s);
+        }
         hipEvent_t ev = prof_start(s);
         const dim3 grid2(bm == 256 ? t256 : t192, 1, b.ngroups);
         if (bm == 256)

@@ -149,6 +149,10 @@ struct GemmBatch {
   // fp32 kernel: 0 chosen by launch_gemm; requested (validated): 1 register-staged,
   // 2 direct-to-LDS, 3 bf16x6 (fp32-accurate products on bf16 matrix cores)
   int32_t kernel = 0;
+  // set by launch_gemm for the tile-phase launches of the 256 x 128 fp32
+  // kernel (0: one launch covers every tile): workgroup b runs tile
+  // (b % 8) * tphase_q + tphase_base + b / 8 of the group's XCD-major order
+  int32_t tphase_q = 0, tphase_base = 0;
 };
 
 // Launch a grouped GEMM (all groups must share the loader / layout kinds).

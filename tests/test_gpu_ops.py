@@ -118,6 +118,30 @@ def test_linear_bf16_large_launches(M, K, N, epi):
     assert_close(got, ref, rtol=1e-4, atol=2e-5 * np.sqrt(K / 1024), name=f"bf16 large {epi}")
 
 
+@pytest.mark.parametrize("M,K,N,epi", [(18440, 6144, 1924, "residual"), (12288, 6144, 4096, "nobias"),
+                                       (12288, 7168, 2048, "gelu")])
+def test_linear_f32_long_k_large_launches(M, K, N, epi):
+    """fp32 launches with K >= 6144 and more than one round of 256 x 128
+    tiles run as one launch per round of tiles: 1168 tiles (ragged M and N)
+    as a full round and a partial one (96 + 50 tiles per XCD), 1536 tiles as
+    two full rounds; 768 tiles stay one launch. Against an fp64 product of the
+    same operands."""
+    case(f"linear f32 long K M={M} K={K} N={N} {epi}")
+    x, W, b, r = rnd(M, K), rnd(N, K, scale=0.02), rnd(N, scale=0.1), rnd(M, N)
+    ref = x.astype(np.float64) @ W.astype(np.float64).T + (0 if epi == "nobias" else b.astype(np.float64))
+    flags = 0
+    if epi == "gelu":
+        flags |= G.EPI_GELU
+        ref = 0.5 * ref * (1 + np.tanh(0.7978845608028654 * (ref + 0.044715 * ref ** 3)))
+    elif epi == "residual":
+        flags |= G.EPI_RESIDUAL
+        ref = ref + r
+    y = dev(r) if epi == "residual" else empty(M, N)  # residual in place
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), None if epi == "nobias" else p(dev(b)), p(y),
+                              M, K, N, 0, flags, p(y) if epi == "residual" else None, stream()))
+    assert_close(host(y), ref, rtol=1e-4, atol=2e-5 * np.sqrt(K / 1024), name=f"f32 long K {epi}")
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 1024, 256), (256, 4096, 256), (300, 1792, 7168),
                                    (129, 96, 130)])
 def test_linear_f32x6_accuracy_vs_fp64(M, K, N):
