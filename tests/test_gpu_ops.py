@@ -142,6 +142,36 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
     assert_close(host(y), ref, rtol=1e-4, atol=2e-5 * np.sqrt(K / 1024), name=f"f32 long K {epi}")
 
 
+# The direct-to-LDS kernels wait for their own loads with hand-counted
+# s_waitcnt vmcnt immediates, which differ between the first, the steady-state
+# and the last K steps. Each kernel here runs K of one, two, three and many
+# steps (odd and even counts), against an fp64 product of the same operands:
+# the fp32 256- and 192-row kernels (16-deep steps), the bf16 two- and
+# three-stage kernels (32-deep steps; K >= 6144 takes three stages) and the
+# 128 x 128 kernel of small launches (32-deep steps, split-K at long K).
+@pytest.mark.parametrize("M,K,N,bf16", [
+    (8192, 16, 3072, False), (8192, 32, 3072, False), (8192, 48, 3072, False),
+    (8192, 272, 3072, False),
+    (24576, 16, 768, False), (24576, 48, 768, False), (24576, 272, 768, False),
+    (8192, 32, 3072, True), (8192, 64, 3072, True), (8192, 96, 3072, True), (8192, 288, 3072, True),
+    (8192, 6176, 3072, True), (8192, 6208, 3072, True),
+    (768, 32, 1024, False), (768, 64, 1024, False), (768, 96, 1024, False), (768, 4128, 1024, False)])
+def test_linear_direct_to_lds_k_classes(M, K, N, bf16):
+    case(f"linear K classes M={M} K={K} N={N} bf16={bf16}")
+    x, W, b = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1)
+    xd, Wd = dev(x), dev(W)
+    if bf16:
+        xr, Wr = xd.to(torch.bfloat16).double(), Wd.to(torch.bfloat16).double()
+    else:
+        xr, Wr = xd.double(), Wd.double()
+    ref = host(torch.mm(xr, Wr.t().contiguous()) + dev(b).double())
+    y = empty(M, N)
+    G.check(L().gs_hip_linear(p(xd), p(Wd), p(dev(b)), p(y), M, K, N, 0, G.EPI_BF16 if bf16 else 0,
+                              None, stream()))
+    assert_close(host(y), ref, rtol=1e-4, atol=4e-5 * np.sqrt(max(K, 256) / 1024),
+                 name=f"K classes K={K}")
+
+
 @pytest.mark.parametrize("M,K,N", [(256, 1024, 256), (256, 4096, 256), (300, 1792, 7168),
                                    (129, 96, 130)])
 def test_linear_f32x6_accuracy_vs_fp64(M, K, N):
@@ -620,14 +650,16 @@ def test_conv2d_any_channels(B, H, W, Cin, Cout, k, s, pd, layout, flags, res):
 
 # conv2d_forward reads kernel_h and kernel_w separately (src/nn/gpu_ops.cr:
 # 491-495): kh x kw kernels through gs_hip_conv2d_hw, on the register-staged
-# conv kernel, the bf16x6 kernel and (the last case: 768 tiles of 192 rows)
-# the direct-to-LDS conv kernel.
+# conv kernel, the bf16x6 kernel and (the last two cases: 768 tiles of 192
+# rows; K = 96 and 48, six and three 16-deep steps of one tap each) the
+# direct-to-LDS conv kernel.
 @pytest.mark.parametrize("B,H,W,Cin,Cout,kh,kw,s,pd,layout,flags", [
     (2, 9, 11, 32, 40, 1, 3, 1, 1, 0, 0),
     (1, 12, 10, 64, 32, 3, 1, 2, 1, 1, G.CONV_RELU_OUT),
     (2, 7, 13, 20, 16, 2, 5, 1, 2, 0, G.CONV_RELU_IN),
     (1, 10, 10, 32, 64, 5, 2, 3, 0, 0, G.CONV_F32X6),
-    (1, 192, 382, 32, 256, 3, 1, 1, 1, 0, 0)])
+    (1, 192, 382, 32, 256, 3, 1, 1, 1, 0, 0),
+    (1, 192, 384, 16, 256, 3, 1, 1, 1, 0, 0)])
 def test_conv2d_nonsquare_kernel(B, H, W, Cin, Cout, kh, kw, s, pd, layout, flags):
     case(f"conv2d_hw B={B} {H}x{W} {Cin}->{Cout} k={kh}x{kw} s={s} p={pd} layout={layout} "
          f"flags={flags}")
