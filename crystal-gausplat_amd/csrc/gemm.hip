@@ -1022,6 +1022,12 @@ constexpr int W2_SS = 68;                    // epilogue stage row stride (float
 // three workgroups per CU (measured at config 3: the 576-tile decoder launches
 // run 105 TFLOP/s on it against 120 on the 128 x 128 kernels)
 constexpr int kF2MinTiles = 768;
+// Small plain-row launches (below one round of 256 x 128 tiles) take the
+// 64-row form unsplit from this many of its tiles. Measured against the split
+// 128 x 128 kernel at one image / one pair: 432 tiles (decoder qkv, two chains)
+// +5 %, 576 +0-5 %, 768 (encoder fc1 on two images) +8 %; 288 and 384 tiles
+// 10-20 % slower.
+constexpr int kW64MinTiles = 432;
 // Long-K launches of the fp32 256 x 128 kernel run as one launch per round of
 // workgroup slots (96 tiles per XCD: 32 CUs x 3 workgroups), so every round
 // starts together, as the first round of one launch does, and its tiles stream
@@ -1418,13 +1424,15 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   constexpr int FK = 16;                     // floats per K step
   constexpr int WTM = BM / 64;               // 32-row blocks per wave
   constexpr int FSTAGE = (BM + W2N) * FK;    // floats per LDS stage
-  static_assert(BM == 256 || BM == 192, "tile rows");
-  static_assert(4 * 32 * W2_SS <= 2 * FSTAGE, "epilogue stages fit the LDS stages");
+  // the epilogue's four 32-row wave stages overlay the LDS stages (BM = 64
+  // allocates past the two K stages for them)
+  constexpr int LDSF = 2 * FSTAGE > 4 * 32 * W2_SS ? 2 * FSTAGE : 4 * 32 * W2_SS;
+  static_assert(BM == 256 || BM == 192 || (BM == 64 && !CONV), "tile rows");
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
   int m0, n0;
   if (!f2_tile<BM>(batch, p, m0, n0)) return;
-  __shared__ __attribute__((aligned(16))) float lds[2 * FSTAGE];
+  __shared__ __attribute__((aligned(16))) float lds[LDSF];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1500,8 +1508,10 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
       GS_F2_ISSUE(buf ^ 1, k0 + FK)
       if constexpr (BM == 256)
         asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
-      else
+      else if constexpr (BM == 192)
         asm volatile("s_waitcnt vmcnt(5)\n\ts_barrier" ::: "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(3)\n\ts_barrier" ::: "memory");
     } else {
       asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     }
@@ -1511,19 +1521,23 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
     for (int u = 0; u < 2; ++u) {
       const int co = ((2 * hl + u) ^ swz) << 2;
       const fx4 a0 = *(const fx4*)(as + ra0 + co);
-      const fx4 a1 = *(const fx4*)(as + ra0 + 32 * FK + co);
-      const fx4 a2 = *(const fx4*)(as + ra0 + 64 * FK + co);
-      fx4 a3 = {};
+      fx4 a1 = {}, a2 = {}, a3 = {};
+      if constexpr (WTM >= 2) a1 = *(const fx4*)(as + ra0 + 32 * FK + co);
+      if constexpr (WTM >= 3) a2 = *(const fx4*)(as + ra0 + 64 * FK + co);
       if constexpr (WTM == 4) a3 = *(const fx4*)(as + ra0 + 96 * FK + co);
       const fx4 b0 = *(const fx4*)(bs + rb0 + co);
       const fx4 b1 = *(const fx4*)(bs + rb0 + 32 * FK + co);
 #define GS_F2_MM(X)                                                                          \
   c00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.X, b0.X, c00, 0, 0, 0);                      \
   c01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.X, b1.X, c01, 0, 0, 0);                      \
-  c10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b0.X, c10, 0, 0, 0);                      \
-  c11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b1.X, c11, 0, 0, 0);                      \
-  c20 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2.X, b0.X, c20, 0, 0, 0);                      \
-  c21 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2.X, b1.X, c21, 0, 0, 0);                      \
+  if constexpr (WTM >= 2) {                                                                  \
+    c10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b0.X, c10, 0, 0, 0);                    \
+    c11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b1.X, c11, 0, 0, 0);                    \
+  }                                                                                          \
+  if constexpr (WTM >= 3) {                                                                  \
+    c20 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2.X, b0.X, c20, 0, 0, 0);                    \
+    c21 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2.X, b1.X, c21, 0, 0, 0);                    \
+  }                                                                                          \
   if constexpr (WTM == 4) {                                                                  \
     c30 = __builtin_amdgcn_mfma_f32_32x32x2f32(a3.X, b0.X, c30, 0, 0, 0);                    \
     c31 = __builtin_amdgcn_mfma_f32_32x32x2f32(a3.X, b1.X, c31, 0, 0, 0);                    \
@@ -1542,13 +1556,13 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   float* stage = lds + wave * 32 * W2_SS;
   if (p.flags & EPI_ROPE) {
     w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
-    w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
-    w2_epi_row<true>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
+    if constexpr (WTM >= 2) w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
+    if constexpr (WTM >= 3) w2_epi_row<true>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
     if constexpr (WTM == 4) w2_epi_row<true>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
   } else {
     w2_epi_row<false>(p, c00, c01, mw, nw, stage, lane, l32, hl);
-    w2_epi_row<false>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
-    w2_epi_row<false>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
+    if constexpr (WTM >= 2) w2_epi_row<false>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
+    if constexpr (WTM >= 3) w2_epi_row<false>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
     if constexpr (WTM == 4) w2_epi_row<false>(p, c30, c31, mw + 96, nw, stage, lane, l32, hl);
   }
 }
@@ -1938,7 +1952,22 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   // kernel at every split factor of those shapes)
   const bool dl_ok = !bf16 && blayout == B_NT && !a_relu && (aload == A_PLAIN || aload == A_CONCAT);
   const bool dl_small = dl_ok && (b.kernel == 2 || (b.kernel == 0 && max_tiles * b.ngroups < kF2MinTiles));
-  if (b.ksplit > 1) {  // requested split
+  // small plain-row launches whose 64 x 128 tiles give every CU at least one:
+  // the 64-row form of the direct-to-LDS kernel, unsplit (no reduce pass)
+  int t64 = 0, tot64 = 0;
+  bool w64 = dl_small && aload == A_PLAIN && b.kernel == 0 && b.ksplit == 0;
+  for (int i = 0; w64 && i < b.ngroups; ++i) {
+    const GemmArgs& g = b.g[i];
+    const int t = ((g.M + 63) / 64) * ((g.N + W2N - 1) / W2N);
+    t64 = std::max(t64, t);
+    tot64 += t;
+    w64 = g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 && aligned16(g.B) &&
+          row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+  }
+  w64 = w64 && tot64 >= kW64MinTiles;
+  if (w64) {
+    b.ksplit = 1;
+  } else if (b.ksplit > 1) {  // requested split
     GS_REQUIRE(splitk_eligible(b), "gemm: this launch cannot split K");
     GS_REQUIRE(b.g[0].K / BK >= b.ksplit &&
                    (int64_t)b.ksplit * b.g[0].M * b.g[0].N * b.ngroups <= b.part_ws_elems,
@@ -2075,6 +2104,13 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   bool long_k = true;
   for (int i = 0; i < b.ngroups; ++i) long_k = long_k && b.g[i].K / b.ksplit >= 2048;
   int kern = b.kernel;
+  if (w64) {
+    hipEvent_t ev = prof_start(s);
+    hipLaunchKernelGGL((gemm_f32_w2_kernel<64, false>), dim3(t64, 1, b.ngroups), dim3(256), 0, s, b);
+    GS_CHECK_HIP(hipGetLastError());
+    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_w2_kernel<64>", b).c_str(), flops, bytes);
+    return post_layernorm(b, s);
+  }
   if (kern == 0) {
     kern = dl_ok && (long_k || dl_small) ? 2 : 1;
     // large unsplit launches with plain rows or an implicit conv (no ReLU

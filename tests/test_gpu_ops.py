@@ -146,16 +146,19 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
 # s_waitcnt vmcnt immediates, which differ between the first, the steady-state
 # and the last K steps. Each kernel here runs K of one, two, three and many
 # steps (odd and even counts), against an fp64 product of the same operands:
-# the fp32 256- and 192-row kernels (16-deep steps), the bf16 two- and
-# three-stage kernels (32-deep steps; K >= 6144 takes three stages) and the
-# 128 x 128 kernel of small launches (32-deep steps, split-K at long K).
+# the fp32 256-, 192- and 64-row kernels (16-deep steps; the 64-row form takes
+# small launches with at least 432 of its tiles, here with ragged M too), the
+# bf16 two- and three-stage kernels (32-deep steps; K >= 6144 takes three
+# stages) and the 128 x 128 kernel of small launches (32-deep steps, split-K
+# at long K).
 @pytest.mark.parametrize("M,K,N,bf16", [
     (8192, 16, 3072, False), (8192, 32, 3072, False), (8192, 48, 3072, False),
     (8192, 272, 3072, False),
     (24576, 16, 768, False), (24576, 48, 768, False), (24576, 272, 768, False),
     (8192, 32, 3072, True), (8192, 64, 3072, True), (8192, 96, 3072, True), (8192, 288, 3072, True),
     (8192, 6176, 3072, True), (8192, 6208, 3072, True),
-    (768, 32, 1024, False), (768, 64, 1024, False), (768, 96, 1024, False), (768, 4128, 1024, False)])
+    (768, 32, 1024, False), (768, 64, 1024, False), (768, 96, 1024, False), (768, 4128, 1024, False),
+    (1536, 16, 3072, False), (1536, 48, 3072, False), (1400, 272, 3072, False)])
 def test_linear_direct_to_lds_k_classes(M, K, N, bf16):
     case(f"linear K classes M={M} K={K} N={N} bf16={bf16}")
     x, W, b = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1)
