@@ -158,7 +158,8 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
     (8192, 32, 3072, True), (8192, 64, 3072, True), (8192, 96, 3072, True), (8192, 288, 3072, True),
     (8192, 6176, 3072, True), (8192, 6208, 3072, True),
     (768, 32, 1024, False), (768, 64, 1024, False), (768, 96, 1024, False), (768, 4128, 1024, False),
-    (1536, 16, 3072, False), (1536, 48, 3072, False), (1400, 272, 3072, False)])
+    (1536, 16, 3072, False), (1536, 48, 3072, False), (1400, 272, 3072, False),
+    (8192, 256, 4096, False), (8142, 320, 4000, False), (8192, 1088, 2048, False)])
 def test_linear_direct_to_lds_k_classes(M, K, N, bf16):
     case(f"linear K classes M={M} K={K} N={N} bf16={bf16}")
     x, W, b = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1)
