@@ -1409,14 +1409,17 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
 // fp32 kernel of the same structure for large launches with plain rows or an
 // implicit conv (CONV: each K step's A rows gathered from the NHWC input, see
 // below):
-// workgroup tile BM x 128 (BM = 256 or 192) of 2 x 2 waves at (BM / 2) x 64
+// workgroup tile BM x 128 (BM = 256, 192 or 64) of 2 x 2 waves at (BM / 2) x 64
 // (BM / 64 x 2 blocks of v_mfma_f32_32x32x2_f32), 16-deep K steps (64-byte
 // rows: the bf16 kernel's LDS geometry, loader and slot swizzle) streamed into
-// two LDS stages (48 / 40 KB), three workgroups per CU, epilogue through
-// w2_epi_row. Lane l (half h) feeds MFMA step t of a K step with k = 8h + t.
-// BM = 192 serves launches whose 256-row tiles would leave part of the last
-// round of workgroup slots empty (the decoder's N = 768 linears: 576 tiles of
-// 256 rows on 768 slots, exactly 768 of 192 rows).
+// two LDS stages (48 / 40 KB; 35 KB at BM = 64, where the epilogue stages are
+// larger than the K stages), three workgroups per CU (four at BM = 64),
+// epilogue through w2_epi_row. Lane l (half h) feeds MFMA step t of a K step
+// with k = 8h + t. BM = 192 serves launches whose 256-row tiles would leave
+// part of the last round of workgroup slots empty (the decoder's N = 768
+// linears: 576 tiles of 256 rows on 768 slots, exactly 768 of 192 rows);
+// BM = 64 (plain rows only) serves launches below one round of 256-row tiles
+// that make at least kW64MinTiles of its tiles, without split-K.
 
 
 template <int BM, bool CONV>
