@@ -1022,11 +1022,13 @@ constexpr int W2_SS = 68;                    // epilogue stage row stride (float
 // three workgroups per CU (measured at config 3: the 576-tile decoder launches
 // run 105 TFLOP/s on it against 120 on the 128 x 128 kernels)
 constexpr int kF2MinTiles = 768;
-// Small plain-row launches (below one round of 256 x 128 tiles) take the
-// 64-row form unsplit from this many of its tiles. Measured against the split
-// 128 x 128 kernel at one image / one pair: 432 tiles (decoder qkv, two chains)
-// +5 %, 576 +0-5 %, 768 (encoder fc1 on two images) +8 %; 288 and 384 tiles
-// 10-20 % slower.
+// Small launches (plain rows below one round of 256 x 128 tiles, implicit
+// convs below one round of 192 x 128) take the 64-row form unsplit from this
+// many of its tiles. Measured against the split 128 x 128 kernel at one image
+// / one pair: 432 tiles (decoder qkv, two chains) +5 %, 576 +0-5 %, 768
+// (encoder fc1 on two images) +8 %; 288 and 384 tiles 10-20 % slower. The
+// 2304-deep DPT convs of 768 tiles: 120-123 TFLOP/s against 116 for the
+// register-staged conv split in two.
 constexpr int kW64MinTiles = 432;
 // Long-K launches of the fp32 256 x 128 kernel run as one launch per round of
 // workgroup slots (96 tiles per XCD: 32 CUs x 3 workgroups), so every round
@@ -1418,8 +1420,9 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
 // with k = 8h + t. BM = 192 serves launches whose 256-row tiles would leave
 // part of the last round of workgroup slots empty (the decoder's N = 768
 // linears: 576 tiles of 256 rows on 768 slots, exactly 768 of 192 rows);
-// BM = 64 (plain rows only) serves launches below one round of 256-row tiles
-// that make at least kW64MinTiles of its tiles, without split-K.
+// BM = 64 serves launches below one round of 256-row tiles (convs: of
+// 192-row tiles) that make at least kW64MinTiles of its tiles, without
+// split-K.
 
 
 template <int BM, bool CONV>
@@ -1430,7 +1433,7 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   // the epilogue's four 32-row wave stages overlay the LDS stages (BM = 64
   // allocates past the two K stages for them)
   constexpr int LDSF = 2 * FSTAGE > 4 * 32 * W2_SS ? 2 * FSTAGE : 4 * 32 * W2_SS;
-  static_assert(BM == 256 || BM == 192 || (BM == 64 && !CONV), "tile rows");
+  static_assert(BM == 256 || BM == 192 || BM == 64, "tile rows");
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
   int m0, n0;
@@ -1955,19 +1958,25 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   // kernel at every split factor of those shapes)
   const bool dl_ok = !bf16 && blayout == B_NT && !a_relu && (aload == A_PLAIN || aload == A_CONCAT);
   const bool dl_small = dl_ok && (b.kernel == 2 || (b.kernel == 0 && max_tiles * b.ngroups < kF2MinTiles));
-  // small plain-row launches whose 64 x 128 tiles give every CU at least one:
-  // the 64-row form of the direct-to-LDS kernel, unsplit (no reduce pass)
+  // small launches whose 64 x 128 tiles give every CU at least one: the
+  // 64-row form of the direct-to-LDS kernel, unsplit (no reduce pass); plain
+  // rows, and implicit convs without a ReLU prologue below one round of the
+  // 192-row form
   int t64 = 0, tot64 = 0;
-  bool w64 = dl_small && aload == A_PLAIN && b.kernel == 0 && b.ksplit == 0;
+  const bool conv64 = !bf16 && aload == A_CONV && !a_relu && blayout == B_NT;
+  bool w64 = ((dl_small && aload == A_PLAIN) || conv64) && b.kernel == 0 && b.ksplit == 0;
+  int tot192c = 0;
   for (int i = 0; w64 && i < b.ngroups; ++i) {
     const GemmArgs& g = b.g[i];
     const int t = ((g.M + 63) / 64) * ((g.N + W2N - 1) / W2N);
     t64 = std::max(t64, t);
     tot64 += t;
-    w64 = g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 && aligned16(g.B) &&
-          row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+    tot192c += ((g.M + 191) / 192) * ((g.N + W2N - 1) / W2N);
+    w64 = g.K % 16 == 0 && (conv64 ? g.cCin % 16 == 0 : g.lda % 4 == 0) && aligned16(g.A) &&
+          g.ldb % 4 == 0 && aligned16(g.B) && row_epi_ok(g) &&
+          (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
   }
-  w64 = w64 && tot64 >= kW64MinTiles;
+  w64 = w64 && tot64 >= kW64MinTiles && !(conv64 && tot192c >= kF2MinTiles);
   if (w64) {
     b.ksplit = 1;
   } else if (b.ksplit > 1) {  // requested split
@@ -2109,9 +2118,16 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   int kern = b.kernel;
   if (w64) {
     hipEvent_t ev = prof_start(s);
-    hipLaunchKernelGGL((gemm_f32_w2_kernel<64, false>), dim3(t64, 1, b.ngroups), dim3(256), 0, s, b);
+    if (conv64)
+      hipLaunchKernelGGL((gemm_f32_w2_kernel<64, true>), dim3(t64, 1, b.ngroups), dim3(256), 0, s, b);
+    else
+      hipLaunchKernelGGL((gemm_f32_w2_kernel<64, false>), dim3(t64, 1, b.ngroups), dim3(256), 0, s, b);
     GS_CHECK_HIP(hipGetLastError());
-    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_w2_kernel<64>", b).c_str(), flops, bytes);
+    if (ev)
+      prof_stop(s, ev,
+                gemm_prof_name(conv64 ? "gemm_f32_w2_kernel<64,A_CONV>" : "gemm_f32_w2_kernel<64>", b)
+                    .c_str(),
+                flops, bytes);
     return post_layernorm(b, s);
   }
   if (kern == 0) {

@@ -222,12 +222,15 @@ def test_ragged_grid_split_paths(tiny_cfg):
 
 
 def test_tiny_batch_invariance_and_determinism(tiny_cfg):
-    """Pair p of a batch equals the same pair run alone, bit for bit (at this
-    size both batch sizes use the same K split of every GEMM), and a rerun
-    is bit-identical (fixed-order reductions, no atomics)."""
+    """Pair p of a batch equals the same pair run alone, bit for bit, and a
+    rerun is bit-identical (fixed-order reductions, no atomics). Kernel and
+    K-split choices follow a launch's tile count, so the batch is sized for
+    both batch sizes to pick the same kernel and split for every GEMM and
+    conv: at three pairs the full-resolution head convs (3 x 64 x 96 rows,
+    two views: 576 tiles of 64 rows) would move to the 64-row kernel."""
     case("tiny batch invariance")
     cfg = G.default_config(**tiny_cfg)
-    B = 3
+    B = 2
     n = B * 3 * cfg.img_h * cfg.img_w
     i1 = G.seed_uniform(1, "view1", n).reshape(B, 3, cfg.img_h, cfg.img_w)
     i2 = G.seed_uniform(1, "view2", n).reshape(B, 3, cfg.img_h, cfg.img_w)

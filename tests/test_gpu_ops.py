@@ -654,16 +654,19 @@ def test_conv2d_any_channels(B, H, W, Cin, Cout, k, s, pd, layout, flags, res):
 
 # conv2d_forward reads kernel_h and kernel_w separately (src/nn/gpu_ops.cr:
 # 491-495): kh x kw kernels through gs_hip_conv2d_hw, on the register-staged
-# conv kernel, the bf16x6 kernel and (the last two cases: 768 tiles of 192
-# rows; K = 96 and 48, six and three 16-deep steps of one tap each) the
-# direct-to-LDS conv kernel.
+# conv kernel, the bf16x6 kernel, the direct-to-LDS conv kernel (768 tiles of
+# 192 rows; K = 96 and 48, six and three 16-deep steps of one tap each) and
+# its 64-row form (768 and 576 tiles of 64 rows, the second strided with a
+# ReLU epilogue).
 @pytest.mark.parametrize("B,H,W,Cin,Cout,kh,kw,s,pd,layout,flags", [
     (2, 9, 11, 32, 40, 1, 3, 1, 1, 0, 0),
     (1, 12, 10, 64, 32, 3, 1, 2, 1, 1, G.CONV_RELU_OUT),
     (2, 7, 13, 20, 16, 2, 5, 1, 2, 0, G.CONV_RELU_IN),
     (1, 10, 10, 32, 64, 5, 2, 3, 0, 0, G.CONV_F32X6),
     (1, 192, 382, 32, 256, 3, 1, 1, 1, 0, 0),
-    (1, 192, 384, 16, 256, 3, 1, 1, 1, 0, 0)])
+    (1, 192, 384, 16, 256, 3, 1, 1, 1, 0, 0),
+    (2, 96, 128, 64, 256, 3, 3, 1, 1, 0, 0),
+    (32, 24, 32, 64, 768, 3, 3, 2, 1, 0, G.CONV_RELU_OUT)])
 def test_conv2d_nonsquare_kernel(B, H, W, Cin, Cout, kh, kw, s, pd, layout, flags):
     case(f"conv2d_hw B={B} {H}x{W} {Cin}->{Cout} k={kh}x{kw} s={s} p={pd} layout={layout} "
          f"flags={flags}")
