@@ -657,7 +657,8 @@ def test_conv2d_any_channels(B, H, W, Cin, Cout, k, s, pd, layout, flags, res):
 # conv kernel, the bf16x6 kernel, the direct-to-LDS conv kernel (768 tiles of
 # 192 rows; K = 96 and 48, six and three 16-deep steps of one tap each) and
 # its 64-row form (768 and 576 tiles of 64 rows, the second strided with a
-# ReLU epilogue).
+# ReLU epilogue; then 768 and 784 tiles at K = 144 and 48, nine and three
+# 16-deep steps: odd step counts end the two-stage loop on either stage).
 @pytest.mark.parametrize("B,H,W,Cin,Cout,kh,kw,s,pd,layout,flags", [
     (2, 9, 11, 32, 40, 1, 3, 1, 1, 0, 0),
     (1, 12, 10, 64, 32, 3, 1, 2, 1, 1, G.CONV_RELU_OUT),
@@ -666,7 +667,9 @@ def test_conv2d_any_channels(B, H, W, Cin, Cout, k, s, pd, layout, flags, res):
     (1, 192, 382, 32, 256, 3, 1, 1, 1, 0, 0),
     (1, 192, 384, 16, 256, 3, 1, 1, 1, 0, 0),
     (2, 96, 128, 64, 256, 3, 3, 1, 1, 0, 0),
-    (32, 24, 32, 64, 768, 3, 3, 2, 1, 0, G.CONV_RELU_OUT)])
+    (32, 24, 32, 64, 768, 3, 3, 2, 1, 0, G.CONV_RELU_OUT),
+    (2, 96, 128, 16, 256, 3, 3, 1, 1, 0, 0),
+    (2, 96, 128, 16, 256, 1, 3, 1, 1, 1, 0)])
 def test_conv2d_nonsquare_kernel(B, H, W, Cin, Cout, kh, kw, s, pd, layout, flags):
     case(f"conv2d_hw B={B} {H}x{W} {Cin}->{Cout} k={kh}x{kw} s={s} p={pd} layout={layout} "
          f"flags={flags}")
