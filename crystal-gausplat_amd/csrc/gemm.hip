@@ -1030,6 +1030,13 @@ constexpr int kF2MinTiles = 768;
 // 2304-deep DPT convs of 768 tiles: 120-123 TFLOP/s against 116 for the
 // register-staged conv split in two.
 constexpr int kW64MinTiles = 432;
+// Plain-row launches too small for that take the 32-row form (1 x 4 waves at
+// 32 x 32) unsplit from this many of its tiles: one full round at three
+// workgroups per CU (one image's encoder fc1, M = 768 and N = 4096: 100
+// TFLOP/s with no reduce pass, against 91 for the 128 x 128 kernel split in
+// four; at 576 tiles, one image's qkv, it ran level with the split kernel
+// and the encoder 0.4 % slower than at this threshold).
+constexpr int kW32MinTiles = 768;
 // Long-K launches of the fp32 256 x 128 kernel run as one launch per round of
 // workgroup slots (96 tiles per XCD: 32 CUs x 3 workgroups), so every round
 // starts together, as the first round of one launch does, and its tiles stream
@@ -1049,19 +1056,23 @@ static_assert(4 * 32 * W2_SS * 4 <= 2 * W2_STAGE * 2, "w2 epilogue stages fit th
 // (row_epi_ok). Measured in the
 // model: the per-element form of the shared epilogue (64-bit addresses, 4-byte
 // accesses) took this kernel from ~1100 TFLOP/s (main loop) to 360-565.
-template <bool ROPE>
+template <bool ROPE, int NB = 2>
 __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0,
                                            const floatx16& q1, int row0, int col0, float* stage,
                                            int lane, int l32, int hl) {
+  static_assert(NB == 1 || NB == 2, "one or two 32-column blocks");
   const int M = p.M, N = p.N;
   const int flags = ROPE ? p.flags & ~(EPI_RES1 | EPI_RES2) : p.flags & ~EPI_ROPE;
   const float rtok = ROPE ? 1.0f / (float)p.tok_per_img : 0.f;
   const float rgw = ROPE ? 1.0f / (float)p.grid_w : 0.f;
-  // col0 is a multiple of 64, so q0 is the y-axis half and q1 the x-axis
-  // half of one head's RoPE columns
+  // NB = 2: col0 is a multiple of 64, so q0 is the y-axis half and q1 the
+  // x-axis half of one head's RoPE columns. NB = 1 (one 32-column block, q1
+  // unused): col0 is a multiple of 32 and names the half
   const float bv0 = (flags & EPI_BIAS) ? p.bias[min(col0 + l32, N - 1)] : 0.f;
-  const float bv1 = (flags & EPI_BIAS) ? p.bias[min(col0 + 32 + l32, N - 1)] : 0.f;
+  const float bv1 =
+      (NB == 2 && (flags & EPI_BIAS)) ? p.bias[min(col0 + 32 + l32, N - 1)] : 0.f;
   const bool rope = ROPE && col0 < p.rope_ncols;
+  const bool xhalf = NB == 1 && (col0 & 32) != 0;
   // With the tokens per image and the grid width multiples of 4, the four
   // rows 4k .. 4k + 3 of accumulator registers 4g .. 4g + 3 lie in one image
   // and grid row: their position is decoded once (the first row's, x + j for
@@ -1107,9 +1118,15 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
       (void)ty;
       const int ix = tx * 16 + (l32 & 15);
       const float cx = p.rope_cos[ix], sx = p.rope_sin[ix];
-      const float p0 = __shfl_xor(v0, 16), p1 = __shfl_xor(v1, 16);
-      v0 = (l32 < 16) ? (v0 * cy - p0 * sy) : (v0 * cy + p0 * sy);
-      v1 = (l32 < 16) ? (v1 * cx - p1 * sx) : (v1 * cx + p1 * sx);
+      if constexpr (NB == 2) {
+        const float p0 = __shfl_xor(v0, 16), p1 = __shfl_xor(v1, 16);
+        v0 = (l32 < 16) ? (v0 * cy - p0 * sy) : (v0 * cy + p0 * sy);
+        v1 = (l32 < 16) ? (v1 * cx - p1 * sx) : (v1 * cx + p1 * sx);
+      } else {
+        const float c = xhalf ? cx : cy, sn = xhalf ? sx : sy;
+        const float p0 = __shfl_xor(v0, 16);
+        v0 = (l32 < 16) ? (v0 * c - p0 * sn) : (v0 * c + p0 * sn);
+      }
     }
     if (flags & EPI_GELU) {
       v0 = gelu_tanh(v0);
@@ -1121,14 +1138,17 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
     }
     float* srow = stage + (8 * (r >> 2) + 4 * hl + (r & 3)) * W2_SS + l32;
     srow[0] = v0;
-    srow[32] = v1;
+    if constexpr (NB == 2) srow[32] = v1;
   }
   // the stage belongs to this wave: LDS accesses of one wave complete in
   // order, so a wave-level fence orders the writes above and the reads below
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const int rin = lane >> 4, c4 = (lane & 15) * 4;
+  // readback: LPR lanes per row (4 columns each), RPP rows per pass, UPH
+  // passes per 16-row half
+  constexpr int LPR = 8 * NB, RPP = 64 / LPR, UPH = 16 / RPP;
+  const int rin = lane / LPR, c4 = (lane % LPR) * 4;
   const int col = col0 + c4;
   const int colc = min(col, N - 4);
   // sub-pixel scatter (EPI_SCATTER): column col = (i * sc_r + j) * sc_C + c;
@@ -1144,26 +1164,26 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
   // two halves of 16 rows, the residuals of a half read before its stores
 #pragma unroll
   for (int hq = 0; hq < 2; ++hq) {
-  fx4 x1[4], x2[4];
+  fx4 x1[UPH], x2[UPH];
   if (flags & EPI_RES1) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int row = min(row0 + 16 * hq + 4 * u + rin, M - 1);
+    for (int u = 0; u < UPH; ++u) {
+      const int row = min(row0 + 16 * hq + RPP * u + rin, M - 1);
       x1[u] = *(const fx4*)(p.R1 + (int64_t)row * p.ldr1 + colc);
     }
   }
   if (flags & EPI_RES2) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int row = min(row0 + 16 * hq + 4 * u + rin, M - 1);
+    for (int u = 0; u < UPH; ++u) {
+      const int row = min(row0 + 16 * hq + RPP * u + rin, M - 1);
       x2[u] = *(const fx4*)(p.R2 + (int64_t)row * p.ldr2 + colc);
     }
   }
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int q = 4 * hq + u;
-    const int row = row0 + 4 * q + rin;
-    fx4 v = *(const fx4*)(stage + (4 * q + rin) * W2_SS + c4);
+  for (int u = 0; u < UPH; ++u) {
+    const int sr = 16 * hq + RPP * u + rin;
+    const int row = row0 + sr;
+    fx4 v = *(const fx4*)(stage + sr * W2_SS + c4);
     if (flags & EPI_RES1) v = v + x1[u];
     if (flags & EPI_RES2) v = x2[u] + v;
     if (row < M && col < N) {
@@ -1422,18 +1442,24 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
 // linears: 576 tiles of 256 rows on 768 slots, exactly 768 of 192 rows);
 // BM = 64 serves launches below one round of 256-row tiles (convs: of
 // 192-row tiles) that make at least kW64MinTiles of its tiles, without
-// split-K.
+// split-K. BM = 32 (plain rows) serves smaller launches that still make
+// kW32MinTiles of its tiles: 1 x 4 waves at 32 x 32 (one MFMA block each);
+// the 32 A rows of a K step are two waves' loads, and waves 2 and 3 issue
+// the same two loads again (identical bytes to the same LDS words), so every
+// wave issues three loads per K step, as at BM = 64.
 
 
 template <int BM, bool CONV>
 __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   constexpr int FK = 16;                     // floats per K step
-  constexpr int WTM = BM / 64;               // 32-row blocks per wave
+  constexpr bool W1X4 = BM == 32;            // 1 x 4 waves at 32 x 32
+  constexpr int WTM = W1X4 ? 1 : BM / 64;    // 32-row blocks per wave
+  constexpr int NA = W1X4 ? 1 : BM / 64;     // A-row loads per wave per K step
   constexpr int FSTAGE = (BM + W2N) * FK;    // floats per LDS stage
   // the epilogue's four 32-row wave stages overlay the LDS stages (BM = 64
   // allocates past the two K stages for them)
   constexpr int LDSF = 2 * FSTAGE > 4 * 32 * W2_SS ? 2 * FSTAGE : 4 * 32 * W2_SS;
-  static_assert(BM == 256 || BM == 192 || BM == 64, "tile rows");
+  static_assert(BM == 256 || BM == 192 || BM == 64 || (BM == 32 && !CONV), "tile rows");
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
   int m0, n0;
@@ -1442,20 +1468,22 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = W1X4 ? 0 : wave >> 1, wn = W1X4 ? wave : wave & 1;
   const int l32 = lane & 31, hl = lane >> 5;
   const int rin = lane >> 2, chunk = (lane & 3) ^ ((rin >> 2) & 3);
-  const float* ag[BM / 64];
+  // first of the 16 A rows that load i of this wave fills
+  auto a_row0 = [&](int i) { return W1X4 ? 16 * (wave & 1) : 16 * (4 * i + wave); };
+  const float* ag[NA];
   const float* bg[W2N / 64];
   // implicit conv (A_CONV): per row, the top-left input coordinate of its
   // window and the address of that (possibly padded) pixel's channel
   // 4 * chunk; a K step of 16 channels lies inside one tap (Cin % 16 == 0),
   // so a lane's 16 bytes are contiguous. Taps outside the image, and rows
   // past M, load from g_zero16.
-  int ohs[BM / 64], ows[BM / 64];
+  int ohs[NA], ows[NA];
 #pragma unroll
-  for (int i = 0; i < BM / 64; ++i) {
-    const int mr = m0 + 16 * (4 * i + wave) + rin;
+  for (int i = 0; i < NA; ++i) {
+    const int mr = m0 + a_row0(i) + rin;
     const int64_t m = min(mr, M - 1);
     if constexpr (CONV) {
       const int hw = p.cHo * p.cWo;
@@ -1482,11 +1510,10 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   {                                                                                          \
     if constexpr (CONV) {                                                                    \
       const int64_t toff = ((int64_t)tkh * p.cW + tkw) * p.cCin + tic;                       \
-      _Pragma("unroll") for (int i = 0; i < BM / 64; ++i) {                                  \
+      _Pragma("unroll") for (int i = 0; i < NA; ++i) {                                       \
         const bool ok = (unsigned)(ohs[i] + tkh) < (unsigned)p.cH &&                          \
                         (unsigned)(ows[i] + tkw) < (unsigned)p.cW;                            \
-        lds_dma16(ok ? ag[i] + toff : zrow,                                                  \
-                  lds0 + ((BUF) * FSTAGE + 16 * (4 * i + wave) * FK) * 4);                   \
+        lds_dma16(ok ? ag[i] + toff : zrow, lds0 + ((BUF) * FSTAGE + a_row0(i) * FK) * 4);   \
       }                                                                                      \
       tic += FK;                                                                             \
       if (tic == p.cCin) {                                                                   \
@@ -1497,19 +1524,19 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
         }                                                                                    \
       }                                                                                      \
     } else {                                                                                 \
-      _Pragma("unroll") for (int i = 0; i < BM / 64; ++i)                                    \
-        lds_dma16(ag[i] + (K0), lds0 + ((BUF) * FSTAGE + 16 * (4 * i + wave) * FK) * 4);     \
+      _Pragma("unroll") for (int i = 0; i < NA; ++i)                                         \
+        lds_dma16(ag[i] + (K0), lds0 + ((BUF) * FSTAGE + a_row0(i) * FK) * 4);               \
     }                                                                                        \
     _Pragma("unroll") for (int i = 0; i < W2N / 64; ++i)                                     \
       lds_dma16(bg[i] + (K0), lds0 + ((BUF) * FSTAGE + (BM + 16 * (4 * i + wave)) * FK) * 4); \
   }
   const int swz = (l32 >> 2) & 3;
-  const int ra0 = (wm * 32 * WTM + l32) * FK, rb0 = (wn * 64 + l32) * FK;
+  const int ra0 = (wm * 32 * WTM + l32) * FK, rb0 = (wn * (W1X4 ? 32 : 64) + l32) * FK;
   floatx16 c00 = {}, c01 = {}, c10 = {}, c11 = {}, c20 = {}, c21 = {}, c30 = {}, c31 = {};
   int buf = 0;
   GS_F2_ISSUE(0, 0)
   for (int k0 = 0; k0 < K; k0 += FK) {
-    // each wave waits for its own BM / 64 + 2 loads of step k0
+    // each wave waits for its own NA + 2 loads of step k0
     if (k0 + FK < K) {
       GS_F2_ISSUE(buf ^ 1, k0 + FK)
       if constexpr (BM == 256)
@@ -1532,10 +1559,11 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
       if constexpr (WTM >= 3) a2 = *(const fx4*)(as + ra0 + 64 * FK + co);
       if constexpr (WTM == 4) a3 = *(const fx4*)(as + ra0 + 96 * FK + co);
       const fx4 b0 = *(const fx4*)(bs + rb0 + co);
-      const fx4 b1 = *(const fx4*)(bs + rb0 + 32 * FK + co);
+      fx4 b1 = {};
+      if constexpr (!W1X4) b1 = *(const fx4*)(bs + rb0 + 32 * FK + co);
 #define GS_F2_MM(X)                                                                          \
   c00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.X, b0.X, c00, 0, 0, 0);                      \
-  c01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.X, b1.X, c01, 0, 0, 0);                      \
+  if constexpr (!W1X4) c01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0.X, b1.X, c01, 0, 0, 0); \
   if constexpr (WTM >= 2) {                                                                  \
     c10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b0.X, c10, 0, 0, 0);                    \
     c11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1.X, b1.X, c11, 0, 0, 0);                    \
@@ -1558,9 +1586,14 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
     buf ^= 1;
   }
 #undef GS_F2_ISSUE
-  const int mw = m0 + wm * 32 * WTM, nw = n0 + wn * 64;
+  const int mw = m0 + wm * 32 * WTM, nw = n0 + wn * (W1X4 ? 32 : 64);
   float* stage = lds + wave * 32 * W2_SS;
-  if (p.flags & EPI_ROPE) {
+  if constexpr (W1X4) {
+    if (p.flags & EPI_ROPE)
+      w2_epi_row<true, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
+    else
+      w2_epi_row<false, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
+  } else if (p.flags & EPI_ROPE) {
     w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
     if constexpr (WTM >= 2) w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
     if constexpr (WTM >= 3) w2_epi_row<true>(p, c20, c21, mw + 64, nw, stage, lane, l32, hl);
@@ -1977,7 +2010,20 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
           (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
   }
   w64 = w64 && tot64 >= kW64MinTiles && !(conv64 && tot192c >= kF2MinTiles);
-  if (w64) {
+  // smaller plain-row launches whose 32 x 128 tiles still fill the CUs: the
+  // 32-row form, unsplit
+  int t32 = 0, tot32 = 0;
+  bool w32 = !w64 && dl_small && aload == A_PLAIN && b.kernel == 0 && b.ksplit == 0;
+  for (int i = 0; w32 && i < b.ngroups; ++i) {
+    const GemmArgs& g = b.g[i];
+    const int t = ((g.M + 31) / 32) * ((g.N + W2N - 1) / W2N);
+    t32 = std::max(t32, t);
+    tot32 += t;
+    w32 = g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
+          aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+  }
+  w32 = w32 && tot32 >= kW32MinTiles;
+  if (w64 || w32) {
     b.ksplit = 1;
   } else if (b.ksplit > 1) {  // requested split
     GS_REQUIRE(splitk_eligible(b), "gemm: this launch cannot split K");
@@ -2116,6 +2162,13 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   bool long_k = true;
   for (int i = 0; i < b.ngroups; ++i) long_k = long_k && b.g[i].K / b.ksplit >= 2048;
   int kern = b.kernel;
+  if (w32) {
+    hipEvent_t ev = prof_start(s);
+    hipLaunchKernelGGL((gemm_f32_w2_kernel<32, false>), dim3(t32, 1, b.ngroups), dim3(256), 0, s, b);
+    GS_CHECK_HIP(hipGetLastError());
+    if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_w2_kernel<32>", b).c_str(), flops, bytes);
+    return post_layernorm(b, s);
+  }
   if (w64) {
     hipEvent_t ev = prof_start(s);
     if (conv64)

@@ -144,13 +144,16 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
 
 # The direct-to-LDS kernels wait for their own loads with hand-counted
 # s_waitcnt vmcnt immediates, which differ between the first, the steady-state
-# and the last K steps. Each kernel here runs K of one, two, three and many
-# steps (odd and even counts), against an fp64 product of the same operands:
-# the fp32 256-, 192- and 64-row kernels (16-deep steps; the 64-row form takes
-# small launches with at least 432 of its tiles, here with ragged M too), the
-# bf16 two- and three-stage kernels (32-deep steps; K >= 6144 takes three
-# stages) and the 128 x 128 kernel of small launches (32-deep steps, split-K
-# at long K).
+# and the last K steps. Each kernel here runs K of few and many steps, against
+# an fp64 product of the same operands: the fp32 256-, 192-, 64- and 32-row
+# kernels (16-deep steps; gs_hip_linear pads K to a multiple of 32, so K =
+# 16 / 48 / 272 run as 2 / 4 / 18 steps; odd step counts of these kernels are
+# reached through the conv op in test_conv2d_nonsquare_kernel; the 64-row form
+# takes small launches with at least 432 of its tiles and the 32-row form
+# smaller ones with at least 768 of its tiles, here with ragged M and N too),
+# the bf16 two- and three-stage kernels (32-deep steps: one, two, three and
+# many; K >= 6144 takes three stages) and the 128 x 128 kernel of small
+# launches (32-deep steps, split-K at long K).
 @pytest.mark.parametrize("M,K,N,bf16", [
     (8192, 16, 3072, False), (8192, 32, 3072, False), (8192, 48, 3072, False),
     (8192, 272, 3072, False),
@@ -159,7 +162,9 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
     (8192, 6176, 3072, True), (8192, 6208, 3072, True),
     (768, 32, 1024, False), (768, 64, 1024, False), (768, 96, 1024, False), (768, 4128, 1024, False),
     (1536, 16, 3072, False), (1536, 48, 3072, False), (1400, 272, 3072, False),
-    (8192, 256, 4096, False), (8142, 320, 4000, False), (8192, 1088, 2048, False)])
+    (8192, 256, 4096, False), (8142, 320, 4000, False), (8192, 1088, 2048, False),
+    (768, 16, 4096, False), (768, 48, 4096, False), (768, 1024, 4096, False),
+    (750, 272, 4000, False)])
 def test_linear_direct_to_lds_k_classes(M, K, N, bf16):
     case(f"linear K classes M={M} K={K} N={N} bf16={bf16}")
     x, W, b = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1)
@@ -174,6 +179,31 @@ def test_linear_direct_to_lds_k_classes(M, K, N, bf16):
                               None, stream()))
     assert_close(host(y), ref, rtol=1e-4, atol=4e-5 * np.sqrt(max(K, 256) / 1024),
                  name=f"K classes K={K}")
+
+
+@pytest.mark.parametrize("M,K,N", [(768, 1024, 4096), (750, 288, 4000)])
+@pytest.mark.parametrize("epi", ["gelu", "relu", "residual"])
+def test_linear_32row_epilogues(M, K, N, epi):
+    """The 32-row direct-to-LDS form (launches of 768 or more 32 x 128 tiles
+    below 432 of 64 rows: 768 here, the second case ragged in M and N)
+    with its one-block epilogue: bias + GELU, bias + ReLU, and a residual
+    added in place, against an fp64 product."""
+    case(f"linear 32-row M={M} K={K} N={N} {epi}")
+    x, W, b, r = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1), rnd(M, N)
+    ref = x.astype(np.float64) @ W.astype(np.float64).T + b.astype(np.float64)
+    if epi == "gelu":
+        flags = G.EPI_GELU
+        ref = 0.5 * ref * (1 + np.tanh(0.7978845608028654 * (ref + 0.044715 * ref ** 3)))
+    elif epi == "relu":
+        flags = G.EPI_RELU
+        ref = np.maximum(ref, 0)
+    else:
+        flags = G.EPI_RESIDUAL
+        ref = ref + r
+    y = dev(r) if epi == "residual" else empty(M, N)
+    G.check(L().gs_hip_linear(p(dev(x)), p(dev(W)), p(dev(b)), p(y), M, K, N, 0, flags,
+                              p(y) if epi == "residual" else None, stream()))
+    assert_close(host(y), ref, rtol=1e-4, atol=4e-5 * np.sqrt(K / 1024), name=f"32-row {epi}")
 
 
 @pytest.mark.parametrize("M,K,N", [(256, 1024, 256), (256, 4096, 256), (300, 1792, 7168),
