@@ -1434,8 +1434,9 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
 // workgroup tile BM x 128 (BM = 256, 192 or 64) of 2 x 2 waves at (BM / 2) x 64
 // (BM / 64 x 2 blocks of v_mfma_f32_32x32x2_f32), 16-deep K steps (64-byte
 // rows: the bf16 kernel's LDS geometry, loader and slot swizzle) streamed into
-// two LDS stages (48 / 40 KB; 35 KB at BM = 64, where the epilogue stages are
-// larger than the K stages), three workgroups per CU (four at BM = 64),
+// two LDS stages (48 / 40 KB; 35 KB at BM = 64 and 32, where the epilogue
+// stages are larger than the K stages), three workgroups per CU (four at
+// BM = 64),
 // epilogue through w2_epi_row. Lane l (half h) feeds MFMA step t of a K step
 // with k = 8h + t. BM = 192 serves launches whose 256-row tiles would leave
 // part of the last round of workgroup slots empty (the decoder's N = 768
@@ -1457,7 +1458,7 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   constexpr int NA = W1X4 ? 1 : BM / 64;     // A-row loads per wave per K step
   constexpr int FSTAGE = (BM + W2N) * FK;    // floats per LDS stage
   // the epilogue's four 32-row wave stages overlay the LDS stages (BM = 64
-  // allocates past the two K stages for them)
+  // and 32 allocate past the two K stages for them)
   constexpr int LDSF = 2 * FSTAGE > 4 * 32 * W2_SS ? 2 * FSTAGE : 4 * 32 * W2_SS;
   static_assert(BM == 256 || BM == 192 || BM == 64 || (BM == 32 && !CONV), "tile rows");
   const GemmArgs& p = batch.g[blockIdx.z];
