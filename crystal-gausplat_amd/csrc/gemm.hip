@@ -1060,19 +1060,17 @@ template <bool ROPE, int NB = 2>
 __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0,
                                            const floatx16& q1, int row0, int col0, float* stage,
                                            int lane, int l32, int hl) {
-  static_assert(NB == 1 || NB == 2, "one or two 32-column blocks");
+  static_assert(NB == 2 || (NB == 1 && !ROPE), "two 32-column blocks, or one without RoPE");
   const int M = p.M, N = p.N;
   const int flags = ROPE ? p.flags & ~(EPI_RES1 | EPI_RES2) : p.flags & ~EPI_ROPE;
   const float rtok = ROPE ? 1.0f / (float)p.tok_per_img : 0.f;
   const float rgw = ROPE ? 1.0f / (float)p.grid_w : 0.f;
-  // NB = 2: col0 is a multiple of 64, so q0 is the y-axis half and q1 the
-  // x-axis half of one head's RoPE columns. NB = 1 (one 32-column block, q1
-  // unused): col0 is a multiple of 32 and names the half
+  // col0 is a multiple of 64, so q0 is the y-axis half and q1 the x-axis
+  // half of one head's RoPE columns. NB = 1: one 32-column block (q1 unused)
   const float bv0 = (flags & EPI_BIAS) ? p.bias[min(col0 + l32, N - 1)] : 0.f;
   const float bv1 =
       (NB == 2 && (flags & EPI_BIAS)) ? p.bias[min(col0 + 32 + l32, N - 1)] : 0.f;
   const bool rope = ROPE && col0 < p.rope_ncols;
-  const bool xhalf = NB == 1 && (col0 & 32) != 0;
   // With the tokens per image and the grid width multiples of 4, the four
   // rows 4k .. 4k + 3 of accumulator registers 4g .. 4g + 3 lie in one image
   // and grid row: their position is decoded once (the first row's, x + j for
@@ -1118,15 +1116,9 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
       (void)ty;
       const int ix = tx * 16 + (l32 & 15);
       const float cx = p.rope_cos[ix], sx = p.rope_sin[ix];
-      if constexpr (NB == 2) {
-        const float p0 = __shfl_xor(v0, 16), p1 = __shfl_xor(v1, 16);
-        v0 = (l32 < 16) ? (v0 * cy - p0 * sy) : (v0 * cy + p0 * sy);
-        v1 = (l32 < 16) ? (v1 * cx - p1 * sx) : (v1 * cx + p1 * sx);
-      } else {
-        const float c = xhalf ? cx : cy, sn = xhalf ? sx : sy;
-        const float p0 = __shfl_xor(v0, 16);
-        v0 = (l32 < 16) ? (v0 * c - p0 * sn) : (v0 * c + p0 * sn);
-      }
+      const float p0 = __shfl_xor(v0, 16), p1 = __shfl_xor(v1, 16);
+      v0 = (l32 < 16) ? (v0 * cy - p0 * sy) : (v0 * cy + p0 * sy);
+      v1 = (l32 < 16) ? (v1 * cx - p1 * sx) : (v1 * cx + p1 * sx);
     }
     if (flags & EPI_GELU) {
       v0 = gelu_tanh(v0);
@@ -1447,7 +1439,8 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
 // kW32MinTiles of its tiles: 1 x 4 waves at 32 x 32 (one MFMA block each);
 // the 32 A rows of a K step are two waves' loads, and waves 2 and 3 issue
 // the same two loads again (identical bytes to the same LDS words), so every
-// wave issues three loads per K step, as at BM = 64.
+// wave issues three loads per K step, as at BM = 64. Its epilogue has no RoPE
+// form (such launches stay on the other kernels).
 
 
 template <int BM, bool CONV>
@@ -1589,11 +1582,8 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
 #undef GS_F2_ISSUE
   const int mw = m0 + wm * 32 * WTM, nw = n0 + wn * (W1X4 ? 32 : 64);
   float* stage = lds + wave * 32 * W2_SS;
-  if constexpr (W1X4) {
-    if (p.flags & EPI_ROPE)
-      w2_epi_row<true, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
-    else
-      w2_epi_row<false, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
+  if constexpr (W1X4) {  // no RoPE launches (checked on the host)
+    w2_epi_row<false, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
   } else if (p.flags & EPI_ROPE) {
     w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
     if constexpr (WTM >= 2) w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
@@ -2021,7 +2011,7 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     t32 = std::max(t32, t);
     tot32 += t;
     w32 = g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
-          aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+          aligned16(g.B) && row_epi_ok(g) && !(g.flags & EPI_ROPE);
   }
   w32 = w32 && tot32 >= kW32MinTiles;
   if (w64 || w32) {
