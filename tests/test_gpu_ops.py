@@ -151,8 +151,9 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
 # reached through the conv op in test_conv2d_nonsquare_kernel; the 64-row form
 # takes small launches with at least 432 of its tiles and the 32-row form
 # smaller ones with at least 768 of its tiles, here with ragged M and N too),
-# the bf16 two- and three-stage kernels (32-deep steps: one, two, three and
-# many; K >= 6144 takes three stages) and the 128 x 128 kernel of small
+# the 192-row form also at ragged M and N (24500 x 760: 128 x 6 tiles, the
+# last row and column tiles partial), the bf16 two- and three-stage kernels
+# (32-deep steps: one, two, three and many; K >= 6144 takes three stages) and the 128 x 128 kernel of small
 # launches (32-deep steps, split-K at long K).
 @pytest.mark.parametrize("M,K,N,bf16", [
     (8192, 16, 3072, False), (8192, 32, 3072, False), (8192, 48, 3072, False),
@@ -164,7 +165,7 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
     (1536, 16, 3072, False), (1536, 48, 3072, False), (1400, 272, 3072, False),
     (8192, 256, 4096, False), (8142, 320, 4000, False), (8192, 1088, 2048, False),
     (768, 16, 4096, False), (768, 48, 4096, False), (768, 1024, 4096, False),
-    (750, 272, 4000, False)])
+    (750, 272, 4000, False), (24500, 48, 760, False), (24500, 1024, 760, False)])
 def test_linear_direct_to_lds_k_classes(M, K, N, bf16):
     case(f"linear K classes M={M} K={K} N={N} bf16={bf16}")
     x, W, b = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1)
