@@ -1018,6 +1018,7 @@ __device__ __forceinline__ void split3(const fx4& v, bf16x4& h, bf16x4& m, bf16x
 constexpr int W2M = 256, W2N = 128, W2K = 32;
 constexpr int W2_STAGE = (W2M + W2N) * W2K;  // bf16 per LDS stage
 constexpr int W2_SS = 68;                    // epilogue stage row stride (floats)
+constexpr int W2_SS1 = 36;                   // the same for one 32-column block
 // fp32 256 x 128 kernel dispatch: at least this many tiles, one full round at
 // three workgroups per CU (measured at config 3: the 576-tile decoder launches
 // run 105 TFLOP/s on it against 120 on the 128 x 128 kernels)
@@ -1031,11 +1032,14 @@ constexpr int kF2MinTiles = 768;
 // register-staged conv split in two.
 constexpr int kW64MinTiles = 432;
 // Plain-row launches too small for that take the 32-row form (1 x 4 waves at
-// 32 x 32) unsplit from this many of its tiles: one full round at three
-// workgroups per CU (one image's encoder fc1, M = 768 and N = 4096: 100
-// TFLOP/s with no reduce pass, against 91 for the 128 x 128 kernel split in
-// four; at 576 tiles, one image's qkv, it ran level with the split kernel
-// and the encoder 0.4 % slower than at this threshold).
+// 32 x 32) unsplit from this many of its tiles: three per CU (one image's
+// encoder fc1, M = 768 and N = 4096: 100 TFLOP/s with no reduce pass, against
+// 91 for the 128 x 128 kernel split in four; at 576 tiles, one image's qkv,
+// it ran level with the split kernel and the encoder 0.4 % slower than at
+// this threshold). It also takes launches of the 64-row form whose busiest
+// CU it loads less (one pair: the encoder qkv, 576 tiles of 64 rows, 3 per
+// CU, against 1152 of 32 rows, 5 per CU: 91.5 -> 97.7 TFLOP/s; the decoder
+// fc1 88.4 -> 96.4).
 constexpr int kW32MinTiles = 768;
 // Long-K launches of the fp32 256 x 128 kernel run as one launch per round of
 // workgroup slots (96 tiles per XCD: 32 CUs x 3 workgroups), so every round
@@ -1060,17 +1064,20 @@ template <bool ROPE, int NB = 2>
 __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0,
                                            const floatx16& q1, int row0, int col0, float* stage,
                                            int lane, int l32, int hl) {
-  static_assert(NB == 2 || (NB == 1 && !ROPE), "two 32-column blocks, or one without RoPE");
+  static_assert(NB == 1 || NB == 2, "one or two 32-column blocks");
+  constexpr int SS = NB == 2 ? W2_SS : W2_SS1;  // stage row stride (floats)
   const int M = p.M, N = p.N;
   const int flags = ROPE ? p.flags & ~(EPI_RES1 | EPI_RES2) : p.flags & ~EPI_ROPE;
   const float rtok = ROPE ? 1.0f / (float)p.tok_per_img : 0.f;
   const float rgw = ROPE ? 1.0f / (float)p.grid_w : 0.f;
-  // col0 is a multiple of 64, so q0 is the y-axis half and q1 the x-axis
-  // half of one head's RoPE columns. NB = 1: one 32-column block (q1 unused)
+  // NB = 2: col0 is a multiple of 64, so q0 is the y-axis half and q1 the
+  // x-axis half of one head's RoPE columns. NB = 1 (one 32-column block, q1
+  // unused): col0 is a multiple of 32 and names the half
   const float bv0 = (flags & EPI_BIAS) ? p.bias[min(col0 + l32, N - 1)] : 0.f;
   const float bv1 =
       (NB == 2 && (flags & EPI_BIAS)) ? p.bias[min(col0 + 32 + l32, N - 1)] : 0.f;
   const bool rope = ROPE && col0 < p.rope_ncols;
+  const bool xhalf = NB == 1 && (col0 & 32) != 0;
   // With the tokens per image and the grid width multiples of 4, the four
   // rows 4k .. 4k + 3 of accumulator registers 4g .. 4g + 3 lie in one image
   // and grid row: their position is decoded once (the first row's, x + j for
@@ -1116,9 +1123,15 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
       (void)ty;
       const int ix = tx * 16 + (l32 & 15);
       const float cx = p.rope_cos[ix], sx = p.rope_sin[ix];
-      const float p0 = __shfl_xor(v0, 16), p1 = __shfl_xor(v1, 16);
-      v0 = (l32 < 16) ? (v0 * cy - p0 * sy) : (v0 * cy + p0 * sy);
-      v1 = (l32 < 16) ? (v1 * cx - p1 * sx) : (v1 * cx + p1 * sx);
+      if constexpr (NB == 2) {
+        const float p0 = __shfl_xor(v0, 16), p1 = __shfl_xor(v1, 16);
+        v0 = (l32 < 16) ? (v0 * cy - p0 * sy) : (v0 * cy + p0 * sy);
+        v1 = (l32 < 16) ? (v1 * cx - p1 * sx) : (v1 * cx + p1 * sx);
+      } else {
+        const float c = xhalf ? cx : cy, sn = xhalf ? sx : sy;
+        const float p0 = __shfl_xor(v0, 16);
+        v0 = (l32 < 16) ? (v0 * c - p0 * sn) : (v0 * c + p0 * sn);
+      }
     }
     if (flags & EPI_GELU) {
       v0 = gelu_tanh(v0);
@@ -1128,7 +1141,7 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
       v0 = fmaxf(v0, 0.f);
       v1 = fmaxf(v1, 0.f);
     }
-    float* srow = stage + (8 * (r >> 2) + 4 * hl + (r & 3)) * W2_SS + l32;
+    float* srow = stage + (8 * (r >> 2) + 4 * hl + (r & 3)) * SS + l32;
     srow[0] = v0;
     if constexpr (NB == 2) srow[32] = v1;
   }
@@ -1175,7 +1188,7 @@ __device__ __forceinline__ void w2_epi_row(const GemmArgs& p, const floatx16& q0
   for (int u = 0; u < UPH; ++u) {
     const int sr = 16 * hq + RPP * u + rin;
     const int row = row0 + sr;
-    fx4 v = *(const fx4*)(stage + sr * W2_SS + c4);
+    fx4 v = *(const fx4*)(stage + sr * SS + c4);
     if (flags & EPI_RES1) v = v + x1[u];
     if (flags & EPI_RES2) v = x2[u] + v;
     if (row < M && col < N) {
@@ -1439,8 +1452,7 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
 // kW32MinTiles of its tiles: 1 x 4 waves at 32 x 32 (one MFMA block each);
 // the 32 A rows of a K step are two waves' loads, and waves 2 and 3 issue
 // the same two loads again (identical bytes to the same LDS words), so every
-// wave issues three loads per K step, as at BM = 64. Its epilogue has no RoPE
-// form (such launches stay on the other kernels).
+// wave issues three loads per K step, as at BM = 64.
 
 
 template <int BM, bool CONV>
@@ -1451,8 +1463,10 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   constexpr int NA = W1X4 ? 1 : BM / 64;     // A-row loads per wave per K step
   constexpr int FSTAGE = (BM + W2N) * FK;    // floats per LDS stage
   // the epilogue's four 32-row wave stages overlay the LDS stages (BM = 64
-  // and 32 allocate past the two K stages for them)
-  constexpr int LDSF = 2 * FSTAGE > 4 * 32 * W2_SS ? 2 * FSTAGE : 4 * 32 * W2_SS;
+  // allocates past the two K stages for them; BM = 32, one 32-column block
+  // per wave, fits in them: 20 KB, so up to eight workgroups per CU)
+  constexpr int ESTAGE = 4 * 32 * (W1X4 ? W2_SS1 : W2_SS);  // the four wave stages
+  constexpr int LDSF = 2 * FSTAGE > ESTAGE ? 2 * FSTAGE : ESTAGE;
   static_assert(BM == 256 || BM == 192 || BM == 64 || (BM == 32 && !CONV), "tile rows");
   const GemmArgs& p = batch.g[blockIdx.z];
   const int M = p.M, N = p.N, K = p.K;
@@ -1581,9 +1595,12 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   }
 #undef GS_F2_ISSUE
   const int mw = m0 + wm * 32 * WTM, nw = n0 + wn * (W1X4 ? 32 : 64);
-  float* stage = lds + wave * 32 * W2_SS;
-  if constexpr (W1X4) {  // no RoPE launches (checked on the host)
-    w2_epi_row<false, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
+  float* stage = lds + wave * 32 * (W1X4 ? W2_SS1 : W2_SS);
+  if constexpr (W1X4) {
+    if (p.flags & EPI_ROPE)
+      w2_epi_row<true, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
+    else
+      w2_epi_row<false, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
   } else if (p.flags & EPI_ROPE) {
     w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
     if constexpr (WTM >= 2) w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
@@ -2001,19 +2018,26 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
           (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
   }
   w64 = w64 && tot64 >= kW64MinTiles && !(conv64 && tot192c >= kF2MinTiles);
-  // smaller plain-row launches whose 32 x 128 tiles still fill the CUs: the
-  // 32-row form, unsplit
+  // the 32-row form, unsplit: smaller plain-row launches whose 32 x 128 tiles
+  // still fill the CUs, and launches of the 64-row form whose busiest CU
+  // would carry more work than the 32-row form's (a 64-row tile is two
+  // 32-row tiles of work; at most six 32-row tiles per CU, one round at up
+  // to eight workgroups per CU)
   int t32 = 0, tot32 = 0;
-  bool w32 = !w64 && dl_small && aload == A_PLAIN && b.kernel == 0 && b.ksplit == 0;
+  bool w32 = dl_small && aload == A_PLAIN && b.kernel == 0 && b.ksplit == 0;
   for (int i = 0; w32 && i < b.ngroups; ++i) {
     const GemmArgs& g = b.g[i];
     const int t = ((g.M + 31) / 32) * ((g.N + W2N - 1) / W2N);
     t32 = std::max(t32, t);
     tot32 += t;
     w32 = g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
-          aligned16(g.B) && row_epi_ok(g) && !(g.flags & EPI_ROPE);
+          aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
   }
-  w32 = w32 && tot32 >= kW32MinTiles;
+  {
+    const int per_cu32 = (tot32 + 255) / 256, per_cu64 = (tot64 + 255) / 256;
+    w32 = w32 && (w64 ? tot32 <= 6 * 256 && per_cu32 < 2 * per_cu64 : tot32 >= kW32MinTiles);
+  }
+  if (w32) w64 = false;
   if (w64 || w32) {
     b.ksplit = 1;
   } else if (b.ksplit > 1) {  // requested split

@@ -149,8 +149,11 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
 # kernels (16-deep steps; gs_hip_linear pads K to a multiple of 32, so K =
 # 16 / 48 / 272 run as 2 / 4 / 18 steps; odd step counts of these kernels are
 # reached through the conv op in test_conv2d_nonsquare_kernel; the 64-row form
-# takes small launches with at least 432 of its tiles and the 32-row form
-# smaller ones with at least 768 of its tiles, here with ragged M and N too),
+# takes small launches with at least 432 of its tiles (N = 4096 here) and the
+# 32-row form smaller ones with at least 768 of its tiles, and those of the
+# 64-row form it spreads more evenly over the CUs (N = 3072 at M = 1536 /
+# 1400: 1152 / 1056 tiles of 32 rows, at most 5 per CU, against 576 / 528 of
+# 64 rows, 3 per CU); ragged M and N too),
 # the 192-row form also at ragged M and N (24500 x 760: 128 x 6 tiles, the
 # last row and column tiles partial), the bf16 two- and three-stage kernels
 # (32-deep steps: one, two, three and many; K >= 6144 takes three stages) and the 128 x 128 kernel of small
@@ -163,6 +166,7 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
     (8192, 6176, 3072, True), (8192, 6208, 3072, True),
     (768, 32, 1024, False), (768, 64, 1024, False), (768, 96, 1024, False), (768, 4128, 1024, False),
     (1536, 16, 3072, False), (1536, 48, 3072, False), (1400, 272, 3072, False),
+    (1536, 16, 4096, False), (1536, 48, 4096, False), (1400, 272, 4096, False),
     (8192, 256, 4096, False), (8142, 320, 4000, False), (8192, 1088, 2048, False),
     (768, 16, 4096, False), (768, 48, 4096, False), (768, 1024, 4096, False),
     (750, 272, 4000, False), (24500, 48, 760, False), (24500, 1024, 760, False)])
