@@ -1039,7 +1039,13 @@ constexpr int kW64MinTiles = 432;
 // this threshold). It also takes launches of the 64-row form whose busiest
 // CU it loads less (one pair: the encoder qkv, 576 tiles of 64 rows, 3 per
 // CU, against 1152 of 32 rows, 5 per CU: 91.5 -> 97.7 TFLOP/s; the decoder
-// fc1 88.4 -> 96.4).
+// fc1 88.4 -> 96.4), and smaller launches whose busiest CU it loads no more
+// than the split 128 x 128 kernel does and which write no LayerNorm (the
+// short-K launches at one pair: K = 96, M = 768 and N = 1536, 11.5 -> 31
+// TFLOP/s; the encoder proj, M = 1536, N = 1024, K = 1024, ran 62.2 -> 69.9
+// but then needed its LayerNorm pass back, 0.18 ms per pair; at K = 4096 the
+// split kernel's three 512-deep ranges per CU beat two full 32-row tiles,
+// 103 against 81 TFLOP/s).
 constexpr int kW32MinTiles = 768;
 // Long-K launches of the fp32 256 x 128 kernel run as one launch per round of
 // workgroup slots (96 tiles per XCD: 32 CUs x 3 workgroups), so every round
@@ -2033,9 +2039,24 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
     w32 = g.K % 16 == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
           aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
   }
-  {
-    const int per_cu32 = (tot32 + 255) / 256, per_cu64 = (tot64 + 255) / 256;
-    w32 = w32 && (w64 ? tot32 <= 6 * 256 && per_cu32 < 2 * per_cu64 : tot32 >= kW32MinTiles);
+  if (w32) {
+    const int per_cu32 = (tot32 + kNumCUs - 1) / kNumCUs, per_cu64 = (tot64 + kNumCUs - 1) / kNumCUs;
+    if (w64) {
+      w32 = tot32 <= 6 * kNumCUs && per_cu32 < 2 * per_cu64;
+    } else if (tot32 < kW32MinTiles && (b.g[0].flags & EPI_LNOUT)) {
+      // a split launch writes the next LayerNorm in its reduce pass; unsplit,
+      // it would take a LayerNorm pass of its own
+      w32 = false;
+    } else if (tot32 < kW32MinTiles) {
+      // against the split 128 x 128 kernel: the busiest CU's multiply-adds
+      // at the split its planner picks, ties to the 32-row form (no reduce
+      // pass)
+      const int S = plan_ksplit_dl(b, max_tiles), steps = b.g[0].K / BK;
+      const double work_dl = (double)((max_tiles * b.ngroups * S + kNumCUs - 1) / kNumCUs) *
+                             BM * BN * (double)((steps + S - 1) / S) * BK;
+      const double work32 = (double)per_cu32 * 32 * W2N * b.g[0].K;
+      w32 = work32 <= work_dl;
+    }
   }
   if (w32) w64 = false;
   if (w64 || w32) {

@@ -145,19 +145,23 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
 # The direct-to-LDS kernels wait for their own loads with hand-counted
 # s_waitcnt vmcnt immediates, which differ between the first, the steady-state
 # and the last K steps. Each kernel here runs K of few and many steps, against
-# an fp64 product of the same operands: the fp32 256-, 192-, 64- and 32-row
-# kernels (16-deep steps; gs_hip_linear pads K to a multiple of 32, so K =
-# 16 / 48 / 272 run as 2 / 4 / 18 steps; odd step counts of these kernels are
-# reached through the conv op in test_conv2d_nonsquare_kernel; the 64-row form
-# takes small launches with at least 432 of its tiles (N = 4096 here) and the
-# 32-row form smaller ones with at least 768 of its tiles, and those of the
-# 64-row form it spreads more evenly over the CUs (N = 3072 at M = 1536 /
-# 1400: 1152 / 1056 tiles of 32 rows, at most 5 per CU, against 576 / 528 of
-# 64 rows, 3 per CU); ragged M and N too),
-# the 192-row form also at ragged M and N (24500 x 760: 128 x 6 tiles, the
-# last row and column tiles partial), the bf16 two- and three-stage kernels
-# (32-deep steps: one, two, three and many; K >= 6144 takes three stages) and the 128 x 128 kernel of small
-# launches (32-deep steps, split-K at long K).
+# an fp64 product of the same operands:
+# - the fp32 256-, 192-, 64- and 32-row kernels (16-deep steps; gs_hip_linear
+#   pads K to a multiple of 32, so K = 16 / 48 / 272 run as 2 / 4 / 18 steps;
+#   odd step counts of these kernels are reached through the conv op in
+#   test_conv2d_nonsquare_kernel). The 192-row form also at ragged M and N
+#   (24500 x 760: 128 x 6 tiles, the last row and column tiles partial). The
+#   64-row form takes small launches with at least 432 of its tiles (N = 4096
+#   here); the 32-row form smaller ones with at least 768 of its tiles, those
+#   of the 64-row form it spreads more evenly over the CUs (N = 3072 at M =
+#   1536 / 1400: 1152 / 1056 tiles of 32 rows, at most 5 per CU, against 576 /
+#   528 of 64 rows, 3 per CU) and those whose busiest CU it loads no more than
+#   the split 128 x 128 kernel (M = 768, N = 1024, K <= 96); ragged M and N too;
+# - the bf16 two- and three-stage kernels (32-deep steps: one, two, three and
+#   many; K >= 6144 takes three stages);
+# - the 128 x 128 kernel of split small launches (M = 768, N = 1024: K = 672,
+#   704 and 736 split in five ranges whose last holds one, two and three
+#   32-deep steps; K = 4128 in five of 26).
 @pytest.mark.parametrize("M,K,N,bf16", [
     (8192, 16, 3072, False), (8192, 32, 3072, False), (8192, 48, 3072, False),
     (8192, 272, 3072, False),
@@ -165,6 +169,7 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
     (8192, 32, 3072, True), (8192, 64, 3072, True), (8192, 96, 3072, True), (8192, 288, 3072, True),
     (8192, 6176, 3072, True), (8192, 6208, 3072, True),
     (768, 32, 1024, False), (768, 64, 1024, False), (768, 96, 1024, False), (768, 4128, 1024, False),
+    (768, 672, 1024, False), (768, 704, 1024, False), (768, 736, 1024, False),
     (1536, 16, 3072, False), (1536, 48, 3072, False), (1400, 272, 3072, False),
     (1536, 16, 4096, False), (1536, 48, 4096, False), (1400, 272, 4096, False),
     (8192, 256, 4096, False), (8142, 320, 4000, False), (8192, 1088, 2048, False),
