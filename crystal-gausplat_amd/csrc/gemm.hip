@@ -2025,10 +2025,11 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   }
   w64 = w64 && tot64 >= kW64MinTiles && !(conv64 && tot192c >= kF2MinTiles);
   // the 32-row form, unsplit: smaller plain-row launches whose 32 x 128 tiles
-  // still fill the CUs, and launches of the 64-row form whose busiest CU
-  // would carry more work than the 32-row form's (a 64-row tile is two
-  // 32-row tiles of work; at most six 32-row tiles per CU, one round at up
-  // to eight workgroups per CU)
+  // still fill the CUs; launches of the 64-row form whose busiest CU would
+  // carry more work than the 32-row form's (a 64-row tile is two 32-row
+  // tiles of work; at most six 32-row tiles per CU, one round at up to eight
+  // workgroups per CU); and, below both, launches whose busiest CU carries
+  // no more work than under the split 128 x 128 kernel
   int t32 = 0, tot32 = 0;
   bool w32 = dl_small && aload == A_PLAIN && b.kernel == 0 && b.ksplit == 0;
   for (int i = 0; w32 && i < b.ngroups; ++i) {
