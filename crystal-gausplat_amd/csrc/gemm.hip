@@ -1045,7 +1045,10 @@ constexpr int kW64MinTiles = 432;
 // TFLOP/s; the encoder proj, M = 1536, N = 1024, K = 1024, ran 62.2 -> 69.9
 // but then needed its LayerNorm pass back, 0.18 ms per pair; at K = 4096 the
 // split kernel's three 512-deep ranges per CU beat two full 32-row tiles,
-// 103 against 81 TFLOP/s).
+// 103 against 81 TFLOP/s). Launches of 512-767 tiles that write no
+// LayerNorm run it split in K (one image's qkv, 576 tiles in three ranges:
+// 62 -> 58 us against the split 128 x 128 kernel; the LayerNorm-writing proj
+// and fc2 ran 1-40 % slower split this way).
 constexpr int kW32MinTiles = 768;
 // Long-K launches of the fp32 256 x 128 kernel run as one launch per round of
 // workgroup slots (96 tiles per XCD: 32 CUs x 3 workgroups), so every round
@@ -1458,7 +1461,8 @@ __global__ __launch_bounds__(256, NST == 3 ? 2 : 3) void gemm_bf16_w2_kernel(Gem
 // kW32MinTiles of its tiles: 1 x 4 waves at 32 x 32 (one MFMA block each);
 // the 32 A rows of a K step are two waves' loads, and waves 2 and 3 issue
 // the same two loads again (identical bytes to the same LDS words), so every
-// wave issues three loads per K step, as at BM = 64.
+// wave issues three loads per K step, as at BM = 64. Split launches give each
+// blockIdx.y one K range and store its raw partial for gemm_splitk_reduce.
 
 
 template <int BM, bool CONV>
@@ -1547,11 +1551,16 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   const int swz = (l32 >> 2) & 3;
   const int ra0 = (wm * 32 * WTM + l32) * FK, rb0 = (wn * (W1X4 ? 32 : 64) + l32) * FK;
   floatx16 c00 = {}, c01 = {}, c10 = {}, c11 = {}, c20 = {}, c21 = {}, c30 = {}, c31 = {};
+  // K range: all of K, or (32-row form, split launch) range blockIdx.y of
+  // batch.ksplit in 32-deep steps (every range non-empty, checked on the host)
+  int kbeg = 0, kend = K;
+  if constexpr (W1X4)
+    if (batch.ksplit > 1) split_range(K, batch.ksplit, BK, kbeg, kend);
   int buf = 0;
-  GS_F2_ISSUE(0, 0)
-  for (int k0 = 0; k0 < K; k0 += FK) {
+  GS_F2_ISSUE(0, kbeg)
+  for (int k0 = kbeg; k0 < kend; k0 += FK) {
     // each wave waits for its own NA + 2 loads of step k0
-    if (k0 + FK < K) {
+    if (k0 + FK < kend) {
       GS_F2_ISSUE(buf ^ 1, k0 + FK)
       if constexpr (BM == 256)
         asm volatile("s_waitcnt vmcnt(6)\n\ts_barrier" ::: "memory");
@@ -1603,10 +1612,22 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_w2_kernel(GemmBatch batch) {
   const int mw = m0 + wm * 32 * WTM, nw = n0 + wn * (W1X4 ? 32 : 64);
   float* stage = lds + wave * 32 * (W1X4 ? W2_SS1 : W2_SS);
   if constexpr (W1X4) {
-    if (p.flags & EPI_ROPE)
+    if (batch.ksplit > 1) {
+      // raw partial of this K range: part[blockIdx.y][row][col] (half-waves
+      // store 128 contiguous bytes of one row); gemm_splitk_reduce sums the
+      // ranges and applies the epilogue
+      float* part = p.part + (int64_t)blockIdx.y * M * N;
+      const int col = nw + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = mw + 8 * (r >> 2) + 4 * hl + (r & 3);
+        if (row < M && col < N) part[(int64_t)row * N + col] = c00[r];
+      }
+    } else if (p.flags & EPI_ROPE) {
       w2_epi_row<true, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
-    else
+    } else {
       w2_epi_row<false, 1>(p, c00, c00, mw, nw, stage, lane, l32, hl);
+    }
   } else if (p.flags & EPI_ROPE) {
     w2_epi_row<true>(p, c00, c01, mw, nw, stage, lane, l32, hl);
     if constexpr (WTM >= 2) w2_epi_row<true>(p, c10, c11, mw + 32, nw, stage, lane, l32, hl);
@@ -2059,9 +2080,30 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
       w32 = work32 <= work_dl;
     }
   }
+  // 512-767 tiles of 32 rows that write no LayerNorm (one image's qkv: 576,
+  // 2.25 per CU): the 32-row form split in K, as many 32-deep ranges as keep
+  // one round at up to eight workgroups per CU
+  int s32 = 1;
+  if (!w32 && !w64 && tot32 >= 512 && tot32 < kW32MinTiles && !(b.g[0].flags & EPI_LNOUT) &&
+      dl_small && aload == A_PLAIN && b.kernel == 0 && b.ksplit == 0 && splitk_eligible(b)) {
+    bool ok = true;
+    for (int i = 0; ok && i < b.ngroups; ++i) {
+      const GemmArgs& g = b.g[i];
+      ok = g.K % BK == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
+           aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+    }
+    const int steps = b.g[0].K / BK;
+    for (int S = 4; ok && S >= 2; --S)
+      if (tot32 * S <= 8 * kNumCUs && steps / S >= 4 &&
+          (int64_t)S * b.g[0].M * b.g[0].N * b.ngroups <= b.part_ws_elems) {
+        w32 = true;
+        s32 = S;
+        break;
+      }
+  }
   if (w32) w64 = false;
   if (w64 || w32) {
-    b.ksplit = 1;
+    b.ksplit = w32 ? s32 : 1;
   } else if (b.ksplit > 1) {  // requested split
     GS_REQUIRE(splitk_eligible(b), "gemm: this launch cannot split K");
     GS_REQUIRE(b.g[0].K / BK >= b.ksplit &&
@@ -2201,8 +2243,13 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
   int kern = b.kernel;
   if (w32) {
     hipEvent_t ev = prof_start(s);
-    hipLaunchKernelGGL((gemm_f32_w2_kernel<32, false>), dim3(t32, 1, b.ngroups), dim3(256), 0, s, b);
+    hipLaunchKernelGGL((gemm_f32_w2_kernel<32, false>), dim3(t32, b.ksplit, b.ngroups), dim3(256), 0,
+                       s, b);
     GS_CHECK_HIP(hipGetLastError());
+    if (b.ksplit > 1) {
+      launch_reduce(b, rgrid, s);
+      GS_CHECK_HIP(hipGetLastError());
+    }
     if (ev) prof_stop(s, ev, gemm_prof_name("gemm_f32_w2_kernel<32>", b).c_str(), flops, bytes);
     return post_layernorm(b, s);
   }

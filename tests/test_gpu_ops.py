@@ -156,7 +156,9 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
 #   of the 64-row form it spreads more evenly over the CUs (N = 3072 at M =
 #   1536 / 1400: 1152 / 1056 tiles of 32 rows, at most 5 per CU, against 576 /
 #   528 of 64 rows, 3 per CU) and those whose busiest CU it loads no more than
-#   the split 128 x 128 kernel (M = 768, N = 1024, K <= 96); ragged M and N too;
+#   the split 128 x 128 kernel (M = 768, N = 1024, K <= 96); ragged M and N
+#   too; split in K at 512-767 tiles (M = 768, N = 3072 and the ragged 750 x
+#   3000: 576 tiles in three ranges of 4, 7 and 10-11 32-deep steps);
 # - the bf16 two- and three-stage kernels (32-deep steps: one, two, three and
 #   many; K >= 6144 takes three stages);
 # - the 128 x 128 kernel of split small launches (M = 768, N = 1024: K = 672,
@@ -174,7 +176,8 @@ def test_linear_f32_long_k_large_launches(M, K, N, epi):
     (1536, 16, 4096, False), (1536, 48, 4096, False), (1400, 272, 4096, False),
     (8192, 256, 4096, False), (8142, 320, 4000, False), (8192, 1088, 2048, False),
     (768, 16, 4096, False), (768, 48, 4096, False), (768, 1024, 4096, False),
-    (750, 272, 4000, False), (24500, 48, 760, False), (24500, 1024, 760, False)])
+    (750, 272, 4000, False), (24500, 48, 760, False), (24500, 1024, 760, False),
+    (768, 384, 3072, False), (750, 672, 3000, False), (768, 1024, 3072, False)])
 def test_linear_direct_to_lds_k_classes(M, K, N, bf16):
     case(f"linear K classes M={M} K={K} N={N} bf16={bf16}")
     x, W, b = rnd(M, K), rnd(N, K, scale=0.05), rnd(N, scale=0.1)
