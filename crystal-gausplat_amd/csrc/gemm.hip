@@ -2101,6 +2101,40 @@ int launch_gemm(const GemmBatch& b_in, int aload, int blayout, bool a_relu,
         break;
       }
   }
+  // launches that write the next LayerNorm (split either way, the reduce
+  // writes it): the 32-row form split in K when its busiest CU carries at
+  // most 0.8 of the split 128 x 128 kernel's multiply-adds (one pair's
+  // encoder proj: three 512-deep 32-row ranges per CU against one 512-deep
+  // 128 x 128 range, 1.249 -> 1.103 ms per pair; the one-image proj and fc2,
+  // at 0.86 and 0.92 of the work, ran 1-5 % slower split this way)
+  if (!w32 && !w64 && tot32 > 0 && (b.g[0].flags & EPI_LNOUT) && dl_small && aload == A_PLAIN &&
+      b.kernel == 0 && b.ksplit == 0 && splitk_eligible(b)) {
+    bool ok = true;
+    for (int i = 0; ok && i < b.ngroups; ++i) {
+      const GemmArgs& g = b.g[i];
+      ok = g.K % BK == 0 && g.lda % 4 == 0 && aligned16(g.A) && g.ldb % 4 == 0 &&
+           aligned16(g.B) && row_epi_ok(g) && (!(g.flags & EPI_ROPE) || g.rope_ncols % 64 == 0);
+    }
+    const int S = plan_ksplit_dl(b, max_tiles), steps = b.g[0].K / BK;
+    const double work_dl = (double)((max_tiles * b.ngroups * S + kNumCUs - 1) / kNumCUs) *
+                           BM * BN * (double)((steps + S - 1) / S) * BK;
+    double best = 0.0;
+    for (int S2 = 2; ok && S2 <= 8; ++S2) {
+      if (tot32 * S2 > 8 * kNumCUs || steps / S2 < 4 ||
+          (int64_t)S2 * b.g[0].M * b.g[0].N * b.ngroups > b.part_ws_elems)
+        break;
+      const double w = (double)((tot32 * S2 + kNumCUs - 1) / kNumCUs) * 32 * W2N *
+                       (double)((steps + S2 - 1) / S2) * BK;
+      if (s32 == 1 || w < best) {
+        best = w;
+        s32 = S2;
+      }
+    }
+    if (s32 > 1 && best <= 0.8 * work_dl)
+      w32 = true;
+    else
+      s32 = 1;
+  }
   if (w32) w64 = false;
   if (w64 || w32) {
     b.ksplit = w32 ? s32 : 1;
